@@ -1,0 +1,236 @@
+/* relx.h - C ABI of librelx, the MI355X-native executor for Sym relocation
+ * plans (wire v0 layout plans and wire v1 typed plans).
+ *
+ * Every entry point is extern "C", takes plain pointers and sizes, and never
+ * throws. Failures return a nonzero status and fill `relx_err` with a stable
+ * code (the reference's codes where one exists) and a message. Calls block
+ * until their device work completes unless a function says otherwise.
+ *
+ * Each declaration names the reference interface it replaces (file:line under
+ * the reference tree JueonPark/sym).
+ */
+#ifndef RELX_H
+#define RELX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RELX_OK 0
+#define RELX_ERROR 1
+
+/* Completion of a failed call (reference QueueCompletion,
+ * libreloc/include/reloc/Backend.h:63-69; TransferError::completion). */
+#define RELX_NOT_LAUNCHED 0
+#define RELX_COMPLETE 1
+#define RELX_UNKNOWN 2
+
+typedef struct relx_err {
+  char code[48];     /* e.g. "decode_error", "bind_error", "invalid_view" */
+  char message[464]; /* human-readable detail (byte offset for decode errors) */
+  int64_t offset;    /* decode errors: byte offset; else -1 */
+  int completion;    /* RELX_NOT_LAUNCHED / RELX_COMPLETE / RELX_UNKNOWN */
+} relx_err;
+
+typedef struct relx_plan relx_plan;   /* decoded, immutable plan */
+typedef struct relx_bound relx_bound; /* bound plan + prepared device program */
+typedef struct relx_ctx relx_ctx;     /* per-device retained execution context */
+
+/* ---------------------------------------------------------------- plans */
+
+/* Library identification string. Replaces reloc::versionString
+ * (libreloc/src/Version.cpp:5-8). */
+const char *relx_version(void);
+
+/* Wire version in bytes 4..8 of an "RPLN" blob, or -1 when the header is not
+ * a plan. Replaces reloc::peekWireVersion (libreloc/src/Decode.cpp:868-874). */
+int relx_wire_version(const uint8_t *blob, size_t n);
+
+/* Decode a wire v0 (layout) or v1 (typed) plan; the header picks the decoder.
+ * Replaces reloc::decodePlan / reloc::decodeTypedPlan
+ * (libreloc/src/Decode.cpp:876-948) and pyreloc.load_plan/load_typed_plan
+ * (libreloc/python/PyReloc.cpp:596,921). Errors: code "decode_error" with the
+ * byte offset of the violated item. */
+int relx_plan_load(const uint8_t *blob, size_t n, relx_plan **out, relx_err *err);
+
+/* 1 for a typed (v1) plan, 0 for a layout (v0) plan. */
+int relx_plan_is_typed(const relx_plan *plan);
+
+/* Number of plan symbols and the i-th symbol name (owned by the plan). */
+int relx_plan_symbol_count(const relx_plan *plan);
+const char *relx_plan_symbol(const relx_plan *plan, int i);
+
+void relx_plan_free(relx_plan *plan);
+
+/* A runtime parameter value by declared name (reference ParameterValue,
+ * libreloc/include/reloc/Bind.h:125-133): element type (kind 0 float,
+ * 1 bfloat, 2 integer; bitwidth), rank 0 or 1 with its length, and the
+ * little-endian element bytes. Bytes are copied during the call. */
+typedef struct relx_param {
+  const char *name;
+  int kind;
+  int bits;
+  int rank;
+  int64_t length;
+  const void *data;
+  size_t nbytes;
+} relx_param;
+
+/* Bind symbols (and, for typed plans, parameters), then prepare the device
+ * program. Replaces reloc::bind / reloc::bindTyped
+ * (libreloc/src/Bind.cpp:176-384, 494-699) + typed::prepareProgram
+ * (libreloc/src/TypedExecute.cpp:292-403), pyreloc.bind / bind_typed
+ * (libreloc/python/PyReloc.cpp:674,987). Errors: "bind_error",
+ * "unsupported_stage", "invalid_parameter". */
+int relx_bind(const relx_plan *plan, const char *const *sym_names, const int64_t *sym_values,
+              int nsym, const relx_param *params, int nparam, relx_bound **out,
+              relx_err *err);
+
+void relx_bound_free(relx_bound *bound);
+
+/* Bound-plan facts (reference BoundPlan / TypedBoundPlan fields,
+ * libreloc/include/reloc/Bind.h:82-102,164-190). Stage boundaries are
+ * 0..stages; bytes_at[k] is the dense footprint at boundary k. */
+#define RELX_MAX_RANK 8
+#define RELX_MAX_STAGES 8
+typedef struct relx_bound_info {
+  int typed;
+  int rank; /* coalesced axes */
+  int64_t extents[RELX_MAX_RANK];
+  int64_t src_strides[RELX_MAX_RANK];
+  int64_t dst_strides[RELX_MAX_RANK];
+  int64_t pad_lo[RELX_MAX_RANK];
+  int64_t pad_hi[RELX_MAX_RANK];
+  int element_size; /* result element bytes */
+  int64_t total_bytes; /* destination footprint */
+  int64_t source_bytes;
+  int64_t destination_bytes;
+  int64_t parameter_bytes;
+  int stages;
+  int64_t bytes_at[RELX_MAX_STAGES + 1];
+  int source_width;
+  int result_width;
+  int source_rank;
+  int64_t source_extents[RELX_MAX_RANK];
+  int result_rank;
+  int64_t result_extents[RELX_MAX_RANK];
+  char kernel[32]; /* device kernel family the program runs */
+} relx_bound_info;
+
+int relx_bound_query(const relx_bound *bound, relx_bound_info *out);
+
+/* ------------------------------------------------------------- contexts */
+
+/* A retained per-device context: a copy stream and a compute stream, a
+ * pinned host staging ring, device wire scratch and events. Replaces
+ * CudaBackend (libreloc/cuda/CudaBackend.cu:55-282) and the retained
+ * ScratchBackend of dispatch::Resources
+ * (libreloc/src/DispatchResources.cpp:44,552-686). `max_retained_bytes`
+ * bounds pinned + device scratch kept between calls (0 = unbounded). */
+int relx_ctx_create(int device, int64_t max_retained_bytes, relx_ctx **out, relx_err *err);
+
+/* Drain and free. A context whose completion is unknown is quarantined (its
+ * memory is kept for the process lifetime), as the reference does
+ * (libreloc/src/Transfer.cpp:336-343). */
+int relx_ctx_close(relx_ctx *ctx, relx_err *err);
+
+/* Retained-resource gauges. */
+typedef struct relx_ctx_stats {
+  int64_t pinned_bytes;
+  int64_t device_bytes;
+  int64_t calls;
+  int64_t failures;
+  int quarantined;
+} relx_ctx_stats;
+int relx_ctx_stats_get(const relx_ctx *ctx, relx_ctx_stats *out);
+
+/* ------------------------------------------------------------ execution */
+
+/* Per-call options (reference TransferOptions,
+ * libreloc/include/reloc/Transfer.h:121-155). Zeroed = defaults. */
+typedef struct relx_options {
+  int n_buffers;        /* pinned ring slots (default 3) */
+  int64_t chunk_bytes;  /* wire bytes per chunk (0 = schedule picks) */
+  int host_stages;      /* leading per-tensor cast stages the host applies
+                           while staging (-1 = auto, 0 = none) */
+  int gather_threads;   /* host staging threads (0 = default 8) */
+  int source_pinned;    /* 1: source is page-locked; DMA it directly.
+                           -1: probe; 0: pageable (stage through the ring) */
+  uint64_t caller_stream; /* hipStream_t the call is ordered after (0 = none) */
+  int no_wait;          /* 1: return after enqueue; the caller's stream (or
+                           relx_ctx_synchronize) orders later work */
+} relx_options;
+
+/* Scalar report of one call (reference dispatch::Report,
+ * libreloc/include/reloc/Dispatch.h:104-124). */
+typedef struct relx_report {
+  char implementation[40]; /* e.g. "hip_relayout", "hip_relayout@1" */
+  int64_t source_bytes;
+  int64_t wire_bytes;
+  int64_t destination_bytes;
+  int64_t parameter_bytes;
+  int64_t payload_bytes_transferred;
+  int64_t chunks;
+  int64_t kernel_launches;
+  int wire_boundary;
+  int direct_dma; /* 1 when the source was DMA'd without staging */
+} relx_report;
+
+/* Run one bound plan: host source (dense, source layout, source dtype) ->
+ * device destination (dense result layout). The source bytes move through
+ * the chunked pinned H2D pipeline on the copy stream; relayout and value
+ * stages run as HIP kernels on the compute stream, overlapped per chunk.
+ * Replaces dispatch::executeDispatch (libreloc/src/Dispatch.cpp:1983-2046)
+ * for the H2D direction, executeTransfer (libreloc/src/Transfer.cpp:493-544)
+ * for layout plans, and pyreloc.execute_dispatch / execute_transfer
+ * (libreloc/python/PyDispatch.cpp:159-235, PyTransfer.cpp:180-219).
+ * Errors: "insufficient_capacity", "invalid_options", "backend_failure",
+ * "channel_out_of_range", "invalid_view". */
+int relx_execute_h2d(relx_ctx *ctx, const relx_bound *bound, const void *src, size_t src_bytes,
+                     void *dst, size_t dst_bytes, const relx_options *opt, relx_report *report,
+                     relx_err *err);
+
+/* A group of bound plans as one schedule: all members' wire bytes through
+ * one ring and one event barrier (reference group_detail::executeGroup,
+ * libreloc/src/Dispatch.cpp:1833-1981; pyreloc.execute_dispatch_group).
+ * `reports` has n entries; `total` (optional) sums them. */
+int relx_execute_group_h2d(relx_ctx *ctx, int n, const relx_bound *const *bounds,
+                           const void *const *srcs, const size_t *src_bytes, void *const *dsts,
+                           const size_t *dst_bytes, const relx_options *opt,
+                           relx_report *reports, relx_report *total, relx_err *err);
+
+/* Device-resident relayout: `wire` is already in device memory (dense source
+ * layout at boundary `wire_boundary`); run the relayout + stages
+ * [wire_boundary, stages) into `dst` on `stream` (0 = the context's compute
+ * stream). Asynchronous: returns after the launch. This is the device half of
+ * relx_execute_h2d and the unit the kernel roofline is measured on; it
+ * replaces the reference's kernel launch wrappers reloc::cuda::*
+ * (libreloc/include/reloc/CudaKernels.h:28-122). */
+int relx_relayout_device(relx_ctx *ctx, const relx_bound *bound, int wire_boundary,
+                         const void *wire, void *dst, uint64_t stream, relx_err *err);
+
+/* Apply a bound plan's leading `host_stages` stages to a dense source on the
+ * host (the staging-side transform of relx_execute_h2d), writing the wire
+ * at that boundary. Used by callers that pre-stage. */
+int relx_host_stage(const relx_bound *bound, int host_stages, const void *src, void *wire,
+                    int threads, relx_err *err);
+
+/* Block until every call on the context has completed. */
+int relx_ctx_synchronize(relx_ctx *ctx, relx_err *err);
+
+/* Pinned host memory helpers (hipHostMalloc / hipHostFree). */
+int relx_host_alloc(size_t bytes, void **out, relx_err *err);
+int relx_host_free(void *p);
+
+/* Measured pinned H2D ceiling (GB/s): `bytes` per copy, `iters` copies after
+ * a warmup, best of `rounds` (restates bench/rtrack/multigpu_h2d.cu:46-91). */
+double relx_measure_h2d(int device, size_t bytes, int iters, int rounds);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RELX_H */

@@ -1,0 +1,116 @@
+"""ctypes driver for oracle/_ref/libreloc_ref.so: the reference's own CPU
+libreloc built from its sources (TEST INFRASTRUCTURE ONLY; see Makefile).
+
+Used by tests to cross-check the numpy oracle and by bench.py as the
+"reference" CPU baseline. Never imported by the product package.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_ref", "libreloc_ref.so")
+_lib = None
+
+KINDS = {"float32": (0, 32), "float16": (0, 16), "bfloat16": (1, 16), "int8": (2, 8),
+         "int32": (2, 32), "int64": (2, 64)}
+
+
+def available():
+    return os.path.exists(LIB_PATH)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        L = ctypes.CDLL(LIB_PATH)
+        vp, cp, sz = ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t
+        L.ref_typed_prepare.restype = vp
+        L.ref_typed_prepare.argtypes = [cp, sz, ctypes.POINTER(cp), ctypes.POINTER(ctypes.c_int64),
+                                        ctypes.c_int, ctypes.POINTER(cp), ctypes.POINTER(ctypes.c_int),
+                                        ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int64),
+                                        ctypes.POINTER(vp), ctypes.POINTER(sz), ctypes.c_int,
+                                        ctypes.c_uint, cp, sz]
+        L.ref_typed_result_bytes.restype = ctypes.c_int64
+        L.ref_typed_result_bytes.argtypes = [vp]
+        L.ref_typed_execute.restype = ctypes.c_int
+        L.ref_typed_execute.argtypes = [vp, vp, vp, cp, sz]
+        L.ref_typed_free.argtypes = [vp]
+        L.ref_layout_prepare.restype = vp
+        L.ref_layout_prepare.argtypes = [cp, sz, ctypes.POINTER(cp), ctypes.POINTER(ctypes.c_int64),
+                                         ctypes.c_int, ctypes.c_uint, cp, sz]
+        L.ref_layout_total_bytes.restype = ctypes.c_int64
+        L.ref_layout_total_bytes.argtypes = [vp]
+        L.ref_layout_execute.restype = ctypes.c_int
+        L.ref_layout_execute.argtypes = [vp, vp, vp]
+        L.ref_layout_free.argtypes = [vp]
+        _lib = L
+    return _lib
+
+
+def _syms(symbols):
+    names = list(symbols)
+    arr_n = (ctypes.c_char_p * max(1, len(names)))(*[n.encode() for n in names])
+    arr_v = (ctypes.c_int64 * max(1, len(names)))(*[int(symbols[n]) for n in names])
+    return arr_n, arr_v, len(names)
+
+
+class TypedRef:
+    """prepare once, execute many (executeHost over every stage)."""
+
+    def __init__(self, blob, symbols, params, threads=1):
+        """params: {name: (dtype name, shape list, bytes)}."""
+        L = lib()
+        sn, sv, ns = _syms(symbols)
+        names = list(params)
+        np_ = max(1, len(names))
+        pn = (ctypes.c_char_p * np_)(*[n.encode() for n in names])
+        pk = (ctypes.c_int * np_)(*[KINDS[params[n][0]][0] for n in names])
+        pb = (ctypes.c_int * np_)(*[KINDS[params[n][0]][1] for n in names])
+        pl = (ctypes.c_int64 * np_)(*[(params[n][1][0] if params[n][1] else -1) for n in names])
+        self._keep = [ctypes.create_string_buffer(params[n][2], len(params[n][2])) for n in names]
+        pd = (ctypes.c_void_p * np_)(*[ctypes.addressof(b) for b in self._keep])
+        psz = (ctypes.c_size_t * np_)(*[len(params[n][2]) for n in names])
+        err = ctypes.create_string_buffer(512)
+        self.h = L.ref_typed_prepare(blob, len(blob), sn, sv, ns, pn, pk, pb, pl, pd, psz,
+                                     len(names), threads, err, 512)
+        if not self.h:
+            raise RuntimeError(err.value.decode())
+        self.result_bytes = L.ref_typed_result_bytes(self.h)
+
+    def execute(self, src, out=None):
+        src = np.ascontiguousarray(src)
+        if out is None:
+            out = np.empty(self.result_bytes, np.uint8)
+        err = ctypes.create_string_buffer(512)
+        if lib().ref_typed_execute(self.h, src.ctypes.data, out.ctypes.data, err, 512):
+            raise RuntimeError(err.value.decode())
+        return out
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().ref_typed_free(self.h)
+            self.h = None
+
+
+class LayoutRef:
+    def __init__(self, blob, symbols, threads=1):
+        sn, sv, ns = _syms(symbols)
+        err = ctypes.create_string_buffer(512)
+        self.h = lib().ref_layout_prepare(blob, len(blob), sn, sv, ns, threads, err, 512)
+        if not self.h:
+            raise RuntimeError(err.value.decode())
+        self.total_bytes = lib().ref_layout_total_bytes(self.h)
+
+    def execute(self, src, out=None):
+        src = np.ascontiguousarray(src)
+        if out is None:
+            out = np.empty(self.total_bytes, np.uint8)
+        lib().ref_layout_execute(self.h, src.ctypes.data, out.ctypes.data)
+        return out
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().ref_layout_free(self.h)
+            self.h = None

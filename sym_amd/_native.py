@@ -1,0 +1,138 @@
+"""ctypes binding of librelx.so (include/relx.h).
+
+The library is built in-tree by sym_amd/build.py. Importing the product path
+without it raises: there is no CPU fallback.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.environ.get("RELX_LIBRARY", os.path.join(HERE, "librelx.so"))
+
+RELX_MAX_RANK = 8
+RELX_MAX_STAGES = 8
+
+
+class NativeLibraryMissing(RuntimeError):
+    pass
+
+
+class relx_err(ctypes.Structure):
+    _fields_ = [("code", ctypes.c_char * 48), ("message", ctypes.c_char * 464),
+                ("offset", ctypes.c_int64), ("completion", ctypes.c_int)]
+
+
+class relx_param(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("kind", ctypes.c_int), ("bits", ctypes.c_int),
+                ("rank", ctypes.c_int), ("length", ctypes.c_int64), ("data", ctypes.c_void_p),
+                ("nbytes", ctypes.c_size_t)]
+
+
+_I64R = ctypes.c_int64 * RELX_MAX_RANK
+
+
+class relx_bound_info(ctypes.Structure):
+    _fields_ = [("typed", ctypes.c_int), ("rank", ctypes.c_int), ("extents", _I64R),
+                ("src_strides", _I64R), ("dst_strides", _I64R), ("pad_lo", _I64R),
+                ("pad_hi", _I64R), ("element_size", ctypes.c_int),
+                ("total_bytes", ctypes.c_int64), ("source_bytes", ctypes.c_int64),
+                ("destination_bytes", ctypes.c_int64), ("parameter_bytes", ctypes.c_int64),
+                ("stages", ctypes.c_int), ("bytes_at", ctypes.c_int64 * (RELX_MAX_STAGES + 1)),
+                ("source_width", ctypes.c_int), ("result_width", ctypes.c_int),
+                ("source_rank", ctypes.c_int), ("source_extents", _I64R),
+                ("result_rank", ctypes.c_int), ("result_extents", _I64R),
+                ("kernel", ctypes.c_char * 32)]
+
+
+class relx_ctx_stats(ctypes.Structure):
+    _fields_ = [("pinned_bytes", ctypes.c_int64), ("device_bytes", ctypes.c_int64),
+                ("calls", ctypes.c_int64), ("failures", ctypes.c_int64),
+                ("quarantined", ctypes.c_int)]
+
+
+class relx_options(ctypes.Structure):
+    _fields_ = [("n_buffers", ctypes.c_int), ("chunk_bytes", ctypes.c_int64),
+                ("host_stages", ctypes.c_int), ("gather_threads", ctypes.c_int),
+                ("source_pinned", ctypes.c_int), ("caller_stream", ctypes.c_uint64),
+                ("no_wait", ctypes.c_int)]
+
+
+class relx_report(ctypes.Structure):
+    _fields_ = [("implementation", ctypes.c_char * 40), ("source_bytes", ctypes.c_int64),
+                ("wire_bytes", ctypes.c_int64), ("destination_bytes", ctypes.c_int64),
+                ("parameter_bytes", ctypes.c_int64),
+                ("payload_bytes_transferred", ctypes.c_int64), ("chunks", ctypes.c_int64),
+                ("kernel_launches", ctypes.c_int64), ("wire_boundary", ctypes.c_int),
+                ("direct_dma", ctypes.c_int)]
+
+    def as_dict(self):
+        return {f: (getattr(self, f).decode() if f == "implementation" else getattr(self, f))
+                for f, _ in self._fields_}
+
+
+# every entry point include/relx.h declares, with its ctypes signature
+_VP, _SZ, _I, _I64, _U64 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int64, ctypes.c_uint64
+_E = ctypes.POINTER(relx_err)
+SIGNATURES = {
+    "relx_version": (ctypes.c_char_p, []),
+    "relx_wire_version": (_I, [ctypes.c_char_p, _SZ]),
+    "relx_plan_load": (_I, [ctypes.c_char_p, _SZ, ctypes.POINTER(_VP), _E]),
+    "relx_plan_is_typed": (_I, [_VP]),
+    "relx_plan_symbol_count": (_I, [_VP]),
+    "relx_plan_symbol": (ctypes.c_char_p, [_VP, _I]),
+    "relx_plan_free": (None, [_VP]),
+    "relx_bind": (_I, [_VP, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_I64), _I,
+                       ctypes.POINTER(relx_param), _I, ctypes.POINTER(_VP), _E]),
+    "relx_bound_free": (None, [_VP]),
+    "relx_bound_query": (_I, [_VP, ctypes.POINTER(relx_bound_info)]),
+    "relx_ctx_create": (_I, [_I, _I64, ctypes.POINTER(_VP), _E]),
+    "relx_ctx_close": (_I, [_VP, _E]),
+    "relx_ctx_stats_get": (_I, [_VP, ctypes.POINTER(relx_ctx_stats)]),
+    "relx_execute_h2d": (_I, [_VP, _VP, _VP, _SZ, _VP, _SZ, ctypes.POINTER(relx_options),
+                              ctypes.POINTER(relx_report), _E]),
+    "relx_execute_group_h2d": (_I, [_VP, _I, ctypes.POINTER(_VP), ctypes.POINTER(_VP),
+                                    ctypes.POINTER(_SZ), ctypes.POINTER(_VP), ctypes.POINTER(_SZ),
+                                    ctypes.POINTER(relx_options), ctypes.POINTER(relx_report),
+                                    ctypes.POINTER(relx_report), _E]),
+    "relx_relayout_device": (_I, [_VP, _VP, _I, _VP, _VP, _U64, _E]),
+    "relx_host_stage": (_I, [_VP, _I, _VP, _VP, _I, _E]),
+    "relx_ctx_synchronize": (_I, [_VP, _E]),
+    "relx_host_alloc": (_I, [_SZ, ctypes.POINTER(_VP), _E]),
+    "relx_host_free": (_I, [_VP]),
+    "relx_measure_h2d": (ctypes.c_double, [_I, _SZ, _I, _I]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded library; raises NativeLibraryMissing when it is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise NativeLibraryMissing(
+                "librelx.so is not built (%s); run `python -m sym_amd.build`" % LIB_PATH)
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+class RelxError(RuntimeError):
+    """A librelx failure: `code` is the stable reason code."""
+
+    def __init__(self, code, message, offset=-1, completion=0):
+        super().__init__("%s: %s" % (code, message))
+        self.code = code
+        self.detail = message
+        self.offset = offset
+        self.completion = {0: "not_launched", 1: "complete", 2: "unknown"}.get(completion, "unknown")
+
+
+def check(rc, err):
+    if rc != 0:
+        raise RelxError(err.code.decode(errors="replace"), err.message.decode(errors="replace"),
+                        err.offset, err.completion)

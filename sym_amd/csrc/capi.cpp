@@ -1,0 +1,358 @@
+// capi.cpp - extern "C" entry points of librelx (declared in include/relx.h).
+// No exception crosses this boundary: every failure becomes a status code and
+// a filled relx_err.
+#include "../../include/relx.h"
+
+#include <cstdio>
+#include <cstring>
+
+#include "runtime.h"
+
+namespace relx {
+void execute_members(Context &ctx, int n, BoundHandle *const *bounds, const void *const *srcs,
+                     const size_t *src_bytes, void *const *dsts, const size_t *dst_bytes,
+                     const relx_options &opt, relx_report *reports, relx_report *total);
+std::unique_ptr<Context> make_context(int device, int64_t max_retained);
+bool drain(Context &ctx);
+void destroy_context(Context &ctx);
+void relayout_device(Context &ctx, BoundHandle &h, uint32_t k, const void *wire, void *dst,
+                     hipStream_t stream);
+double measure_h2d(int device, size_t bytes, int iters, int rounds);
+} // namespace relx
+
+struct relx_plan {
+  std::unique_ptr<relx::Plan> plan;
+};
+struct relx_bound {
+  relx::BoundHandle h;
+};
+struct relx_ctx {
+  std::unique_ptr<relx::Context> ctx;
+};
+
+namespace {
+
+void set_err(relx_err *err, const std::string &code, const std::string &msg, int64_t offset = -1,
+             int completion = RELX_NOT_LAUNCHED) {
+  if (!err)
+    return;
+  std::memset(err, 0, sizeof(*err));
+  std::snprintf(err->code, sizeof(err->code), "%s", code.c_str());
+  std::snprintf(err->message, sizeof(err->message), "%s", msg.c_str());
+  err->offset = offset;
+  err->completion = completion;
+}
+
+void clear_err(relx_err *err) {
+  if (err) {
+    std::memset(err, 0, sizeof(*err));
+    err->offset = -1;
+  }
+}
+
+template <class F> int guarded(relx_err *err, F &&fn) {
+  try {
+    clear_err(err);
+    fn();
+    return RELX_OK;
+  } catch (const relx::Error &e) {
+    set_err(err, e.code, e.message, e.offset);
+  } catch (const std::bad_alloc &) {
+    set_err(err, "out_of_memory", "host allocation failed");
+  } catch (const std::exception &e) {
+    set_err(err, "internal_error", e.what());
+  }
+  return RELX_ERROR;
+}
+
+} // namespace
+
+extern "C" {
+
+const char *relx_version(void) {
+  return "librelx 0.1 (gfx950; wire format v0 layout, v1 typed)";
+}
+
+int relx_wire_version(const uint8_t *blob, size_t n) {
+  return blob ? relx::peek_wire_version(blob, n) : -1;
+}
+
+int relx_plan_load(const uint8_t *blob, size_t n, relx_plan **out, relx_err *err) {
+  return guarded(err, [&] {
+    if (!blob || !out)
+      throw relx::Error("invalid_argument", "null blob or output");
+    auto p = relx::decode(blob, n);
+    *out = new relx_plan{std::move(p)};
+  });
+}
+
+int relx_plan_is_typed(const relx_plan *plan) { return plan && plan->plan->version == 1; }
+
+int relx_plan_symbol_count(const relx_plan *plan) {
+  return plan ? static_cast<int>(plan->plan->symbols.size()) : 0;
+}
+
+const char *relx_plan_symbol(const relx_plan *plan, int i) {
+  if (!plan || i < 0 || i >= static_cast<int>(plan->plan->symbols.size()))
+    return nullptr;
+  return plan->plan->symbols[static_cast<size_t>(i)].c_str();
+}
+
+void relx_plan_free(relx_plan *plan) { delete plan; }
+
+int relx_bind(const relx_plan *plan, const char *const *sym_names, const int64_t *sym_values,
+              int nsym, const relx_param *params, int nparam, relx_bound **out,
+              relx_err *err) {
+  return guarded(err, [&] {
+    if (!plan || !out)
+      throw relx::Error("invalid_argument", "null plan or output");
+    std::map<std::string, int64_t> syms;
+    for (int i = 0; i < nsym; ++i)
+      syms[sym_names[i]] = sym_values[i];
+    std::map<std::string, relx::ParamValue> pv;
+    for (int i = 0; i < nparam; ++i) {
+      const relx_param &p = params[i];
+      relx::ParamValue v;
+      v.type.kind = static_cast<uint8_t>(p.kind);
+      v.type.bits = static_cast<uint32_t>(p.bits);
+      if (p.rank == 1)
+        v.extents.push_back(p.length);
+      else if (p.rank != 0)
+        throw relx::Error("bind_error", "parameter rank must be 0 or 1");
+      const auto *d = static_cast<const uint8_t *>(p.data);
+      if (p.nbytes && !d)
+        throw relx::Error("bind_error", "parameter data is null");
+      v.bytes.assign(d, d + p.nbytes);
+      pv[p.name] = std::move(v);
+    }
+    auto b = new relx_bound;
+    try {
+      b->h.bound = relx::bind(*plan->plan, syms, pv);
+      if (b->h.bound->typed)
+        relx::prepare_stages(*b->h.bound, b->h.prep);
+      // Build the default device program now so unsupported plans fail here.
+      (void)b->h.program(0);
+    } catch (...) {
+      delete b;
+      throw;
+    }
+    *out = b;
+  });
+}
+
+void relx_bound_free(relx_bound *bound) { delete bound; }
+
+int relx_bound_query(const relx_bound *bound, relx_bound_info *out) {
+  if (!bound || !out)
+    return RELX_ERROR;
+  std::memset(out, 0, sizeof(*out));
+  const relx::Bound &b = *bound->h.bound;
+  const relx::BoundLayout &L = b.layout;
+  out->typed = b.typed;
+  out->rank = static_cast<int>(L.extents.size());
+  for (int i = 0; i < out->rank && i < RELX_MAX_RANK; ++i) {
+    out->extents[i] = L.extents[static_cast<size_t>(i)];
+    out->src_strides[i] = L.src_strides[static_cast<size_t>(i)];
+    out->dst_strides[i] = L.dst_strides[static_cast<size_t>(i)];
+  }
+  for (const relx::BoundPad &p : L.pads)
+    if (p.axis < RELX_MAX_RANK) {
+      out->pad_lo[p.axis] = p.lo;
+      out->pad_hi[p.axis] = p.hi;
+    }
+  out->element_size = static_cast<int>(L.element_size);
+  out->total_bytes = L.total_bytes;
+  out->source_bytes = b.source_bytes;
+  out->destination_bytes = b.typed ? b.destination_bytes : L.total_bytes;
+  out->parameter_bytes = b.parameter_bytes;
+  out->stages = static_cast<int>(b.stages.size());
+  for (size_t i = 0; i < b.bytes_at.size() && i <= RELX_MAX_STAGES; ++i)
+    out->bytes_at[i] = b.bytes_at[i];
+  out->source_width = static_cast<int>(b.typed ? b.source_type.width() : L.element_size);
+  out->result_width = static_cast<int>(L.element_size);
+  out->source_rank = static_cast<int>(b.source_extents.size());
+  for (int i = 0; i < out->source_rank && i < RELX_MAX_RANK; ++i)
+    out->source_extents[i] = b.source_extents[static_cast<size_t>(i)];
+  out->result_rank = static_cast<int>(b.result_extents.size());
+  for (int i = 0; i < out->result_rank && i < RELX_MAX_RANK; ++i)
+    out->result_extents[i] = b.result_extents[static_cast<size_t>(i)];
+  try {
+    const relx::DeviceProgram &dp = const_cast<relx::BoundHandle &>(bound->h).program(0);
+    std::snprintf(out->kernel, sizeof(out->kernel), "%s", dp.kernel);
+    if (!b.typed)
+      out->source_bytes = dp.wire_elems * L.element_size;
+  } catch (...) {
+    std::snprintf(out->kernel, sizeof(out->kernel), "unavailable");
+  }
+  return RELX_OK;
+}
+
+int relx_ctx_create(int device, int64_t max_retained_bytes, relx_ctx **out, relx_err *err) {
+  return guarded(err, [&] {
+    if (!out)
+      throw relx::Error("invalid_argument", "null output");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
+      throw relx::Error("backend_failure", "no HIP device is visible");
+    if (device < 0 || device >= n)
+      throw relx::Error("device_mismatch", "device " + std::to_string(device) + " out of range");
+    *out = new relx_ctx{relx::make_context(device, max_retained_bytes)};
+  });
+}
+
+int relx_ctx_close(relx_ctx *ctx, relx_err *err) {
+  return guarded(err, [&] {
+    if (!ctx)
+      return;
+    std::lock_guard<std::mutex> g(ctx->ctx->mu);
+    if (!relx::drain(*ctx->ctx)) {
+      // Completion unknown: keep every resource for the process lifetime.
+      ctx->ctx->quarantined = true;
+      ctx->ctx->closed = true;
+      throw relx::Error("completion_unknown", "context could not be drained; quarantined");
+    }
+    relx::destroy_context(*ctx->ctx);
+    ctx->ctx->closed = true;
+  }) == RELX_OK
+             ? (delete ctx, RELX_OK)
+             : RELX_ERROR;
+}
+
+int relx_ctx_stats_get(const relx_ctx *ctx, relx_ctx_stats *out) {
+  if (!ctx || !out)
+    return RELX_ERROR;
+  const relx::Context &c = *ctx->ctx;
+  out->pinned_bytes = static_cast<int64_t>(c.slots.size() * c.slot_bytes);
+  out->device_bytes = static_cast<int64_t>(c.wire_cap);
+  out->calls = c.calls;
+  out->failures = c.failures;
+  out->quarantined = c.quarantined ? 1 : 0;
+  return RELX_OK;
+}
+
+static int run_group(relx_ctx *ctx, int n, const relx_bound *const *bounds,
+                     const void *const *srcs, const size_t *src_bytes, void *const *dsts,
+                     const size_t *dst_bytes, const relx_options *opt, relx_report *reports,
+                     relx_report *total, relx_err *err) {
+  if (!ctx) {
+    set_err(err, "invalid_argument", "null context");
+    return RELX_ERROR;
+  }
+  relx::Context &c = *ctx->ctx;
+  std::lock_guard<std::mutex> g(c.mu);
+  if (c.closed || c.quarantined) {
+    set_err(err, "resources_closed", "context is closed or quarantined");
+    return RELX_ERROR;
+  }
+  relx_options o{};
+  o.host_stages = -1;
+  o.source_pinned = -1;
+  if (opt)
+    o = *opt;
+  ++c.calls;
+  const int rc = guarded(err, [&] {
+    if (n < 1 || n > 256)
+      throw relx::Error("invalid_options", "a group holds 1..256 members");
+    std::vector<relx::BoundHandle *> hs;
+    for (int i = 0; i < n; ++i) {
+      if (!bounds[i])
+        throw relx::Error("invalid_argument", "null bound plan");
+      hs.push_back(const_cast<relx::BoundHandle *>(&bounds[i]->h));
+    }
+    relx::execute_members(c, n, hs.data(), srcs, src_bytes, dsts, dst_bytes, o, reports, total);
+  });
+  if (rc != RELX_OK) {
+    ++c.failures;
+    // Drain what was enqueued; unknown completion quarantines the context.
+    const bool complete = relx::drain(c);
+    if (err)
+      err->completion = complete ? RELX_COMPLETE : RELX_UNKNOWN;
+    if (!complete)
+      c.quarantined = true;
+  }
+  return rc;
+}
+
+int relx_execute_h2d(relx_ctx *ctx, const relx_bound *bound, const void *src, size_t src_bytes,
+                     void *dst, size_t dst_bytes, const relx_options *opt, relx_report *report,
+                     relx_err *err) {
+  return run_group(ctx, 1, &bound, &src, &src_bytes, &dst, &dst_bytes, opt, report, nullptr,
+                   err);
+}
+
+int relx_execute_group_h2d(relx_ctx *ctx, int n, const relx_bound *const *bounds,
+                           const void *const *srcs, const size_t *src_bytes, void *const *dsts,
+                           const size_t *dst_bytes, const relx_options *opt,
+                           relx_report *reports, relx_report *total, relx_err *err) {
+  return run_group(ctx, n, bounds, srcs, src_bytes, dsts, dst_bytes, opt, reports, total, err);
+}
+
+int relx_relayout_device(relx_ctx *ctx, const relx_bound *bound, int wire_boundary,
+                         const void *wire, void *dst, uint64_t stream, relx_err *err) {
+  return guarded(err, [&] {
+    if (!ctx || !bound || !wire || !dst)
+      throw relx::Error("invalid_argument", "null argument");
+    if (wire_boundary < 0)
+      throw relx::Error("invalid_boundary", "negative wire boundary");
+    relx::relayout_device(*ctx->ctx, const_cast<relx::BoundHandle &>(bound->h),
+                          static_cast<uint32_t>(wire_boundary), wire, dst,
+                          reinterpret_cast<hipStream_t>(stream));
+  });
+}
+
+int relx_host_stage(const relx_bound *bound, int host_stages, const void *src, void *wire,
+                    int threads, relx_err *err) {
+  return guarded(err, [&] {
+    if (!bound || !src || !wire)
+      throw relx::Error("invalid_argument", "null argument");
+    const relx::BoundHandle &h = bound->h;
+    if (!h.bound->typed && host_stages != 0)
+      throw relx::Error("invalid_boundary", "layout plans have no stages");
+    if (host_stages < 0 || host_stages > static_cast<int>(h.prep.stages.size()))
+      throw relx::Error("invalid_boundary", "host stages outside the program");
+    for (int j = 0; j < host_stages; ++j)
+      if (h.prep.stages[static_cast<size_t>(j)].mode != relx::kChanNone)
+        throw relx::Error("invalid_options", "host stages must be per-tensor stages");
+    const uint32_t sw = h.bound->typed ? h.bound->source_type.width() : h.bound->layout.element_size;
+    int64_t n = 1;
+    if (h.bound->typed)
+      for (int64_t e : h.bound->source_extents)
+        n *= e;
+    else
+      n = const_cast<relx::BoundHandle &>(h).program(0).wire_elems;
+    relx::Workers w(static_cast<unsigned>(threads > 0 ? threads : 1));
+    w.parallel_for(n, int64_t{1} << 16, [&](int64_t a, int64_t b) {
+      relx::host_transform(h.prep, static_cast<uint32_t>(host_stages), sw, src, wire, a, b);
+    });
+  });
+}
+
+int relx_ctx_synchronize(relx_ctx *ctx, relx_err *err) {
+  return guarded(err, [&] {
+    if (!ctx)
+      throw relx::Error("invalid_argument", "null context");
+    if (!relx::drain(*ctx->ctx))
+      throw relx::Error("backend_failure", "stream synchronize failed");
+  });
+}
+
+int relx_host_alloc(size_t bytes, void **out, relx_err *err) {
+  return guarded(err, [&] {
+    if (!out)
+      throw relx::Error("invalid_argument", "null output");
+    if (hipHostMalloc(out, bytes, hipHostMallocDefault) != hipSuccess)
+      throw relx::Error("out_of_memory", "hipHostMalloc failed");
+  });
+}
+
+int relx_host_free(void *p) { return hipHostFree(p) == hipSuccess ? RELX_OK : RELX_ERROR; }
+
+double relx_measure_h2d(int device, size_t bytes, int iters, int rounds) {
+  try {
+    return relx::measure_h2d(device, bytes, iters, rounds);
+  } catch (...) {
+    return -1.0;
+  }
+}
+
+} // extern "C"

@@ -1,0 +1,107 @@
+// program.h - the device form of a bound plan: POD launch arguments shared
+// by the host planner (program.cpp) and the HIP kernels (kernels.hip).
+//
+// A DeviceProgram describes, for one wire boundary k, how to turn the dense
+// SOURCE-layout wire values at boundary k into the dense RESULT-layout values
+// after the last stage: an iteration box over the coalesced destination axes
+// (padded coordinates), the source strides of the valid region, the pad fill,
+// and the remaining value stages with their per-channel parameters.
+#pragma once
+
+#include <cstdint>
+
+namespace relx {
+
+constexpr int kMaxRank = 8;
+constexpr int kMaxStages = 6;
+constexpr int kMaxChanTokens = 24;
+
+// Value-stage operations the device runs (docs/reloc-typed-semantics.md).
+enum DevOp : uint8_t {
+  kOpF32toF16 = 0, // cast ieee_rne
+  kOpF16toF32 = 1, // cast exact
+  kOpF32toBF16 = 2,
+  kOpBF16toF32 = 3,
+  kOpQuantize = 4,   // symmetric_rne with inv = fl32(1/scale) formed on the host
+  kOpDequantize = 5, // affine: (q - zp) * scale, one rounding
+};
+
+// How a stage picks its parameter entry.
+enum ChanMode : uint8_t {
+  kChanNone = 0, // per tensor: entry 0
+  kChanDim = 1,  // the logical result coordinate along `dim`
+  kChanExpr = 2, // a channel expression over result coordinates (generic kernel)
+};
+
+// Division by a runtime constant for n < 2^32: q = (umulhi(n, m) + n) >> s.
+struct FastDiv {
+  uint32_t d, m, s, pad_;
+};
+
+struct ChanToken {
+  int32_t op; // plan opcode; PUSH_SYM is resolved to PUSH_CONST at prepare time
+  int32_t pad_;
+  int64_t value;
+};
+
+struct DevStage {
+  uint8_t op;
+  uint8_t mode;
+  uint8_t dim;       // kChanDim: result dimension
+  uint8_t zp_per_ch; // zero point has one entry per channel
+  uint8_t vec;       // fast kernels: 0 channel constant across a vector, 1 +1 per element
+  uint8_t pad_[3];
+  uint32_t scale_off; // float param index (dequant scale / quant reciprocal)
+  uint32_t zp_off;    // int param index
+  uint32_t len;       // parameter entries
+  int32_t tok_begin, tok_count;
+};
+
+struct Chain {
+  int32_t n;
+  int32_t ntok;
+  DevStage st[kMaxStages];
+  ChanToken tok[kMaxChanTokens];
+};
+
+enum Family : int32_t {
+  kFamGeneric = 0,
+  kFamStream = 1,     // innermost axis contiguous on both sides
+  kFamTranspose = 2,  // batched 2-D transpose, LDS tiled
+  kFamInterleave = 3, // planar -> interleaved with a small padded inner axis
+};
+
+// Launch arguments. All extents/strides are in elements of the coalesced
+// destination-order axes of the bound layout.
+struct KArgs {
+  const uint8_t *src; // wire (device) at the program's boundary
+  uint8_t *dst;       // result (device)
+  const float *pf;    // float parameters
+  const int32_t *pi;  // int parameters
+  int32_t rank;
+  int32_t win, wout;  // element bytes of the wire and of the result
+  int32_t has_fill;
+  uint64_t fill;
+  int64_t pext[kMaxRank]; // padded extents
+  int64_t lo[kMaxRank];   // leading pad per axis
+  int64_t vext[kMaxRank]; // valid extents
+  int64_t ss[kMaxRank];   // source strides (valid coordinates)
+  int64_t ds[kMaxRank];   // destination strides (padded coordinates)
+  int64_t box_lo[kMaxRank];
+  int64_t box_ext[kMaxRank];
+  FastDiv box_div[kMaxRank]; // over box_ext (family-specific inner handling)
+  int32_t res_rank;
+  int32_t idx32; // every index of this launch fits in 32 bits
+  int64_t rs[kMaxRank]; // result strides (dense, padded result)
+  int64_t re[kMaxRank]; // result extents
+  FastDiv rs_div[kMaxRank];
+  FastDiv re_div[kMaxRank];
+  int64_t work; // work items in this launch
+  // family parameters
+  int32_t qa, ca; // transpose: source-inner axis (dst row) and dst-inner axis
+  int32_t vec;    // stream: elements per vector; interleave: pixels per thread
+  int32_t cpad;   // interleave: padded inner extent
+  Chain chain;
+};
+
+} // namespace relx

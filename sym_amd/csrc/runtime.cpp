@@ -1,0 +1,594 @@
+// runtime.cpp - the H2D pipeline on one MI355X.
+//
+// Role of the reference's CudaBackend + Pipeline + transformToDevice
+// (libreloc/cuda/CudaBackend.cu:55-282, libreloc/src/Pipeline.cpp:163-232,
+// libreloc/src/Dispatch.cpp:246-564), designed for this GPU:
+//
+//   * compact bytes cross PCIe: the wire is the SOURCE at boundary k (int8 /
+//     fp16 as stored, or the source after leading narrowing casts applied by
+//     the host while it stages), never the widened result;
+//   * chunks follow the source-outer axis, so each chunk's wire bytes are one
+//     contiguous range and the kernel for that chunk needs nothing else;
+//   * copy stream: host workers fill pinned ring slot i (event-gated reuse),
+//     hipMemcpyAsync moves it to the device wire buffer, an event marks it;
+//   * compute stream: waits on the chunk's event and relayouts that chunk's
+//     box while the next chunk is in flight.
+// A page-locked source skips the ring and is DMA'd in place.
+#include "runtime.h"
+
+#include <immintrin.h>
+
+#include <algorithm>
+#include <cstring>
+
+#include "../../include/relx.h"
+
+namespace relx {
+
+#define HIPCHECK(expr)                                                                      \
+  do {                                                                                      \
+    hipError_t e_ = (expr);                                                                 \
+    if (e_ != hipSuccess)                                                                   \
+      throw Error("backend_failure", std::string(#expr) + ": " + hipGetErrorString(e_));    \
+  } while (0)
+
+// ------------------------------------------------------------ workers
+
+Workers::Workers(unsigned threads) {
+  for (unsigned i = 1; i < std::max(1u, threads); ++i)
+    threads_.emplace_back([this, i] { loop(i); });
+}
+
+Workers::~Workers() {
+  {
+    std::lock_guard<std::mutex> g(mu_);
+    stop_ = true;
+  }
+  go_.notify_all();
+  for (auto &t : threads_)
+    t.join();
+}
+
+void Workers::loop(unsigned id) {
+  uint64_t seen = 0;
+  for (;;) {
+    std::pair<int64_t, int64_t> r;
+    const std::function<void(int64_t, int64_t)> *fn;
+    {
+      std::unique_lock<std::mutex> g(mu_);
+      go_.wait(g, [&] { return stop_ || generation_ != seen; });
+      if (stop_)
+        return;
+      seen = generation_;
+      r = ranges_[id];
+      fn = fn_;
+    }
+    if (r.second > r.first)
+      (*fn)(r.first, r.second);
+    {
+      std::lock_guard<std::mutex> g(mu_);
+      if (--pending_ == 0)
+        done_.notify_one();
+    }
+  }
+}
+
+void Workers::parallel_for(int64_t n, int64_t grain,
+                           const std::function<void(int64_t, int64_t)> &fn) {
+  const unsigned total = size();
+  const int64_t parts =
+      std::max<int64_t>(1, std::min<int64_t>(total, n / std::max<int64_t>(1, grain)));
+  if (parts <= 1 || threads_.empty()) {
+    if (n > 0)
+      fn(0, n);
+    return;
+  }
+  {
+    std::lock_guard<std::mutex> g(mu_);
+    ranges_.assign(total, {0, 0});
+    for (int64_t i = 0; i < parts; ++i)
+      ranges_[static_cast<size_t>(i)] = {n * i / parts, n * (i + 1) / parts};
+    fn_ = &fn;
+    pending_ = static_cast<unsigned>(threads_.size());
+    ++generation_;
+  }
+  go_.notify_all();
+  fn(ranges_[0].first, ranges_[0].second);
+  std::unique_lock<std::mutex> g(mu_);
+  done_.wait(g, [&] { return pending_ == 0; });
+}
+
+// ------------------------------------------------------------ staging
+
+namespace {
+
+__attribute__((target("avx2,f16c"))) void f32_to_f16_f16c(const float *s, uint16_t *d,
+                                                          int64_t n) {
+  int64_t i = 0;
+  for (; i + 8 <= n; i += 8) {
+    const __m256 x = _mm256_loadu_ps(s + i);
+    _mm_storeu_si128(reinterpret_cast<__m128i *>(d + i),
+                     _mm256_cvtps_ph(x, _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC));
+  }
+  for (; i < n; ++i) {
+    uint32_t b;
+    std::memcpy(&b, s + i, 4);
+    d[i] = f32_to_f16_bits(b);
+  }
+}
+
+bool have_f16c() {
+  static const bool ok = __builtin_cpu_supports("f16c") && __builtin_cpu_supports("avx2");
+  return ok;
+}
+
+} // namespace
+
+void host_transform(const Prepared &p, uint32_t k, uint32_t src_width, const void *src,
+                    void *dst, int64_t e0, int64_t e1) {
+  const uint8_t *s = static_cast<const uint8_t *>(src);
+  uint8_t *d = static_cast<uint8_t *>(dst);
+  if (k == 0) {
+    std::memcpy(d + e0 * src_width, s + e0 * src_width, static_cast<size_t>(e1 - e0) * src_width);
+    return;
+  }
+  if (k == 1 && p.stages[0].op == kOpF32toF16 && have_f16c()) {
+    f32_to_f16_f16c(reinterpret_cast<const float *>(s) + e0, reinterpret_cast<uint16_t *>(d) + e0,
+                    e1 - e0);
+    return;
+  }
+  const uint32_t wout = p.stages[k - 1].out_width;
+  for (int64_t i = e0; i < e1; ++i) {
+    uint64_t x = 0;
+    std::memcpy(&x, s + i * src_width, src_width);
+    for (uint32_t j = 0; j < k; ++j)
+      x = host_apply(p.stages[j], x, 0);
+    std::memcpy(d + i * wout, &x, wout);
+  }
+}
+
+// ------------------------------------------------------------ handles
+
+const DeviceProgram &BoundHandle::program(uint32_t k) {
+  std::lock_guard<std::mutex> g(mu);
+  auto it = programs.find(k);
+  if (it == programs.end())
+    it = programs.emplace(k, build_program(*bound, prep, k)).first;
+  return *it->second;
+}
+
+BoundHandle::DevParams BoundHandle::device_params(int device, uint32_t k) {
+  const DeviceProgram &dp = program(k);
+  std::lock_guard<std::mutex> g(mu);
+  auto key = std::make_pair(device, k);
+  auto it = params.find(key);
+  if (it != params.end())
+    return it->second;
+  DevParams d;
+  HIPCHECK(hipMalloc(&d.pf, dp.pf.size() * sizeof(float)));
+  HIPCHECK(hipMalloc(&d.pi, dp.pi.size() * sizeof(int32_t)));
+  HIPCHECK(hipMemcpy(d.pf, dp.pf.data(), dp.pf.size() * sizeof(float), hipMemcpyHostToDevice));
+  HIPCHECK(hipMemcpy(d.pi, dp.pi.data(), dp.pi.size() * sizeof(int32_t), hipMemcpyHostToDevice));
+  params.emplace(key, d);
+  return d;
+}
+
+BoundHandle::~BoundHandle() {
+  for (auto &kv : params) {
+    int cur = 0;
+    if (hipGetDevice(&cur) == hipSuccess && cur != kv.first.first)
+      (void)hipSetDevice(kv.first.first);
+    (void)hipFree(kv.second.pf);
+    (void)hipFree(kv.second.pi);
+    if (cur != kv.first.first)
+      (void)hipSetDevice(cur);
+  }
+}
+
+} // namespace relx
+
+// ================================================================ driver
+
+namespace relx {
+
+namespace {
+
+struct DeviceGuard {
+  int prev = -1;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess)
+      prev = -1;
+    if (prev != dev)
+      HIPCHECK(hipSetDevice(dev));
+  }
+  ~DeviceGuard() {
+    int cur;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev)
+      (void)hipSetDevice(prev);
+  }
+};
+
+constexpr int kChunkEvents = 32;
+
+void ensure_wire(Context &ctx, size_t bytes) {
+  if (ctx.wire_cap >= bytes)
+    return;
+  if (ctx.wire) {
+    HIPCHECK(hipStreamSynchronize(ctx.compute));
+    HIPCHECK(hipFree(ctx.wire));
+    ctx.wire = nullptr;
+    ctx.wire_cap = 0;
+  }
+  const size_t round = size_t{2} << 20;
+  const size_t cap = (bytes + round - 1) / round * round;
+  HIPCHECK(hipMalloc(&ctx.wire, cap));
+  ctx.wire_cap = cap;
+}
+
+void ensure_ring(Context &ctx, int n, size_t slot_bytes) {
+  if (static_cast<int>(ctx.slots.size()) >= n && ctx.slot_bytes >= slot_bytes)
+    return;
+  // drain users of the old ring before freeing it
+  for (hipEvent_t e : ctx.slot_ev)
+    HIPCHECK(hipEventSynchronize(e));
+  for (void *s : ctx.slots)
+    HIPCHECK(hipHostFree(s));
+  for (hipEvent_t e : ctx.slot_ev)
+    HIPCHECK(hipEventDestroy(e));
+  ctx.slots.clear();
+  ctx.slot_ev.clear();
+  const size_t round = size_t{1} << 20;
+  ctx.slot_bytes = std::max(ctx.slot_bytes, (slot_bytes + round - 1) / round * round);
+  const int want = std::max<int>(n, 2);
+  for (int i = 0; i < want; ++i) {
+    void *p = nullptr;
+    HIPCHECK(hipHostMalloc(&p, ctx.slot_bytes, hipHostMallocDefault));
+    ctx.slots.push_back(p);
+    hipEvent_t e;
+    HIPCHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    HIPCHECK(hipEventRecord(e, ctx.copy)); // a recorded, completed state
+    ctx.slot_ev.push_back(e);
+  }
+}
+
+bool probe_pinned(const void *p) {
+  hipPointerAttribute_t attr;
+  const hipError_t e = hipPointerGetAttributes(&attr, p);
+  if (e != hipSuccess) {
+    (void)hipGetLastError(); // pageable memory: clear the probe's error
+    return false;
+  }
+  return attr.type == hipMemoryTypeHost;
+}
+
+// Leading stages the host applies while staging: per-tensor stages that do
+// not widen the element (so the wire shrinks or stays), stopping at the
+// first per-channel or widening stage.
+uint32_t auto_host_stages(const BoundHandle &h) {
+  if (!h.bound->typed)
+    return 0;
+  uint32_t k = 0;
+  uint32_t width = h.bound->source_type.width();
+  for (const HostStage &s : h.prep.stages) {
+    if (s.mode != kChanNone || s.out_width >= width)
+      break;
+    width = s.out_width;
+    ++k;
+  }
+  return k;
+}
+
+struct Member {
+  BoundHandle *h;
+  const uint8_t *src;
+  size_t src_bytes;
+  uint8_t *dst;
+  size_t dst_bytes;
+  relx_report *report;
+  uint32_t k;
+  const DeviceProgram *dp;
+  bool direct;
+  size_t wire_off;
+};
+
+} // namespace
+
+void execute(Context &ctx, std::vector<Member> &members, const relx_options &opt,
+             relx_report *total);
+
+} // namespace relx
+
+// The functions below are reached through capi.cpp.
+namespace relx {
+
+void execute_members(Context &ctx, int n, BoundHandle *const *bounds, const void *const *srcs,
+                     const size_t *src_bytes, void *const *dsts, const size_t *dst_bytes,
+                     const relx_options &opt, relx_report *reports, relx_report *total) {
+  DeviceGuard guard(ctx.device);
+  std::vector<Member> ms;
+  size_t wire_total = 0;
+  const int hs = opt.host_stages;
+  for (int i = 0; i < n; ++i) {
+    BoundHandle *h = bounds[i];
+    Member m{h, static_cast<const uint8_t *>(srcs[i]), src_bytes[i],
+             static_cast<uint8_t *>(dsts[i]), dst_bytes[i], reports ? &reports[i] : nullptr, 0,
+             nullptr, false, 0};
+    const bool pinned = opt.source_pinned > 0 || (opt.source_pinned < 0 && probe_pinned(m.src));
+    const uint32_t nst = static_cast<uint32_t>(h->prep.stages.size());
+    if (hs < 0)
+      m.k = pinned ? 0 : auto_host_stages(*h);
+    else
+      m.k = static_cast<uint32_t>(std::min<int>(hs, static_cast<int>(nst)));
+    for (uint32_t j = 0; j < m.k; ++j)
+      if (h->prep.stages[j].mode != kChanNone)
+        throw Error("invalid_options", "host stages must be per-tensor stages");
+    m.dp = &h->program(m.k);
+    m.direct = pinned && m.k == 0;
+    const Bound &b = *h->bound;
+    const int64_t need_src = b.typed ? b.source_bytes
+                                     : m.dp->wire_elems * static_cast<int64_t>(b.layout.element_size);
+    if (static_cast<int64_t>(m.src_bytes) < need_src)
+      throw Error("insufficient_capacity", "source holds " + std::to_string(m.src_bytes) +
+                                               " bytes, the plan reads " + std::to_string(need_src));
+    const int64_t need_dst = m.dp->dst_elems * m.dp->base.wout;
+    if (static_cast<int64_t>(m.dst_bytes) < need_dst)
+      throw Error("insufficient_capacity", "destination holds " + std::to_string(m.dst_bytes) +
+                                               " bytes, the plan writes " + std::to_string(need_dst));
+    if (!m.src || !m.dst)
+      throw Error("invalid_view", "null source or destination");
+    m.wire_off = wire_total;
+    wire_total += (static_cast<size_t>(m.dp->wire_bytes) + 255) / 256 * 256;
+    ms.push_back(m);
+  }
+  execute(ctx, ms, opt, total);
+}
+
+void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
+             relx_report *total) {
+  size_t wire_total = 0;
+  for (const Member &m : ms)
+    wire_total = std::max(wire_total, m.wire_off + static_cast<size_t>(m.dp->wire_bytes));
+  ensure_wire(ctx, wire_total);
+
+  // Chunk plan per member: units of the chunk axis per chunk.
+  const int64_t default_chunk = int64_t{8} << 20;
+  const int64_t want_chunk = opt.chunk_bytes > 0 ? opt.chunk_bytes : default_chunk;
+  size_t max_slot = 0;
+  struct Plan1 {
+    int64_t units, per_chunk, unit_wire, unit_src;
+  };
+  std::vector<Plan1> plans;
+  for (const Member &m : ms) {
+    const DeviceProgram &dp = *m.dp;
+    Plan1 p{};
+    const uint32_t sw = m.h->bound->typed ? m.h->bound->source_type.width()
+                                          : m.h->bound->layout.element_size;
+    if (dp.chunk_axis >= 0) {
+      p.units = dp.base.vext[dp.chunk_axis];
+      p.unit_wire = dp.chunk_stride * dp.base.win;
+      p.unit_src = dp.chunk_stride * sw;
+      int64_t per = std::max<int64_t>(1, want_chunk / std::max<int64_t>(1, p.unit_wire));
+      per = std::max<int64_t>(dp.chunk_align, per / dp.chunk_align * dp.chunk_align);
+      p.per_chunk = std::min(per, p.units);
+    } else {
+      p.units = 1;
+      p.per_chunk = 1;
+      p.unit_wire = dp.wire_bytes;
+      p.unit_src = dp.wire_elems * sw;
+    }
+    if (!m.direct)
+      max_slot = std::max(max_slot, static_cast<size_t>(p.per_chunk * p.unit_wire));
+    plans.push_back(p);
+  }
+  const int nslots = opt.n_buffers > 0 ? opt.n_buffers : 3;
+  if (max_slot)
+    ensure_ring(ctx, nslots, max_slot);
+  const unsigned threads = opt.gather_threads > 0 ? static_cast<unsigned>(opt.gather_threads) : 8u;
+  if (!ctx.workers || ctx.worker_threads != threads) {
+    ctx.workers = std::make_unique<Workers>(threads);
+    ctx.worker_threads = threads;
+  }
+
+  hipStream_t caller = reinterpret_cast<hipStream_t>(opt.caller_stream);
+  if (caller) {
+    HIPCHECK(hipEventRecord(ctx.start_ev, caller));
+    HIPCHECK(hipStreamWaitEvent(ctx.copy, ctx.start_ev, 0));
+    HIPCHECK(hipStreamWaitEvent(ctx.compute, ctx.start_ev, 0));
+  }
+  bool any_generic = false;
+  for (const Member &m : ms)
+    any_generic = any_generic || m.dp->family == kFamGeneric;
+  if (any_generic)
+    HIPCHECK(hipMemsetAsync(ctx.status, 0, sizeof(int32_t), ctx.compute));
+
+  int slot = 0;
+  int ev = 0;
+  relx_report sum{};
+  for (size_t mi = 0; mi < ms.size(); ++mi) {
+    Member &m = ms[mi];
+    const DeviceProgram &dp = *m.dp;
+    const Plan1 &p = plans[mi];
+    const BoundHandle::DevParams par = m.h->device_params(ctx.device, m.k);
+    const uint32_t sw = m.h->bound->typed ? m.h->bound->source_type.width()
+                                          : m.h->bound->layout.element_size;
+    uint8_t *wire = ctx.wire + m.wire_off;
+    int64_t chunks = 0, launches = 0;
+    for (int64_t v0 = 0; v0 < p.units; v0 += p.per_chunk) {
+      const int64_t v1 = std::min(p.units, v0 + p.per_chunk);
+      const int64_t woff = v0 * p.unit_wire, wbytes = (v1 - v0) * p.unit_wire;
+      if (m.direct) {
+        HIPCHECK(hipMemcpyAsync(wire + woff, m.src + woff, static_cast<size_t>(wbytes),
+                                hipMemcpyHostToDevice, ctx.copy));
+      } else {
+        uint8_t *s = static_cast<uint8_t *>(ctx.slots[static_cast<size_t>(slot)]);
+        HIPCHECK(hipEventSynchronize(ctx.slot_ev[static_cast<size_t>(slot)]));
+        const int64_t e0 = v0 * (p.unit_src / sw), e1 = v1 * (p.unit_src / sw);
+        const int64_t ne = e1 - e0;
+        const uint8_t *src_base = m.src + e0 * sw;
+        const uint32_t k = m.k;
+        const Prepared &prep = m.h->prep;
+        // each worker converts a contiguous element range into the slot
+        ctx.workers->parallel_for(ne, int64_t{1} << 16, [&](int64_t a, int64_t b) {
+          host_transform(prep, k, sw, src_base, s, a, b);
+        });
+        HIPCHECK(hipMemcpyAsync(wire + woff, s, static_cast<size_t>(wbytes),
+                                hipMemcpyHostToDevice, ctx.copy));
+        HIPCHECK(hipEventRecord(ctx.slot_ev[static_cast<size_t>(slot)], ctx.copy));
+        slot = (slot + 1) % static_cast<int>(ctx.slots.size());
+      }
+      hipEvent_t ce = ctx.chunk_ev[static_cast<size_t>(ev)];
+      ev = (ev + 1) % kChunkEvents;
+      HIPCHECK(hipEventRecord(ce, ctx.copy));
+      HIPCHECK(hipStreamWaitEvent(ctx.compute, ce, 0));
+      KArgs a = box_args(dp, v0, v1, v0 == 0, v1 == p.units);
+      a.src = wire;
+      a.dst = m.dst;
+      a.pf = par.pf;
+      a.pi = par.pi;
+      HIPCHECK(launch_box(dp.family, a, ctx.status, ctx.compute));
+      ++chunks;
+      ++launches;
+    }
+    if (m.report) {
+      relx_report &r = *m.report;
+      std::memset(&r, 0, sizeof(r));
+      const std::string impl =
+          m.k == 0 ? std::string("hip_relayout") : "hip_relayout@" + std::to_string(m.k);
+      std::snprintf(r.implementation, sizeof(r.implementation), "%s", impl.c_str());
+      const Bound &b = *m.h->bound;
+      r.source_bytes = b.typed ? b.source_bytes : dp.wire_elems * sw;
+      r.wire_bytes = dp.wire_bytes;
+      r.destination_bytes = dp.dst_elems * dp.base.wout;
+      r.parameter_bytes = b.parameter_bytes;
+      r.payload_bytes_transferred = dp.wire_bytes;
+      r.chunks = chunks;
+      r.kernel_launches = launches;
+      r.wire_boundary = static_cast<int>(m.k);
+      r.direct_dma = m.direct ? 1 : 0;
+      sum.source_bytes += r.source_bytes;
+      sum.wire_bytes += r.wire_bytes;
+      sum.destination_bytes += r.destination_bytes;
+      sum.parameter_bytes += r.parameter_bytes;
+      sum.payload_bytes_transferred += r.payload_bytes_transferred;
+      sum.chunks += r.chunks;
+      sum.kernel_launches += r.kernel_launches;
+    }
+  }
+  HIPCHECK(hipEventRecord(ctx.done_ev, ctx.compute));
+  if (caller)
+    HIPCHECK(hipStreamWaitEvent(caller, ctx.done_ev, 0));
+  if (total) {
+    std::snprintf(sum.implementation, sizeof(sum.implementation), "hip_relayout_group");
+    *total = sum;
+  }
+  if (opt.no_wait)
+    return;
+  HIPCHECK(hipEventSynchronize(ctx.done_ev));
+  if (any_generic) {
+    int32_t flag = 0;
+    HIPCHECK(hipMemcpy(&flag, ctx.status, sizeof(flag), hipMemcpyDeviceToHost));
+    if (flag)
+      throw Error("channel_out_of_range", "a stage selected a channel outside its parameters");
+  }
+}
+
+// ----------------------------------------------------------- contexts
+
+std::unique_ptr<Context> make_context(int device, int64_t max_retained) {
+  auto ctx = std::make_unique<Context>();
+  ctx->device = device;
+  ctx->max_retained = max_retained;
+  DeviceGuard guard(device);
+  HIPCHECK(hipStreamCreateWithFlags(&ctx->copy, hipStreamNonBlocking));
+  HIPCHECK(hipStreamCreateWithFlags(&ctx->compute, hipStreamNonBlocking));
+  HIPCHECK(hipEventCreateWithFlags(&ctx->start_ev, hipEventDisableTiming));
+  HIPCHECK(hipEventCreateWithFlags(&ctx->done_ev, hipEventDisableTiming));
+  for (int i = 0; i < kChunkEvents; ++i) {
+    hipEvent_t e;
+    HIPCHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    ctx->chunk_ev.push_back(e);
+  }
+  HIPCHECK(hipMalloc(&ctx->status, 256));
+  HIPCHECK(hipMemset(ctx->status, 0, 256));
+  return ctx;
+}
+
+// Drain both streams. False when completion cannot be proven.
+bool drain(Context &ctx) {
+  DeviceGuard guard(ctx.device);
+  const bool a = hipStreamSynchronize(ctx.copy) == hipSuccess;
+  const bool b = hipStreamSynchronize(ctx.compute) == hipSuccess;
+  return a && b;
+}
+
+void destroy_context(Context &ctx) {
+  DeviceGuard guard(ctx.device);
+  for (void *s : ctx.slots)
+    (void)hipHostFree(s);
+  for (hipEvent_t e : ctx.slot_ev)
+    (void)hipEventDestroy(e);
+  for (hipEvent_t e : ctx.chunk_ev)
+    (void)hipEventDestroy(e);
+  if (ctx.start_ev)
+    (void)hipEventDestroy(ctx.start_ev);
+  if (ctx.done_ev)
+    (void)hipEventDestroy(ctx.done_ev);
+  if (ctx.wire)
+    (void)hipFree(ctx.wire);
+  if (ctx.status)
+    (void)hipFree(ctx.status);
+  if (ctx.copy)
+    (void)hipStreamDestroy(ctx.copy);
+  if (ctx.compute)
+    (void)hipStreamDestroy(ctx.compute);
+  ctx.slots.clear();
+  ctx.workers.reset();
+}
+
+void relayout_device(Context &ctx, BoundHandle &h, uint32_t k, const void *wire, void *dst,
+                     hipStream_t stream) {
+  DeviceGuard guard(ctx.device);
+  const DeviceProgram &dp = h.program(k);
+  const BoundHandle::DevParams par = h.device_params(ctx.device, k);
+  KArgs a = box_args(dp, 0, 0, true, true);
+  a.src = static_cast<const uint8_t *>(wire);
+  a.dst = static_cast<uint8_t *>(dst);
+  a.pf = par.pf;
+  a.pi = par.pi;
+  HIPCHECK(launch_box(dp.family, a, ctx.status, stream ? stream : ctx.compute));
+}
+
+double measure_h2d(int device, size_t bytes, int iters, int rounds) {
+  DeviceGuard guard(device);
+  void *h = nullptr, *d = nullptr;
+  hipStream_t s;
+  hipEvent_t e0, e1;
+  HIPCHECK(hipHostMalloc(&h, bytes, hipHostMallocDefault));
+  HIPCHECK(hipMalloc(&d, bytes));
+  std::memset(h, 1, bytes);
+  HIPCHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  HIPCHECK(hipEventCreate(&e0));
+  HIPCHECK(hipEventCreate(&e1));
+  for (int i = 0; i < 3; ++i)
+    HIPCHECK(hipMemcpyAsync(d, h, bytes, hipMemcpyHostToDevice, s));
+  HIPCHECK(hipStreamSynchronize(s));
+  double best = 0.0;
+  for (int r = 0; r < rounds; ++r) {
+    HIPCHECK(hipEventRecord(e0, s));
+    for (int i = 0; i < iters; ++i)
+      HIPCHECK(hipMemcpyAsync(d, h, bytes, hipMemcpyHostToDevice, s));
+    HIPCHECK(hipEventRecord(e1, s));
+    HIPCHECK(hipEventSynchronize(e1));
+    float ms = 0.0f;
+    HIPCHECK(hipEventElapsedTime(&ms, e0, e1));
+    best = std::max(best, static_cast<double>(bytes) * iters / (ms * 1e-3) / 1e9);
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  (void)hipStreamDestroy(s);
+  (void)hipFree(d);
+  (void)hipHostFree(h);
+  return best;
+}
+
+} // namespace relx

@@ -1,0 +1,125 @@
+// runtime.h - internal declarations shared by program.cpp, runtime.cpp,
+// staging.cpp and capi.cpp.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <condition_variable>
+#include <cstdint>
+#include <functional>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "plan.h"
+#include "program.h"
+
+namespace relx {
+
+// One value stage as host scalars (reference StageArithmetic,
+// libreloc/include/reloc/TypedExecute.h:52-68).
+struct HostStage {
+  uint8_t op = 0;
+  uint32_t in_width = 0, out_width = 0;
+  std::vector<float> scale, inv; // inv = fl32(1/scale) for quantize
+  std::vector<int32_t> zero_point{0};
+  uint8_t mode = kChanNone;
+  int dim = 0;
+  int64_t len = 1;
+  std::vector<ChanToken> tokens; // kChanExpr, symbols resolved
+};
+
+struct Prepared {
+  std::vector<HostStage> stages;
+  std::vector<int64_t> res_strides;
+};
+
+struct DeviceProgram {
+  int family = kFamGeneric;
+  const char *kernel = "generic";
+  uint32_t boundary = 0;
+  KArgs base;
+  int64_t wire_elems = 0, wire_bytes = 0, dst_elems = 0;
+  int chunk_axis = -1;
+  int64_t chunk_stride = 0, chunk_align = 1;
+  std::vector<float> pf;
+  std::vector<int32_t> pi;
+};
+
+void prepare_stages(const Bound &b, Prepared &p);
+bool fill_at(const Bound &b, const Prepared &p, uint32_t to, uint64_t &bits);
+uint64_t host_apply(const HostStage &s, uint64_t x, int64_t c);
+std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, uint32_t k);
+KArgs box_args(const DeviceProgram &dp, int64_t v0, int64_t v1, bool first, bool last);
+hipError_t launch_box(int family, const KArgs &a, int32_t *status, hipStream_t s);
+
+// ------------------------------------------------------------ workers
+
+// Persistent worker threads; parallel_for splits [0, n) into contiguous
+// ranges (no smaller than `grain`), the calling thread runs one of them.
+class Workers {
+public:
+  explicit Workers(unsigned threads);
+  ~Workers();
+  unsigned size() const { return static_cast<unsigned>(threads_.size()) + 1; }
+  void parallel_for(int64_t n, int64_t grain, const std::function<void(int64_t, int64_t)> &fn);
+
+private:
+  void loop(unsigned id);
+  std::vector<std::thread> threads_;
+  std::mutex mu_;
+  std::condition_variable go_, done_;
+  const std::function<void(int64_t, int64_t)> *fn_ = nullptr;
+  std::vector<std::pair<int64_t, int64_t>> ranges_;
+  uint64_t generation_ = 0;
+  unsigned pending_ = 0;
+  bool stop_ = false;
+};
+
+// Host staging transform: source elements [e0, e1) at boundary 0 -> wire
+// elements at boundary `k` (leading per-tensor stages applied elementwise).
+void host_transform(const Prepared &p, uint32_t k, uint32_t src_width, const void *src, void *dst,
+                    int64_t e0, int64_t e1);
+
+// ------------------------------------------------------------ handles
+
+struct BoundHandle {
+  std::unique_ptr<Bound> bound;
+  Prepared prep;
+  std::mutex mu;
+  std::map<uint32_t, std::unique_ptr<DeviceProgram>> programs; // by wire boundary
+  struct DevParams {
+    float *pf = nullptr;
+    int32_t *pi = nullptr;
+  };
+  std::map<std::pair<int, uint32_t>, DevParams> params; // (device, boundary)
+  const DeviceProgram &program(uint32_t k);
+  DevParams device_params(int device, uint32_t k);
+  ~BoundHandle();
+};
+
+struct Context {
+  int device = 0;
+  hipStream_t copy = nullptr, compute = nullptr;
+  std::vector<void *> slots;
+  size_t slot_bytes = 0;
+  std::vector<hipEvent_t> slot_ev;
+  std::vector<hipEvent_t> chunk_ev;
+  hipEvent_t start_ev = nullptr, done_ev = nullptr;
+  uint8_t *wire = nullptr;
+  size_t wire_cap = 0;
+  int32_t *status = nullptr;
+  std::unique_ptr<Workers> workers;
+  unsigned worker_threads = 0;
+  int64_t max_retained = 0;
+  std::mutex mu;
+  int64_t calls = 0, failures = 0;
+  bool quarantined = false;
+  bool closed = false;
+};
+
+} // namespace relx

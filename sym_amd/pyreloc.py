@@ -1,0 +1,297 @@
+"""Python surface over librelx, mirroring the reference's `pyreloc` module
+(libreloc/python/PyReloc.cpp:596-987, PyDispatch.cpp:517-901,
+PyTransfer.cpp:312-461) for the H2D plan-execution path.
+
+Names and argument meaning follow the reference: `wire_version`,
+`load_plan`, `load_typed_plan`, `bind`, `bind_typed`, and errors raised as
+`DecodeError`, `BindError` or `TransferError("<code>: <detail>")`. Buffers
+cross as (pointer, nbytes) pairs; ctypes releases the GIL during each call.
+"""
+import ctypes
+
+from . import _native as N
+from ._native import RelxError
+
+DTYPE_KINDS = {
+    "float32": (0, 32), "float16": (0, 16), "float64": (0, 64), "bfloat16": (1, 16),
+    "int8": (2, 8), "int16": (2, 16), "int32": (2, 32), "int64": (2, 64), "uint8": (2, 8),
+}
+
+
+class DecodeError(ValueError):
+    def __init__(self, message, offset=-1):
+        super().__init__(message)
+        self.offset = offset
+
+
+class BindError(ValueError):
+    pass
+
+
+class TransferError(RuntimeError):
+    def __init__(self, code, detail, completion="not_launched"):
+        super().__init__("%s: %s" % (code, detail))
+        self.code = code
+        self.detail = detail
+        self.completion = completion
+
+
+_BIND_CODES = {"bind_error", "unsupported_stage", "invalid_parameter", "unsupported_layout",
+               "pads_not_settled", "fill_crosses_channel_stage", "mixed_fills_unsupported",
+               "fill_mismatch", "invalid_boundary"}
+
+
+def _raise(err):
+    code = err.code.decode(errors="replace")
+    msg = err.message.decode(errors="replace")
+    if code == "decode_error":
+        raise DecodeError("%s (at byte %d)" % (msg, err.offset), err.offset)
+    if code in _BIND_CODES:
+        raise BindError("%s: %s" % (code, msg) if code != "bind_error" else msg)
+    raise TransferError(code, msg, {0: "not_launched", 1: "complete", 2: "unknown"}.get(
+        err.completion, "unknown"))
+
+
+def version():
+    return N.lib().relx_version().decode()
+
+
+def wire_version(blob):
+    """Wire version of a plan blob (bytes 4..8), or None if it is not a plan."""
+    blob = bytes(blob)
+    v = N.lib().relx_wire_version(blob, len(blob))
+    return None if v < 0 else v
+
+
+class Plan:
+    """A decoded, immutable plan (v0 layout or v1 typed)."""
+
+    def __init__(self, blob):
+        self.blob = bytes(blob)
+        err = N.relx_err()
+        h = ctypes.c_void_p()
+        if N.lib().relx_plan_load(self.blob, len(self.blob), ctypes.byref(h), ctypes.byref(err)):
+            _raise(err)
+        self._h = h
+
+    @property
+    def typed(self):
+        return bool(N.lib().relx_plan_is_typed(self._h))
+
+    @property
+    def symbols(self):
+        L = N.lib()
+        return [L.relx_plan_symbol(self._h, i).decode() for i in range(L.relx_plan_symbol_count(self._h))]
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            N.lib().relx_plan_free(h)
+            self._h = None
+
+
+def load_plan(blob):
+    """Decode a layout (v0) plan; a v1 blob is rejected like the reference's
+    decodePlan does (unsupported wire format version at byte 4)."""
+    if wire_version(blob) not in (0, None):
+        raise DecodeError("unsupported wire format version (at byte 4)", 4)
+    return Plan(blob)
+
+
+def load_typed_plan(blob):
+    """Decode a typed (v1) plan; a v0 blob is rejected at byte 4."""
+    if wire_version(blob) not in (1, None):
+        raise DecodeError("unsupported wire format version (at byte 4)", 4)
+    return Plan(blob)
+
+
+class Bound:
+    """A bound plan with its prepared device program."""
+
+    def __init__(self, plan, symbols, parameters=None):
+        self.plan = plan
+        names = list(symbols)
+        n = len(names)
+        sn = (ctypes.c_char_p * max(1, n))(*[s.encode() for s in names])
+        sv = (ctypes.c_int64 * max(1, n))(*[int(symbols[s]) for s in names])
+        params = parameters or {}
+        keep = []
+        arr = (N.relx_param * max(1, len(params)))()
+        for i, (name, value) in enumerate(params.items()):
+            dtype, extents, data = value
+            kind, bits = DTYPE_KINDS[dtype]
+            data = bytes(data)
+            buf = ctypes.create_string_buffer(data, len(data))
+            keep += [buf, name.encode()]
+            arr[i] = N.relx_param(keep[-1], kind, bits, len(extents),
+                                  int(extents[0]) if extents else 1,
+                                  ctypes.cast(buf, ctypes.c_void_p), len(data))
+        err = N.relx_err()
+        h = ctypes.c_void_p()
+        if N.lib().relx_bind(plan._h, sn, sv, n, arr, len(params), ctypes.byref(h), ctypes.byref(err)):
+            _raise(err)
+        self._h = h
+        info = N.relx_bound_info()
+        N.lib().relx_bound_query(h, ctypes.byref(info))
+        self.info = info
+
+    @property
+    def extents(self):
+        return list(self.info.extents[:self.info.rank])
+
+    @property
+    def src_strides(self):
+        return list(self.info.src_strides[:self.info.rank])
+
+    @property
+    def dst_strides(self):
+        return list(self.info.dst_strides[:self.info.rank])
+
+    @property
+    def element_size(self):
+        return self.info.element_size
+
+    @property
+    def total_bytes(self):
+        return self.info.total_bytes
+
+    @property
+    def source_bytes(self):
+        return self.info.source_bytes
+
+    @property
+    def destination_bytes(self):
+        return self.info.destination_bytes
+
+    @property
+    def parameter_bytes(self):
+        return self.info.parameter_bytes
+
+    @property
+    def stage_count(self):
+        return self.info.stages
+
+    @property
+    def kernel(self):
+        return self.info.kernel.decode()
+
+    def bytes_at(self, boundary):
+        return self.info.bytes_at[boundary]
+
+    def footprints(self):
+        return [self.info.bytes_at[k] for k in range(self.info.stages + 1)]
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            N.lib().relx_bound_free(h)
+            self._h = None
+
+
+def bind(plan, symbols):
+    """bind (Bind.cpp:176-384) for a layout plan."""
+    return Bound(plan, symbols)
+
+
+def bind_typed(plan, symbols, parameters):
+    """bindTyped (Bind.cpp:494-699): parameters are {name: (dtype, extents,
+    little-endian bytes)} exactly as the reference's pyreloc.bind_typed."""
+    return Bound(plan, symbols, parameters)
+
+
+def _options(n_buffers=0, chunk_bytes=0, host_stages=-1, gather_threads=0, source_pinned=-1,
+             caller_stream=0, no_wait=False):
+    return N.relx_options(int(n_buffers), int(chunk_bytes), int(host_stages), int(gather_threads),
+                          int(source_pinned), int(caller_stream or 0), 1 if no_wait else 0)
+
+
+class Context:
+    """A retained per-device execution context (streams, pinned ring, device
+    wire scratch): the role of the reference's TransferResources /
+    dispatch::Resources owners."""
+
+    def __init__(self, device=0, max_retained_bytes=0):
+        err = N.relx_err()
+        h = ctypes.c_void_p()
+        if N.lib().relx_ctx_create(int(device), int(max_retained_bytes), ctypes.byref(h),
+                                   ctypes.byref(err)):
+            _raise(err)
+        self._h = h
+        self.device = device
+
+    def execute_h2d(self, bound, src_ptr, src_nbytes, dst_ptr, dst_nbytes, **options):
+        """Run one bound plan host -> device; returns the report dict."""
+        rep = N.relx_report()
+        err = N.relx_err()
+        opt = _options(**options)
+        if N.lib().relx_execute_h2d(self._h, bound._h, src_ptr, src_nbytes, dst_ptr, dst_nbytes,
+                                    ctypes.byref(opt), ctypes.byref(rep), ctypes.byref(err)):
+            _raise(err)
+        return rep.as_dict()
+
+    def execute_group_h2d(self, bounds, srcs, dsts, **options):
+        """srcs/dsts: lists of (pointer, nbytes). Returns (reports, total)."""
+        n = len(bounds)
+        bh = (ctypes.c_void_p * n)(*[b._h.value for b in bounds])
+        sp = (ctypes.c_void_p * n)(*[s[0] for s in srcs])
+        sb = (ctypes.c_size_t * n)(*[s[1] for s in srcs])
+        dp = (ctypes.c_void_p * n)(*[d[0] for d in dsts])
+        db = (ctypes.c_size_t * n)(*[d[1] for d in dsts])
+        reps = (N.relx_report * n)()
+        total = N.relx_report()
+        err = N.relx_err()
+        opt = _options(**options)
+        if N.lib().relx_execute_group_h2d(self._h, n, bh, sp, sb, dp, db, ctypes.byref(opt), reps,
+                                          ctypes.byref(total), ctypes.byref(err)):
+            _raise(err)
+        return [r.as_dict() for r in reps], total.as_dict()
+
+    def relayout_device(self, bound, wire_ptr, dst_ptr, wire_boundary=0, stream=0):
+        """Launch the device relayout on a device-resident wire (async)."""
+        err = N.relx_err()
+        if N.lib().relx_relayout_device(self._h, bound._h, int(wire_boundary), wire_ptr, dst_ptr,
+                                        int(stream or 0), ctypes.byref(err)):
+            _raise(err)
+
+    def synchronize(self):
+        err = N.relx_err()
+        if N.lib().relx_ctx_synchronize(self._h, ctypes.byref(err)):
+            _raise(err)
+
+    def stats(self):
+        s = N.relx_ctx_stats()
+        N.lib().relx_ctx_stats_get(self._h, ctypes.byref(s))
+        return {f: getattr(s, f) for f, _ in s._fields_}
+
+    def close(self):
+        h = getattr(self, "_h", None)
+        if h:
+            err = N.relx_err()
+            self._h = None
+            if N.lib().relx_ctx_close(h, ctypes.byref(err)):
+                _raise(err)
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+        return False
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def host_stage(bound, host_stages, src_ptr, wire_ptr, threads=8):
+    err = N.relx_err()
+    if N.lib().relx_host_stage(bound._h, int(host_stages), src_ptr, wire_ptr, int(threads),
+                               ctypes.byref(err)):
+        _raise(err)
+
+
+def measure_h2d(device=0, nbytes=256 << 20, iters=20, rounds=3):
+    """Pinned H2D ceiling in GB/s (bench/rtrack/multigpu_h2d.cu:46-91 restated)."""
+    return N.lib().relx_measure_h2d(int(device), int(nbytes), int(iters), int(rounds))
