@@ -109,6 +109,12 @@ def lib():
     """The loaded library; raises NativeLibraryMissing when it is not built."""
     global _lib
     if _lib is None:
+        # One HIP runtime per process: when torch is present its bundled
+        # libamdhip64.so.7 is loaded first and satisfies librelx's dependency.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         if not os.path.exists(LIB_PATH):
             raise NativeLibraryMissing(
                 "librelx.so is not built (%s); run `python -m sym_amd.build`" % LIB_PATH)

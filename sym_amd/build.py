@@ -21,7 +21,7 @@ ARCH = os.environ.get("RELX_OFFLOAD_ARCH", "gfx950")
 # denormals. Packed-FP32 instructions are disabled for all HIP code.
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "-Wall",
           "-Wno-unused-command-line-argument"]
-DEVICE = ["--offload-arch=" + ARCH, "-fno-gpu-flush-denormals-to-zero",
+DEVICE = ["--offload-arch=" + ARCH, "-mcode-object-version=5", "-fno-gpu-flush-denormals-to-zero",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 SOURCES = ["plan.cpp", "program.cpp", "runtime.cpp", "capi.cpp", "kernels.hip"]
 

@@ -352,10 +352,25 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
   }
   dp->wire_elems = wire_elems;
   dp->wire_bytes = wire_elems * win;
-  int64_t total = 1;
-  for (int64_t e : pext)
-    total *= e;
-  dp->dst_elems = total;
+  // Bounds proofs the kernels rely on: every source offset the valid box
+  // reaches lies inside the wire, every destination offset inside the result.
+  int64_t src_span = 0, dst_span = 0, total = 1;
+  for (int i = 0; i < r; ++i) {
+    if (a.ss[i] < 0 || a.ds[i] < 0)
+      fail("unsupported_layout", "negative stride");
+    int64_t t;
+    if (__builtin_mul_overflow(a.vext[i] - 1, a.ss[i], &t) ||
+        __builtin_add_overflow(src_span, t, &src_span) ||
+        __builtin_mul_overflow(a.pext[i] - 1, a.ds[i], &t) ||
+        __builtin_add_overflow(dst_span, t, &dst_span) ||
+        __builtin_mul_overflow(total, a.pext[i], &total))
+      fail("integer_overflow", "layout offsets overflow");
+  }
+  if (src_span >= wire_elems)
+    fail("unsupported_layout", "the plan reads beyond its source (span " +
+                                   std::to_string(src_span + 1) + " > " +
+                                   std::to_string(wire_elems) + " elements)");
+  dp->dst_elems = std::max(total, dst_span + 1);
 
   // ------------------------------------------------------ family choice
   const bool widths_ok = (win == 1 || win == 2 || win == 4) && (wout == 1 || wout == 2 || wout == 4);

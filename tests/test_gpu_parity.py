@@ -1,0 +1,300 @@
+"""HIP path parity: librelx on an MI355X against the pinned oracle.
+
+Bit-exact for every config (the reference contract is bit-exact for dequant
+too, inside the <= 1 ULP allowance). Small cases compare whole outputs with
+the oracle / numpy replays; full-size configs compare whole outputs where
+numpy finishes in seconds and otherwise every element of randomly sampled
+rows, plus size-independent checks (checksums of the whole buffer against
+the sampled oracle where exact).
+"""
+import hashlib
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import relx_oracle as O
+from sym_amd import encoder as EN
+from sym_amd import pyreloc as P
+from sym_amd import workloads as W
+from tests import golden_io as G
+from tests.test_encoder import small_cases
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+
+def say(*a):
+    print("[gpu-case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    assert torch.cuda.is_available(), "a GPU test needs the MI355X"
+    c = P.Context(0)
+    yield c
+    c.close()
+
+
+def run_h2d(ctx, blob, syms, params, src, name="", **opts):
+    plan = P.Plan(blob)
+    b = P.Bound(plan, syms, params if plan.typed else None)
+    nbytes = b.destination_bytes if plan.typed else b.total_bytes
+    out = torch.empty(max(1, nbytes), dtype=torch.uint8, device="cuda")
+    src = np.ascontiguousarray(src)
+    say(name, "kernel=%s" % b.kernel, "src=%d B dst=%d B" % (src.nbytes, nbytes), opts)
+    rep = ctx.execute_h2d(b, src.ctypes.data, src.nbytes, out.data_ptr(), nbytes, **opts)
+    torch.cuda.synchronize()
+    return out[:nbytes].cpu().numpy(), rep, b
+
+
+def f16_bits(x32):
+    return O.narrow_f32_f16_bits(np.ascontiguousarray(x32, np.float32).view(np.uint32))
+
+
+# ------------------------------------------------------------- corpus
+
+TYPED = G.typed_fixtures()
+
+
+@pytest.mark.parametrize("meta,blob", TYPED, ids=[m["name"] for m, _ in TYPED])
+@pytest.mark.parametrize("host_stages", [0, -1])
+def test_typed_corpus(ctx, meta, blob, host_stages):
+    for b in meta["bindings"]:
+        src = G.bits_array(b["source"])
+        out, rep, _ = run_h2d(ctx, blob, b["symbols"], G.fixture_params(meta), src,
+                              meta["name"], host_stages=host_stages)
+        exp = G.bits_array(b["expected"])
+        assert np.array_equal(out.view(exp.dtype), exp), (meta["name"], b["symbols"])
+        assert hashlib.sha256(out.tobytes()).hexdigest() == b["expected"]["sha256"]
+        assert rep["destination_bytes"] == b["footprints"]["h2d"]["destination_bytes"]
+
+
+LAYOUT = G.layout_fixtures()
+NPD = {"f32": np.float32, "f16": np.float16, "i8": np.int8}
+
+
+def _eval_dim(d, binding):
+    if isinstance(d, int):
+        return d
+    p = d.split()
+    return binding[p[0]] // int(p[2]) if len(p) == 3 else binding[d]
+
+
+@pytest.mark.parametrize("meta,blob", LAYOUT, ids=[m["name"] for m, _ in LAYOUT])
+def test_layout_corpus(ctx, meta, blob, rng):
+    bindings = [{}] if not meta["symbols"] else \
+        [{n: c["multiple_of"] * f for n, c in meta["symbols"].items()} for f in (1, 2, 3)]
+    for binding in bindings:
+        shape = [_eval_dim(d, binding) for d in meta["src_shape"]]
+        dt = NPD[meta["dtype"]]
+        src = rng.integers(0, 256, int(np.prod(shape)) * np.dtype(dt).itemsize,
+                           dtype=np.uint8).view(dt).reshape(shape)
+        out, _, b = run_h2d(ctx, blob, binding, None, src, meta["name"])
+        want = O.execute_layout(O.bind(O.decode_plan(blob), binding), src.tobytes())
+        assert out.tobytes() == want, (meta["name"], binding)
+
+
+# ---------------------------------------------------------- configs small
+
+def test_configs_small(ctx, rng):
+    for name, plan, syms, params, src, expected in small_cases(rng):
+        for hs in (0, -1):
+            out, rep, _ = run_h2d(ctx, plan.blob, syms, params, src, name, host_stages=hs)
+            assert out.tobytes() == expected, (name, hs)
+
+
+# ------------------------------------------------------------ C1 (all N)
+
+@pytest.mark.parametrize("n", W.C1_SIZES)
+def test_c1_readme_plan(ctx, n):
+    x = W.c1_input(n)
+    out, rep, b = run_h2d(ctx, W.c1_plan().blob, {"s0": n}, None, x, "c1 N=%d" % n)
+    assert out.view(np.float32).reshape(64, n // 64).tobytes() == x.reshape(n // 64, 64).T.tobytes()
+    assert rep["wire_bytes"] == 4 * n and rep["destination_bytes"] == 4 * n
+
+
+def test_c1_one_plan_rebinds(ctx):
+    plan = P.Plan(W.c1_plan().blob)
+    for n in (128, 192, 256, 4096, 64 * 1000):
+        b = P.Bound(plan, {"s0": n})
+        x = W.c1_input(n, seed=n)
+        out = torch.empty(4 * n, dtype=torch.uint8, device="cuda")
+        say("c1 rebind N=%d" % n)
+        ctx.execute_h2d(b, x.ctypes.data, x.nbytes, out.data_ptr(), 4 * n)
+        assert out.cpu().numpy().tobytes() == x.reshape(n // 64, 64).T.tobytes()
+    with pytest.raises(P.BindError, match="divisibility"):
+        P.Bound(plan, {"s0": 100})
+
+
+# ------------------------------------------------------------------ C2
+
+@pytest.mark.parametrize("host_stages", [0, 1])
+def test_c2_image_batch_full(ctx, host_stages):
+    x = W.c2_input()
+    out, rep, b = run_h2d(ctx, W.c2_plan().blob, {}, None, x, "c2", host_stages=host_stages)
+    want = f16_bits(np.pad(x, [(0, 0), (0, 1), (0, 0), (0, 0)]).transpose(0, 2, 3, 1))
+    assert np.array_equal(out.view(np.uint16).reshape(want.shape), want)
+    assert b.kernel == "interleave"
+    assert rep["wire_bytes"] == (19267584 if host_stages == 0 else 9633792)
+    assert rep["destination_bytes"] == 12845056
+
+
+def test_c2_pinned_source_direct_dma(ctx):
+    x = torch.from_numpy(W.c2_input()).pin_memory()
+    plan = P.Plan(W.c2_plan().blob)
+    b = P.Bound(plan, {})
+    out = torch.empty(b.destination_bytes, dtype=torch.uint8, device="cuda")
+    say("c2 pinned direct")
+    rep = ctx.execute_h2d(b, x.data_ptr(), x.numel() * 4, out.data_ptr(), out.numel())
+    assert rep["direct_dma"] == 1 and rep["wire_boundary"] == 0
+    want = f16_bits(np.pad(x.numpy(), [(0, 0), (0, 1), (0, 0), (0, 0)]).transpose(0, 2, 3, 1))
+    assert np.array_equal(out.cpu().numpy().view(np.uint16).reshape(want.shape), want)
+
+
+# ------------------------------------------------------------------ C3
+
+@pytest.mark.parametrize("opts", [{}, {"chunk_bytes": 1 << 20, "n_buffers": 2}, {"source_pinned": 0, "gather_threads": 1}])
+def test_c3_weight_full(ctx, opts):
+    q, s = W.c3_input()
+    out, rep, b = run_h2d(ctx, W.c3_plan().blob, {"s0": 4096, "s1": 11008}, W.param("scale", s), q,
+                          "c3", **opts)
+    assert b.kernel == "transpose"
+    want = f16_bits(O.dequantize_s8_f32(q, s[None, :], np.int32(0)).T)
+    assert np.array_equal(out.view(np.uint16).reshape(11008, 4096), want)
+    assert rep["wire_bytes"] == 45088768 and rep["destination_bytes"] == 90177536
+    if "chunk_bytes" in opts:
+        assert rep["chunks"] > 10
+
+
+# ------------------------------------------------------------------ C4
+
+def _c4_expected_rows(q, s, rows):
+    return f16_bits(O.dequantize_s8_f32(q[rows], s[rows, None], np.int32(0)))
+
+
+def test_c4_expert_group(ctx, rng):
+    """Two experts (6 matrices) as one grouped transfer at full size; every
+    element of 64 sampled rows per matrix checked, plus full-buffer equality
+    for the down projection (4096 x 14336)."""
+    pool = W.c4_pool(experts=2)
+    plan = P.Plan(W.c4_plan().blob)
+    bounds, srcs, dsts, outs = [], [], [], []
+    for e in range(2):
+        for q, s in pool[e]:
+            b = P.Bound(plan, {"s0": q.shape[0], "s1": q.shape[1]}, W.param("scale", s))
+            out = torch.empty(b.destination_bytes, dtype=torch.uint8, device="cuda")
+            bounds.append(b)
+            srcs.append((q.ctypes.data, q.nbytes))
+            dsts.append((out.data_ptr(), out.numel()))
+            outs.append(out)
+    say("c4 group of", len(bounds))
+    reps, total = ctx.execute_group_h2d(bounds, srcs, dsts)
+    torch.cuda.synchronize()
+    assert total["wire_bytes"] == 352321536 and total["destination_bytes"] == 704643072
+    i = 0
+    for e in range(2):
+        for q, s in pool[e]:
+            got = outs[i].cpu().numpy().view(np.uint16).reshape(q.shape)
+            rows = np.sort(rng.choice(q.shape[0], 64, replace=False))
+            assert np.array_equal(got[rows], _c4_expected_rows(q, s, rows)), (e, q.shape)
+            if q.shape[0] == 4096:
+                assert np.array_equal(got, _c4_expected_rows(q, s, np.arange(4096)))
+            i += 1
+
+
+def test_c4_device_relayout_matches_h2d(ctx):
+    """relx_relayout_device on a device-resident wire equals the H2D path."""
+    rng = np.random.default_rng(7)
+    q = W.int8_weight(1024, 4096, rng)
+    s = W.scales(1024, rng)
+    plan = P.Plan(W.c4_plan().blob)
+    b = P.Bound(plan, {"s0": 1024, "s1": 4096}, W.param("scale", s))
+    wire = torch.from_numpy(q).cuda()
+    out = torch.empty(b.destination_bytes, dtype=torch.uint8, device="cuda")
+    say("c4 device relayout")
+    ctx.relayout_device(b, wire.data_ptr(), out.data_ptr())
+    ctx.synchronize()
+    want = _c4_expected_rows(q, s, np.arange(1024))
+    assert np.array_equal(out.cpu().numpy().view(np.uint16).reshape(q.shape), want)
+
+
+# ------------------------------------------------------------------ C5
+
+def _c5_expected(x, s, b_idx=None):
+    inv = (np.float32(1) / s).astype(np.float32)
+    sub = x if b_idx is None else x[b_idx]
+    wid = np.ascontiguousarray(sub.transpose(0, 2, 1, 3)).astype(np.float32)
+    return O.quantize_f32_s8(wid, inv[None, :, None, None])
+
+
+@pytest.mark.parametrize("B,S", W.C5_SHAPES)
+def test_c5_activation_quant(ctx, B, S):
+    """One plan bound per (B, S). Whole-output check up to E = 32M elements;
+    beyond that every element of two sampled batch entries."""
+    plan = W.c5_plan()
+    x, s = W.c5_input(B, S, seed=B * 10007 + S)
+    out, rep, b = run_h2d(ctx, plan.blob, {"B": B, "S": S}, W.param("scale", s), x,
+                          "c5 B=%d S=%d" % (B, S))
+    E = B * S * 4096
+    assert rep["wire_bytes"] == 2 * E and rep["destination_bytes"] == E
+    got = out.view(np.int8).reshape(B, 32, S, 128)
+    if E <= 33554432:
+        assert np.array_equal(got, _c5_expected(x, s))
+    else:
+        picks = sorted({0, B - 1, B // 2})
+        assert np.array_equal(got[picks], _c5_expected(x, s, picks))
+
+
+# -------------------------------------------------------- value sweeps
+
+def _cast_plan(src_dtype, dst_dtype, n):
+    return EN.encode([n], src_dtype, [EN.Cast(dst_dtype)]).blob
+
+
+def test_f16_widening_exhaustive(ctx):
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    out, _, _ = run_h2d(ctx, _cast_plan("float16", "float32", 65536), {}, {}, h, "widen all f16")
+    assert np.array_equal(out.view(np.uint32), O.widen_f16_f32_bits(h))  # NaN payloads included
+
+
+def test_f32_narrowing_sweep(ctx):
+    rng = np.random.default_rng(11)
+    e = np.arange(256, dtype=np.uint32) << 23
+    edges = np.concatenate([e | m for m in (0, 1, 0x1000, 0x0fff, 0x1fff, 0x2000, 0x3000,
+                                            0x7fffff, 0x400000, 0x7fe000, 0x7ff000)])
+    bits = np.concatenate([rng.integers(0, 2**32, 1 << 24, dtype=np.uint64).astype(np.uint32),
+                           edges, edges | 0x80000000]).astype(np.uint32)
+    n = bits.size
+    out, _, _ = run_h2d(ctx, _cast_plan("float32", "float16", n), {}, {}, bits, "narrow sweep")
+    assert np.array_equal(out.view(np.uint16), O.narrow_f32_f16_bits(bits))  # NaNs included
+    out, _, _ = run_h2d(ctx, _cast_plan("float32", "bfloat16", n), {}, {}, bits, "bf16 sweep")
+    assert np.array_equal(out.view(np.uint16), O.narrow_f32_bf16_bits(bits))
+
+
+def test_quantize_dequantize_sweep(ctx):
+    rng = np.random.default_rng(12)
+    bits = np.concatenate([rng.integers(0, 2**32, 1 << 22, dtype=np.uint64).astype(np.uint32),
+                           np.array([0x7fc00000, 0xffc00000, 0x7f800000, 0xff800000, 0x80000000,
+                                     0x00000001, 0x3f000000, 0xbfc00000], np.uint32)])
+    x = bits.view(np.float32)
+    for scale in (0.3, 1.0, 1e-3, 2.0 ** -130):
+        sc = EN.InlineParam((scale,))
+        plan = EN.encode([x.size], "float32", [EN.Quantize(sc)]).blob
+        out, _, _ = run_h2d(ctx, plan, {}, {}, x, "quant scale=%g" % scale)
+        inv = (np.float32(1) / np.float32(scale)).astype(np.float32)
+        assert np.array_equal(out.view(np.int8), O.quantize_f32_s8(x, inv))
+    q = np.arange(-128, 128, dtype=np.int8).repeat(4096)
+    for scale, zp in ((0.3, 0), (0.3, 127), (2.0 ** -140, -128), (1e30, 5)):
+        plan = EN.encode([q.size], "int8", [EN.Dequantize(EN.InlineParam((scale,)),
+                                                          EN.InlineParam((zp,), "int32"))]).blob
+        out, _, _ = run_h2d(ctx, plan, {}, {}, q, "dequant scale=%g zp=%d" % (scale, zp))
+        want = O.dequantize_s8_f32(q, np.float32(scale), np.int32(zp))
+        assert np.array_equal(out.view(np.uint32), want.view(np.uint32))
+
+
+def test_context_stats_and_reuse(ctx):
+    st = ctx.stats()
+    assert st["calls"] > 0 and st["failures"] == 0 and not st["quarantined"]
+    assert st["device_bytes"] > 0
