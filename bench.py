@@ -1,0 +1,371 @@
+#!/usr/bin/env python3
+"""Benchmark of the libreloc plan-execution hot path on one MI355X.
+
+Headline (C2 image-batch relayout): fp32 NCHW
+[32,3,224,224] -> pad C 3->4 -> NHWC -> fp16.
+
+* `value`: output GB/s of the fused device relayout with the wire already
+  resident in HBM (K back-to-back launches over rotating buffer sets that
+  together exceed the 256 MB Infinity Cache).
+* `roofline`: the dominant kernel's algorithmic bytes per launch over its
+  average launch duration (per-launch HIP events on the launch stream),
+  against 8 TB/s; `traffic` from the committed rocprofv3 PMC summary.
+* `e2e`: the PCIe-inclusive rate (pageable and pinned host source) against
+  the measured pinned H2D ceiling -- reported, never `value`.
+* `cpu_baseline`: the reference's own compiled CPU executor (oracle/_ref,
+  typed::executeHost) on this host, on a bounded sample.
+
+`--report` prints one JSON line per config (C1..C5) instead.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "effective GB/s (output bytes/s) fused relayout+H2D; % of PCIe and HBM roofline"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--e2e-samples", type=int, default=40)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--report", action="store_true", help="one JSON line per config")
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5")
+    return ap.parse_args()
+
+
+# ------------------------------------------------------------------ setup
+
+def torch_mod():
+    import torch
+    if not torch.cuda.is_available():
+        sys.exit("bench.py needs a GPU (torch.cuda.is_available() is False)")
+    return torch
+
+
+class Case:
+    """One workload: a bound plan plus host inputs for it."""
+
+    def __init__(self, name, workload, blob, symbols, params, src, extra=None):
+        from sym_amd import pyreloc as P
+        self.name, self.workload = name, workload
+        self.plan = P.Plan(blob)
+        self.bound = P.Bound(self.plan, symbols, params if self.plan.typed else None)
+        self.blob, self.symbols, self.params = blob, symbols, params
+        self.src = np.ascontiguousarray(src)
+        self.extra = extra or {}
+        b = self.bound
+        self.out_bytes = b.destination_bytes if self.plan.typed else b.total_bytes
+        self.wire_bytes = self.src.nbytes  # boundary-0 wire (device programs start there)
+        self.kernel = b.kernel
+
+
+def make_case(name):
+    from sym_amd import workloads as W
+    if name == "c1":
+        n = 16777216
+        return Case(name, "C1 README plan f32[N=16777216] -> [N/64,64] -> transpose [64,N/64]",
+                    W.c1_plan().blob, {"s0": n}, None, W.c1_input(n))
+    if name == "c2":
+        return Case(name, "C2 image batch f32 NCHW [32,3,224,224] -> pad C 3->4 -> NHWC -> f16",
+                    W.c2_plan().blob, {}, {}, W.c2_input())
+    if name == "c3":
+        q, s = W.c3_input()
+        return Case(name, "C3 int8 weight [4096,11008] -> dequant(scale[11008]) -> f16 -> [11008,4096]",
+                    W.c3_plan().blob, {"s0": 4096, "s1": 11008}, W.param("scale", s), q)
+    if name.startswith("c5"):
+        b, s = (64, 4096) if name == "c5" else tuple(int(v) for v in name[3:].split("x"))
+        x, sc = W.c5_input(b, s)
+        return Case(name, "C5 f16 [%d,%d,32,128] -> [B,32,S,128] -> f32 -> int8 (per-head scale)"
+                    % (b, s), W.c5_plan().blob, {"B": b, "S": s}, W.param("scale", sc), x,
+                    {"B": b, "S": s})
+    raise ValueError(name)
+
+
+# ----------------------------------------------------------- measurements
+
+def device_rate(torch, ctx, bound, wire_bytes, out_bytes, steps, warmup, sets=None):
+    """K back-to-back device relayouts over rotating buffer sets. Returns
+    (ms_per_step over the bracketed region, mean per-launch kernel ms)."""
+    per = wire_bytes + out_bytes
+    sets = sets or max(2, min(16, int(np.ceil(600e6 / per))))
+    wires = [torch.empty(wire_bytes, dtype=torch.uint8, device="cuda") for _ in range(sets)]
+    outs = [torch.empty(out_bytes, dtype=torch.uint8, device="cuda") for _ in range(sets)]
+    for w in wires:
+        w.random_(0, 256)
+    # a dedicated (non-null) stream: the kernels and the events must share it
+    stream = torch.cuda.Stream()
+    sp = stream.cuda_stream
+    assert sp != 0
+    for i in range(warmup):
+        ctx.relayout_device(bound, wires[i % sets].data_ptr(), outs[i % sets].data_ptr(), stream=sp)
+    torch.cuda.synchronize()
+    # whole-job: K steps bracketed by synchronize
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for i in range(steps):
+        ctx.relayout_device(bound, wires[i % sets].data_ptr(), outs[i % sets].data_ptr(), stream=sp)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms_step = t0.elapsed_time(t1) / steps
+    # per-launch durations on the launch stream
+    n = min(steps, 400)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for i in range(n):
+        ev[i][0].record(stream)
+        ctx.relayout_device(bound, wires[i % sets].data_ptr(), outs[i % sets].data_ptr(), stream=sp)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    kms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
+    torch.cuda.synchronize()
+    del wires, outs
+    return ms_step, kms
+
+
+def e2e_rate(torch, ctx, case, samples, pinned, host_stages=-1):
+    out = torch.empty(case.out_bytes, dtype=torch.uint8, device="cuda")
+    if pinned:
+        src_t = torch.from_numpy(case.src.view(np.uint8).reshape(-1)).pin_memory()
+        ptr, nb = src_t.data_ptr(), src_t.numel()
+    else:
+        ptr, nb = case.src.ctypes.data, case.src.nbytes
+    for _ in range(8):  # reference protocol: 8 warmups, then samples
+        rep = ctx.execute_h2d(case.bound, ptr, nb, out.data_ptr(), case.out_bytes,
+                              host_stages=host_stages, source_pinned=1 if pinned else 0)
+    ts = []
+    for _ in range(samples):
+        t = time.perf_counter()
+        rep = ctx.execute_h2d(case.bound, ptr, nb, out.data_ptr(), case.out_bytes,
+                              host_stages=host_stages, source_pinned=1 if pinned else 0)
+        ts.append(time.perf_counter() - t)
+    p50, p95 = float(np.percentile(ts, 50)), float(np.percentile(ts, 95))
+    return p50, p95, rep
+
+
+def hbm_copy_ceiling(torch, nbytes=1 << 30, iters=20):
+    a = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    a.random_(0, 256)
+    for _ in range(3):
+        b.copy_(a)
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(iters):
+        b.copy_(a)
+    e.record()
+    torch.cuda.synchronize()
+    return 2 * nbytes * iters / (s.elapsed_time(e) * 1e-3) / 1e9
+
+
+def cpu_baseline(case, seconds, threads):
+    """The reference libreloc CPU executor (oracle/_ref) timed on this host:
+    repeated typed::executeHost / executeH2DThreaded over the config."""
+    from oracle import ref
+    if not ref.available():
+        return None
+    if case.plan.typed:
+        r = ref.TypedRef(case.blob, case.symbols, case.params, threads=threads)
+    else:
+        r = ref.LayoutRef(case.blob, case.symbols, threads=threads)
+    out = np.empty(case.out_bytes, np.uint8)
+    r.execute(case.src, out)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        r.execute(case.src, out)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and n >= 3:
+            break
+    return {"value": round(case.out_bytes * n / el / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "reference",
+            "sample": "%d x typed::executeHost of the full %s batch (%d output bytes each) in %.1f s"
+                      % (n, case.name.upper(), case.out_bytes, el)}
+
+
+def traffic_for(kernel_key):
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get(kernel_key)
+
+
+# --------------------------------------------------------------- report
+
+def one_config(torch, ctx, P, name, args, h2d_ceiling):
+    case = make_case(name)
+    ms_step, kms = device_rate(torch, ctx, case.bound, case.wire_bytes, case.out_bytes,
+                               max(50, args.steps // 10), 20)
+    alg = case.wire_bytes + case.out_bytes + case.bound.parameter_bytes
+    p50, p95, rep = e2e_rate(torch, ctx, case, max(10, args.e2e_samples // 2), pinned=False)
+    q50, q95, prep = e2e_rate(torch, ctx, case, max(10, args.e2e_samples // 2), pinned=True)
+    return {"config": name, "workload": case.workload, "kernel": case.kernel,
+            "device": {"ms_per_step": round(ms_step, 5),
+                       "output_GBps": round(case.out_bytes / ms_step / 1e6, 1),
+                       "algorithmic_bytes": alg, "achieved_GBps": round(alg / ms_step / 1e6, 1),
+                       "hbm_frac": round(alg / ms_step / 1e6 / HBM_PEAK_GBS, 4)},
+            "e2e_pageable": {"p50_ms": round(p50 * 1e3, 3), "p95_ms": round(p95 * 1e3, 3),
+                             "effective_GBps": round(case.out_bytes / p50 / 1e9, 2),
+                             "wire_bytes": rep["wire_bytes"],
+                             "pcie_frac": round(rep["wire_bytes"] / p50 / 1e9 / h2d_ceiling, 4),
+                             "implementation": rep["implementation"], "chunks": rep["chunks"]},
+            "e2e_pinned": {"p50_ms": round(q50 * 1e3, 3), "p95_ms": round(q95 * 1e3, 3),
+                           "effective_GBps": round(case.out_bytes / q50 / 1e9, 2),
+                           "wire_bytes": prep["wire_bytes"],
+                           "pcie_frac": round(prep["wire_bytes"] / q50 / 1e9 / h2d_ceiling, 4),
+                           "implementation": prep["implementation"], "chunks": prep["chunks"]}}
+
+
+def c4_report(torch, ctx, P, args, h2d_ceiling):
+    """C4: two experts (6 matrices) per step as one grouped transfer."""
+    from sym_amd import workloads as W
+    pool = W.c4_pool()
+    steps = W.c4_steps(20)
+    plan = P.Plan(W.c4_plan().blob)
+    bounds = {}
+    for e in range(8):
+        for j, (q, s) in enumerate(pool[e]):
+            bounds[(e, j)] = P.Bound(plan, {"s0": q.shape[0], "s1": q.shape[1]}, W.param("scale", s))
+    # gate, up and down hold the same element count: one output buffer per slot
+    dst = [torch.empty(bounds[(0, 0)].destination_bytes, dtype=torch.uint8, device="cuda")
+           for _ in range(6)]
+
+    def step(experts):
+        bl, sl, dl = [], [], []
+        k = 0
+        for e in experts:
+            for j in range(3):
+                q, _ = pool[e][j]
+                bl.append(bounds[(e, j)])
+                sl.append((q.ctypes.data, q.nbytes))
+                dl.append((dst[k].data_ptr(), dst[k].numel()))
+                k += 1
+        return ctx.execute_group_h2d(bl, sl, dl)
+
+    for ex in steps[:3]:
+        step(ex)
+    ts = []
+    for ex in steps:
+        t = time.perf_counter()
+        reps, total = step(ex)
+        ts.append(time.perf_counter() - t)
+    p50 = float(np.percentile(ts, 50))
+    # device-only: one matrix per launch over resident wires
+    b = bounds[(0, 0)]
+    q = pool[0][0][0]
+    ms_step, kms = device_rate(torch, ctx, b, q.nbytes, b.destination_bytes, 200, 20)
+    alg = q.nbytes + b.destination_bytes + b.parameter_bytes
+    return {"config": "c4", "workload": "C4 MoE: 2 of 8 experts x {gate,up [14336,4096], down [4096,14336]} int8 -> per-row dequant -> f16",
+            "kernel": b.kernel,
+            "device": {"matrix": "gate [14336,4096]", "ms_per_step": round(ms_step, 5),
+                       "output_GBps": round(b.destination_bytes / ms_step / 1e6, 1),
+                       "achieved_GBps": round(alg / ms_step / 1e6, 1),
+                       "hbm_frac": round(alg / ms_step / 1e6 / HBM_PEAK_GBS, 4)},
+            "e2e_pageable": {"p50_ms": round(p50 * 1e3, 3),
+                             "effective_GBps": round(total["destination_bytes"] / p50 / 1e9, 2),
+                             "wire_bytes": total["wire_bytes"],
+                             "pcie_frac": round(total["wire_bytes"] / p50 / 1e9 / h2d_ceiling, 4),
+                             "steps": len(steps)}}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        sys.exit("bench.py measures one GPU: this build runs the path on one MI355X only "
+                 "(every GPU box here has one GPU); got --gpus %d" % args.gpus)
+    torch = torch_mod()
+    from sym_amd import pyreloc as P
+    ctx = P.Context(0)
+    h2d_ceiling = P.measure_h2d(0, 256 << 20, 20, 3)
+
+    if args.report:
+        print(json.dumps({"pinned_h2d_ceiling_GBps": round(h2d_ceiling, 2),
+                          "hbm_copy_GBps": round(hbm_copy_ceiling(torch), 1)}), flush=True)
+        for name in args.configs.split(","):
+            if name == "c4":
+                print(json.dumps(c4_report(torch, ctx, P, args, h2d_ceiling)), flush=True)
+            elif name == "c1":
+                print(json.dumps(one_config(torch, ctx, P, "c1", args, h2d_ceiling)), flush=True)
+                for n in (128, 192, 256):
+                    from sym_amd import workloads as W
+                    case = Case("c1", "C1 N=%d" % n, W.c1_plan().blob, {"s0": n}, None, W.c1_input(n))
+                    p50, p95, rep = e2e_rate(torch, ctx, case, 50, pinned=False)
+                    print(json.dumps({"config": "c1", "N": n, "e2e_latency_us_p50": round(p50 * 1e6, 1),
+                                      "e2e_latency_us_p95": round(p95 * 1e6, 1)}), flush=True)
+            elif name == "c5":
+                from sym_amd import workloads as W
+                for b, s in W.C5_SHAPES:
+                    print(json.dumps(one_config(torch, ctx, P, "c5_%dx%d" % (b, s), args, h2d_ceiling)),
+                          flush=True)
+            else:
+                print(json.dumps(one_config(torch, ctx, P, name, args, h2d_ceiling)), flush=True)
+        ctx.close()
+        return
+
+    # ---------------------------------------------------- headline: C2
+    case = make_case("c2")
+    ms_step, kms = device_rate(torch, ctx, case.bound, case.wire_bytes, case.out_bytes,
+                               args.steps, args.warmup)
+    value = case.out_bytes / (ms_step * 1e-3) / 1e9
+    alg = case.wire_bytes + case.out_bytes
+    achieved = alg / (ms_step * 1e-3) / 1e9
+    p50, p95, rep = e2e_rate(torch, ctx, case, args.e2e_samples, pinned=False)
+    q50, q95, prep = e2e_rate(torch, ctx, case, args.e2e_samples, pinned=True)
+    f50, f95, frep = e2e_rate(torch, ctx, case, args.e2e_samples, pinned=False, host_stages=0)
+    cpu = None if args.no_cpu else cpu_baseline(case, args.cpu_seconds, 8)
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32->f16",
+        "data": "synthetic (seed 20260710, N(0,1) fp32)",
+        "config": {"workload": case.workload, "kernel": "interleave",
+                   "output_bytes": case.out_bytes, "wire_bytes_per_step": case.wire_bytes,
+                   "value_definition": "output bytes / step time, wire resident in HBM"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_for("c2_interleave"), "kernel_ms": round(ms_step, 5),
+                     "kernel_ms_per_launch_events": round(kms, 5),
+                     "algorithmic_bytes": alg},
+        "e2e": {"pinned_h2d_ceiling_GBps": round(h2d_ceiling, 2),
+                "pageable": {"p50_ms": round(p50 * 1e3, 3), "p95_ms": round(p95 * 1e3, 3),
+                             "effective_GBps": round(case.out_bytes / p50 / 1e9, 2),
+                             "wire_bytes": rep["wire_bytes"], "implementation": rep["implementation"],
+                             "pcie_frac": round(rep["wire_bytes"] / p50 / 1e9 / h2d_ceiling, 4)},
+                "pageable_f32_wire": {"p50_ms": round(f50 * 1e3, 3),
+                                      "effective_GBps": round(case.out_bytes / f50 / 1e9, 2),
+                                      "wire_bytes": frep["wire_bytes"],
+                                      "pcie_frac": round(frep["wire_bytes"] / f50 / 1e9 / h2d_ceiling, 4)},
+                "pinned": {"p50_ms": round(q50 * 1e3, 3), "p95_ms": round(q95 * 1e3, 3),
+                           "effective_GBps": round(case.out_bytes / q50 / 1e9, 2),
+                           "wire_bytes": prep["wire_bytes"], "implementation": prep["implementation"],
+                           "pcie_frac": round(prep["wire_bytes"] / q50 / 1e9 / h2d_ceiling, 4)}},
+        "cpu_baseline": cpu,
+    }
+    ctx.close()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -23,7 +23,8 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "
           "-Wno-unused-command-line-argument"]
 DEVICE = ["--offload-arch=" + ARCH, "-mcode-object-version=5", "-fno-gpu-flush-denormals-to-zero",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
-SOURCES = ["plan.cpp", "program.cpp", "runtime.cpp", "capi.cpp", "kernels.hip"]
+SOURCES = ["plan.cpp", "program.cpp", "runtime.cpp", "capi.cpp", "kernels.hip",
+           "k_stream_fast.hip", "k_stream_generic.hip", "k_transpose.hip", "k_interleave.hip"]
 
 
 def _compile(src):
@@ -41,7 +42,7 @@ def _compile(src):
 
 def build(verbose=False):
     os.makedirs(OUT_DIR, exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
+    with ThreadPoolExecutor(max_workers=min(os.cpu_count() or 8, len(SOURCES), 16)) as ex:
         results = list(ex.map(_compile, SOURCES))
     for obj, err in results:
         if verbose and err.strip():

@@ -1,0 +1,753 @@
+// kernels.h - gfx950 relayout + value-stage kernel templates (device code).
+//
+// Every kernel maps dense SOURCE-layout wire values at some stage boundary to
+// the dense RESULT layout after the last stage, over an iteration box of
+// padded destination coordinates (so a chunked pipeline can launch one box
+// per arrived chunk). Pads are written with the folded fill; every value
+// stage keeps its own rounding (docs/reloc-typed-semantics.md), including the
+// reference's NaN encodings, so results are bit-identical to the reference
+// CPU executor (libreloc/src/TypedExecute.cpp:472-499).
+//
+// Families (chosen on the host, program.cpp):
+//   generic    one element per thread, any rank/stride/pad/channel map
+//   stream     innermost axis contiguous on both sides: one vector of
+//              16/min(width) elements per thread (16-byte loads/stores)
+//   transpose  batched 2-D transpose through a 64x64 LDS tile (32-bit
+//              words, row pitch 65: conflict-free for every element width
+//              pairing), XCD-grouped tile order
+//   interleave planar -> interleaved with a small padded inner axis
+//              (NCHW -> NHWC + pad): per-plane 16-byte loads, packed pixels
+// The common stage sequences get a compile-time body (ChainCode); the rest
+// dispatch per stage. Plain (cached) global accesses throughout: on gfx950
+// nontemporal stores of multi-vector lanes measured ~40% slower.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "program.h"
+
+namespace relx {
+namespace {
+
+constexpr int kBlock = 256;
+
+// Native 16-byte vector.
+typedef uint32_t vec4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv &f) {
+  const uint32_t hi = __umulhi(n, f.m);
+  return static_cast<uint32_t>((static_cast<uint64_t>(hi) + n) >> f.s);
+}
+
+// ------------------------------------------------------------ value ops
+
+__device__ __forceinline__ uint32_t op_f32_f16(uint32_t b) {
+  float f = __uint_as_float(b);
+  // The binary32 value must exist before it is narrowed: without this
+  // barrier the backend folds a producing multiply and the narrowing into
+  // v_fma_mixlo_f16 (one rounding), breaking dequantize -> cast, whose
+  // contract keeps both roundings.
+  asm volatile("" : "+v"(f));
+  const _Float16 h = static_cast<_Float16>(f);
+  uint32_t r = __builtin_bit_cast(unsigned short, h);
+  if ((b & 0x7fffffffu) > 0x7f800000u) // NaN: quiet, top payload bits kept
+    r = ((b >> 16) & 0x8000u) | 0x7e00u | ((b >> 13) & 0x3ffu);
+  return r;
+}
+
+__device__ __forceinline__ uint32_t op_f16_f32(uint32_t h) {
+  const _Float16 x = __builtin_bit_cast(_Float16, static_cast<unsigned short>(h));
+  uint32_t r = __float_as_uint(static_cast<float>(x));
+  if ((h & 0x7c00u) == 0x7c00u && (h & 0x3ffu)) // NaN: payload shifted, not quieted
+    r = ((h & 0x8000u) << 16) | 0x7f800000u | ((h & 0x3ffu) << 13);
+  return r;
+}
+
+__device__ __forceinline__ uint32_t op_f32_bf16(uint32_t b) {
+  if ((b & 0x7fffffffu) > 0x7f800000u)
+    return ((b >> 16) | 0x40u) & 0xffffu;
+  const uint64_t w = b;
+  return static_cast<uint32_t>((w + 0x7fffu + ((w >> 16) & 1u)) >> 16);
+}
+
+__device__ __forceinline__ uint32_t op_quant(uint32_t b, float inv) {
+  float y = __uint_as_float(b) * inv;
+  y = __builtin_fmaxf(y, -128.0f); // maxNum: NaN -> -128
+  y = __builtin_fminf(y, 127.0f);
+  return static_cast<uint32_t>(static_cast<int32_t>(__builtin_rintf(y))) & 0xffu;
+}
+
+__device__ __forceinline__ uint32_t op_dequant(uint32_t b, float scale, int32_t zp) {
+  const int32_t q = static_cast<int8_t>(static_cast<uint8_t>(b));
+  return __float_as_uint(static_cast<float>(q - zp) * scale);
+}
+
+__device__ __forceinline__ uint32_t apply(const DevStage &s, uint32_t x, uint32_t c,
+                                          const float *pf, const int32_t *pi) {
+  switch (s.op) {
+  case kOpF32toF16:
+    return op_f32_f16(x);
+  case kOpF16toF32:
+    return op_f16_f32(x);
+  case kOpF32toBF16:
+    return op_f32_bf16(x);
+  case kOpBF16toF32:
+    return x << 16;
+  case kOpQuantize:
+    return op_quant(x, pf[s.scale_off + c]);
+  default:
+    return op_dequant(x, pf[s.scale_off + c], pi[s.zp_off + (s.zp_per_ch ? c : 0u)]);
+  }
+}
+
+// Parameter entry of a kChanDim stage for dense result offset `o`.
+__device__ __forceinline__ uint32_t chan_of(const DevStage &s, int64_t o, int idx32) {
+  if (s.mode != kChanDim)
+    return 0u;
+  if (idx32) {
+    const uint32_t q = fdiv(static_cast<uint32_t>(o), s.ch_rs_div);
+    return q - fdiv(q, s.ch_re_div) * s.ch_re_div.d;
+  }
+  return static_cast<uint32_t>((o / s.ch_rs) % s.ch_re);
+}
+
+// --------------------------------------------------------- element access
+
+__device__ __forceinline__ uint64_t load_el(const uint8_t *p, int w) {
+  switch (w) {
+  case 1:
+    return *p;
+  case 2:
+    return *reinterpret_cast<const uint16_t *>(p);
+  case 4:
+    return *reinterpret_cast<const uint32_t *>(p);
+  default:
+    return *reinterpret_cast<const uint64_t *>(p);
+  }
+}
+
+__device__ __forceinline__ void store_el(uint8_t *p, uint64_t v, int w) {
+  switch (w) {
+  case 1:
+    *p = static_cast<uint8_t>(v);
+    break;
+  case 2:
+    *reinterpret_cast<uint16_t *>(p) = static_cast<uint16_t>(v);
+    break;
+  case 4:
+    *reinterpret_cast<uint32_t *>(p) = static_cast<uint32_t>(v);
+    break;
+  default:
+    *reinterpret_cast<uint64_t *>(p) = v;
+  }
+}
+
+__device__ int64_t eval_channel(const KArgs &a, const DevStage &s, int64_t o) {
+  int64_t st[kMaxChanTokens];
+  int sp = 0;
+  for (int t = s.tok_begin; t < s.tok_begin + s.tok_count; ++t) {
+    const ChanToken &k = a.chain.tok[t];
+    switch (k.op) {
+    case 1: // PUSH_CONST (symbols were resolved on the host)
+      st[sp++] = k.value;
+      break;
+    case 7: // PUSH_DIM
+      st[sp++] = (o / a.rs[k.value]) % a.re[k.value];
+      break;
+    default: {
+      const int64_t r = st[--sp], l = st[--sp];
+      int64_t v = 0;
+      if (k.op == 2)
+        v = l + r;
+      else if (k.op == 3)
+        v = l - r;
+      else if (k.op == 4)
+        v = l * r;
+      else {
+        if (r == 0)
+          return -1;
+        int64_t q = l / r;
+        if ((l % r != 0) && ((l < 0) != (r < 0)))
+          --q;
+        v = k.op == 5 ? q : l - q * r;
+      }
+      st[sp++] = v;
+    }
+    }
+  }
+  return st[0];
+}
+
+// -------------------------------------------------------------- generic
+
+// One element per thread; runtime indices are fine here (correctness path).
+__global__ __launch_bounds__(kBlock) __attribute__((unused)) void k_generic(KArgs a, int32_t *status) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < a.work;
+       i += stride) {
+    int64_t rem = i, dof = 0, sof = 0;
+    bool pad = false;
+    for (int k = a.rank - 1; k >= 0; --k) {
+      const int64_t e = a.box_ext[k];
+      const int64_t p = rem % e + a.box_lo[k];
+      rem /= e;
+      dof += p * a.ds[k];
+      const int64_t v = p - a.lo[k];
+      if (v < 0 || v >= a.vext[k])
+        pad = true;
+      else
+        sof += v * a.ss[k];
+    }
+    uint64_t x;
+    if (pad) {
+      x = a.fill;
+    } else {
+      x = load_el(a.src + sof * a.win, a.win);
+      for (int k = 0; k < a.chain.n; ++k) {
+        const DevStage &s = a.chain.st[k];
+        int64_t c = 0;
+        if (s.mode == kChanDim)
+          c = (dof / s.ch_rs) % s.ch_re;
+        else if (s.mode == kChanExpr)
+          c = eval_channel(a, s, dof);
+        if (c < 0 || c >= s.len) {
+          atomicExch(status, 1); // channel_out_of_range, reported by the host
+          c = 0;
+        }
+        x = apply(s, static_cast<uint32_t>(x), static_cast<uint32_t>(c), a.pf, a.pi);
+      }
+    }
+    store_el(a.dst + dof * a.wout, x, a.wout);
+  }
+}
+
+// --------------------------------------------------------- vector helpers
+
+// 32-bit word `i` of an array of 16-byte vectors.
+__device__ __forceinline__ uint32_t word(const vec4 *p, int i) { return p[i >> 2][i & 3]; }
+__device__ __forceinline__ void set_word(vec4 *p, int i, uint32_t x) { p[i >> 2][i & 3] = x; }
+
+template <int W, int V>
+__device__ __forceinline__ void unpack(const vec4 *in, uint32_t (&v)[V]) {
+#pragma unroll
+  for (int e = 0; e < V; ++e) {
+    if constexpr (W == 4)
+      v[e] = word(in, e);
+    else if constexpr (W == 2)
+      v[e] = (word(in, e >> 1) >> ((e & 1) * 16)) & 0xffffu;
+    else
+      v[e] = (word(in, e >> 2) >> ((e & 3) * 8)) & 0xffu;
+  }
+}
+
+template <int W, int V>
+__device__ __forceinline__ void pack(const uint32_t (&v)[V], vec4 *out) {
+  if constexpr (W == 4) {
+#pragma unroll
+    for (int e = 0; e < V; ++e)
+      set_word(out, e, v[e]);
+  } else if constexpr (W == 2) {
+#pragma unroll
+    for (int e = 0; e < V / 2; ++e)
+      set_word(out, e, (v[2 * e] & 0xffffu) | (v[2 * e + 1] << 16));
+  } else {
+#pragma unroll
+    for (int e = 0; e < V / 4; ++e)
+      set_word(out, e,
+               (v[4 * e] & 0xffu) | ((v[4 * e + 1] & 0xffu) << 8) |
+                   ((v[4 * e + 2] & 0xffu) << 16) | (v[4 * e + 3] << 24));
+  }
+}
+
+// One stage over V consecutive destination elements starting at dense result
+// offset `o` (channel constant or +1 per element, proven on the host).
+template <int V>
+__device__ __forceinline__ void stage_vec(const KArgs &a, const DevStage &s, uint32_t (&v)[V],
+                                          int64_t o) {
+  const uint32_t c = chan_of(s, o, a.idx32);
+  switch (s.op) {
+  case kOpF32toF16:
+#pragma unroll
+    for (int e = 0; e < V; ++e)
+      v[e] = op_f32_f16(v[e]);
+    break;
+  case kOpF16toF32:
+#pragma unroll
+    for (int e = 0; e < V; ++e)
+      v[e] = op_f16_f32(v[e]);
+    break;
+  case kOpF32toBF16:
+#pragma unroll
+    for (int e = 0; e < V; ++e)
+      v[e] = op_f32_bf16(v[e]);
+    break;
+  case kOpBF16toF32:
+#pragma unroll
+    for (int e = 0; e < V; ++e)
+      v[e] <<= 16;
+    break;
+  case kOpQuantize:
+    if (s.vec == 0) {
+      const float inv = a.pf[s.scale_off + c];
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+        v[e] = op_quant(v[e], inv);
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+        v[e] = op_quant(v[e], a.pf[s.scale_off + c + e]);
+    }
+    break;
+  default:
+    if (s.vec == 0) {
+      const float sc = a.pf[s.scale_off + c];
+      const int32_t zp = a.pi[s.zp_off + (s.zp_per_ch ? c : 0u)];
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+        v[e] = op_dequant(v[e], sc, zp);
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+        v[e] = op_dequant(v[e], a.pf[s.scale_off + c + e],
+                          a.pi[s.zp_off + (s.zp_per_ch ? c + e : 0u)]);
+    }
+  }
+}
+
+// The stage chain over one vector: compile-time bodies for the common
+// sequences, per-stage dispatch (stage index still compile-time) otherwise.
+template <int CH, int V>
+__device__ __forceinline__ void chain_vec(const KArgs &a, uint32_t (&v)[V], int64_t o) {
+  if constexpr (CH == kChainNone) {
+  } else if constexpr (CH == kChainF32F16) {
+#pragma unroll
+    for (int e = 0; e < V; ++e)
+      v[e] = op_f32_f16(v[e]);
+  } else if constexpr (CH == kChainF16F32) {
+#pragma unroll
+    for (int e = 0; e < V; ++e)
+      v[e] = op_f16_f32(v[e]);
+  } else if constexpr (CH == kChainDeqF16) {
+    const DevStage &s = a.chain.st[0];
+    const uint32_t c = chan_of(s, o, a.idx32);
+    if (s.vec == 0) {
+      const float sc = a.pf[s.scale_off + c];
+      const int32_t zp = a.pi[s.zp_off + (s.zp_per_ch ? c : 0u)];
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+        v[e] = op_f32_f16(op_dequant(v[e], sc, zp));
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+        v[e] = op_f32_f16(op_dequant(v[e], a.pf[s.scale_off + c + e],
+                                     a.pi[s.zp_off + (s.zp_per_ch ? c + e : 0u)]));
+    }
+  } else if constexpr (CH == kChainDeq) {
+    stage_vec<V>(a, a.chain.st[0], v, o);
+  } else if constexpr (CH == kChainF16Quant) {
+    const DevStage &s = a.chain.st[1];
+    const uint32_t c = chan_of(s, o, a.idx32);
+    if (s.vec == 0) {
+      const float inv = a.pf[s.scale_off + c];
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+        v[e] = op_quant(op_f16_f32(v[e]), inv);
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+        v[e] = op_quant(op_f16_f32(v[e]), a.pf[s.scale_off + c + e]);
+    }
+  } else if constexpr (CH == kChainQuant) {
+    stage_vec<V>(a, a.chain.st[0], v, o);
+  } else {
+#pragma unroll
+    for (int k = 0; k < kMaxStages; ++k) {
+      if (k >= a.chain.n)
+        break;
+      stage_vec<V>(a, a.chain.st[k], v, o);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- stream
+
+// Box decomposition of vector `i` into padded coordinates (the innermost
+// box coordinate counts vectors of `inner_mul` elements). RANK > 0 fixes the
+// rank at compile time; 0 reads it. Returns true when any coordinate lies in
+// a pad. Loops are unrolled over kMaxRank so every argument index is static.
+template <int RANK>
+__device__ __forceinline__ bool locate(const KArgs &a, int64_t i, int inner_mul, int64_t &sof,
+                                       int64_t &dof) {
+  constexpr int KMAX = RANK > 0 ? RANK : kMaxRank;
+  const int rank = RANK > 0 ? RANK : a.rank;
+  bool pad = false;
+  sof = 0;
+  dof = 0;
+  if (a.idx32) {
+    uint32_t rem = static_cast<uint32_t>(i);
+#pragma unroll
+    for (int k = KMAX - 1; k >= 0; --k) {
+      if (RANK == 0 && k >= rank)
+        continue;
+      uint32_t ck = rem;
+      if (k > 0) { // the outermost axis needs no division
+        const uint32_t q = fdiv(rem, a.box_div[k]);
+        ck = rem - q * a.box_div[k].d;
+        rem = q;
+      }
+      if (k == rank - 1)
+        ck *= inner_mul;
+      const int64_t p = static_cast<int64_t>(ck) + a.box_lo[k];
+      dof += p * a.ds[k];
+      const int64_t v = p - a.lo[k];
+      if (v < 0 || v >= a.vext[k])
+        pad = true;
+      else
+        sof += v * a.ss[k];
+    }
+  } else {
+    int64_t rem = i;
+#pragma unroll
+    for (int k = KMAX - 1; k >= 0; --k) {
+      if (RANK == 0 && k >= rank)
+        continue;
+      const int64_t e = k == rank - 1 ? a.box_ext[k] / inner_mul : a.box_ext[k];
+      int64_t ck = rem % e;
+      rem /= e;
+      if (k == rank - 1)
+        ck *= inner_mul;
+      const int64_t p = ck + a.box_lo[k];
+      dof += p * a.ds[k];
+      const int64_t v = p - a.lo[k];
+      if (v < 0 || v >= a.vext[k])
+        pad = true;
+      else
+        sof += v * a.ss[k];
+    }
+  }
+  return pad;
+}
+
+// One vector of V = 16/min(width) elements per thread: the narrower side
+// moves exactly 16 bytes and the wider side 32 or 64, all lane-contiguous.
+template <int WIN, int WOUT, int RANK, int CH>
+__global__ __launch_bounds__(kBlock) void k_stream(KArgs a) {
+  constexpr int V = 16 / (WIN < WOUT ? WIN : WOUT);
+  constexpr int NI = V * WIN / 16, NO = V * WOUT / 16;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < a.work;
+       i += stride) {
+    int64_t sof, dof;
+    const bool pad = locate<RANK>(a, i, V, sof, dof);
+    uint32_t v[V];
+    if (pad) {
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+        v[e] = static_cast<uint32_t>(a.fill);
+    } else {
+      vec4 in[NI];
+      const vec4 *src = reinterpret_cast<const vec4 *>(a.src + sof * WIN);
+#pragma unroll
+      for (int j = 0; j < NI; ++j)
+        in[j] = src[j];
+      unpack<WIN, V>(in, v);
+      chain_vec<CH, V>(a, v, dof);
+    }
+    vec4 out[NO];
+    pack<WOUT, V>(v, out);
+    vec4 *dst = reinterpret_cast<vec4 *>(a.dst + dof * WOUT);
+#pragma unroll
+    for (int j = 0; j < NO; ++j)
+      dst[j] = out[j];
+  }
+}
+
+// ------------------------------------------------------------- transpose
+
+constexpr int kTile = 64;
+constexpr int kPitch = kTile + 1;
+
+// Map a linear block id so that the blocks one XCD runs (ids congruent mod 8)
+// take a contiguous run of tiles: neighbouring tiles share source cache lines.
+__device__ __forceinline__ uint32_t xcd_tile(uint32_t b, uint32_t n) {
+  constexpr uint32_t kXcd = 8;
+  if (n < kXcd)
+    return b;
+  const uint32_t per = n / kXcd, extra = n % kXcd, x = b % kXcd, j = b / kXcd;
+  // XCD x owns tiles [x*per + min(x, extra), ...) of length per + (x < extra)
+  return x * per + (x < extra ? x : extra) + j;
+}
+
+// Batch offsets of linear batch index `rest` (row-major over b_ext).
+__device__ __forceinline__ void batch_offsets(const KArgs &a, int64_t rest, int64_t &sbase,
+                                              int64_t &dbase, bool &pad) {
+  sbase = 0;
+  dbase = 0;
+  pad = false;
+#pragma unroll
+  for (int k = kMaxRank - 1; k >= 0; --k) {
+    if (k >= a.nbatch)
+      continue;
+    const int64_t e = a.b_ext[k];
+    const int64_t p = rest % e + a.b_lo[k];
+    rest /= e;
+    dbase += p * a.b_ds[k];
+    const int64_t v = p - a.b_pad[k];
+    if (v < 0 || v >= a.b_vext[k])
+      pad = true;
+    else
+      sbase += v * a.b_ss[k];
+  }
+}
+
+template <int WIN, int WOUT, int CH>
+__global__ __launch_bounds__(kBlock) void k_transpose(KArgs a) {
+  __shared__ uint32_t tile[kTile * kPitch]; // [c][q]
+  constexpr int VI = 16 / WIN, VO = 16 / WOUT;
+  constexpr int VPRI = kTile / VI, VPRO = kTile / VO;
+  constexpr int NI = kTile * VPRI / kBlock, NO = kTile * VPRO / kBlock;
+  const uint32_t t = xcd_tile(blockIdx.x, gridDim.x);
+  if (t >= a.work)
+    return;
+  int64_t rest = t;
+  const int64_t tq = rest % a.t_nq;
+  rest /= a.t_nq;
+  const int64_t tc = rest % a.t_nc;
+  rest /= a.t_nc;
+  int64_t sbase, dbase;
+  bool unused;
+  batch_offsets(a, rest, sbase, dbase, unused); // transposes carry no pads
+  const int64_t q0 = a.t_q0 + tq * kTile, c0 = a.t_c0 + tc * kTile;
+  // load: source rows c (stride t_ssc), contiguous q
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    const int vid = threadIdx.x + j * kBlock;
+    const int row = vid / VPRI, cv = vid % VPRI;
+    const vec4 *p = reinterpret_cast<const vec4 *>(
+        a.src + (sbase + (c0 + row) * a.t_ssc + q0 + cv * VI) * WIN);
+    const vec4 in = *p;
+    uint32_t v[VI];
+    unpack<WIN, VI>(&in, v);
+#pragma unroll
+    for (int e = 0; e < VI; ++e)
+      tile[row * kPitch + cv * VI + e] = v[e];
+  }
+  __syncthreads();
+  // store: destination rows q (stride t_dsq), contiguous c
+#pragma unroll
+  for (int j = 0; j < NO; ++j) {
+    const int vid = threadIdx.x + j * kBlock;
+    const int q = vid / VPRO, cv = vid % VPRO;
+    uint32_t v[VO];
+#pragma unroll
+    for (int e = 0; e < VO; ++e)
+      v[e] = tile[(cv * VO + e) * kPitch + q];
+    const int64_t o = dbase + (q0 + q) * a.t_dsq + c0 + cv * VO;
+    chain_vec<CH, VO>(a, v, o);
+    vec4 out;
+    pack<WOUT, VO>(v, &out);
+    *reinterpret_cast<vec4 *>(a.dst + o * WOUT) = out;
+  }
+}
+
+// ------------------------------------------------------------ interleave
+
+// Axes: [batch..., P, C] with C (padded to CP) innermost in the destination
+// and a plane stride in the source; P contiguous in the source. Each thread
+// takes G = 16/WIN consecutive pixels: one 16-byte load per valid plane, one
+// packed run of G*CP output elements. Stages are per tensor.
+template <int WIN, int WOUT, int CP, int CH>
+__global__ __launch_bounds__(kBlock) void k_interleave(KArgs a) {
+  constexpr int G = 16 / WIN;
+  constexpr int NO = G * CP * WOUT / 16;
+  static_assert(G * CP * WOUT % 16 == 0, "packed pixels must fill whole vectors");
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < a.work;
+       i += stride) {
+    const int64_t g = i % a.i_ngroups;
+    int64_t sbase, dbase;
+    bool pad;
+    batch_offsets(a, i / a.i_ngroups, sbase, dbase, pad);
+    const int64_t p0 = a.i_p0 + g * G; // pixel axis is unpadded
+    uint32_t px[CP][G];
+#pragma unroll
+    for (int ch = 0; ch < CP; ++ch) {
+      const int64_t vc = ch - a.i_loc;
+      if (pad || vc < 0 || vc >= a.i_vc) {
+#pragma unroll
+        for (int e = 0; e < G; ++e)
+          px[ch][e] = static_cast<uint32_t>(a.fill);
+      } else {
+        const vec4 in =
+            *reinterpret_cast<const vec4 *>(a.src + (sbase + vc * a.i_ssc + p0) * WIN);
+        uint32_t v[G];
+        unpack<WIN, G>(&in, v);
+        chain_vec<CH, G>(a, v, 0);
+#pragma unroll
+        for (int e = 0; e < G; ++e)
+          px[ch][e] = v[e];
+      }
+    }
+    uint32_t flat[G * CP];
+#pragma unroll
+    for (int e = 0; e < G; ++e)
+#pragma unroll
+      for (int ch = 0; ch < CP; ++ch)
+        flat[e * CP + ch] = px[ch][e];
+    vec4 out[NO];
+    pack<WOUT, G * CP>(flat, out);
+    vec4 *dst = reinterpret_cast<vec4 *>(a.dst + (dbase + p0 * CP) * WOUT);
+#pragma unroll
+    for (int j = 0; j < NO; ++j)
+      dst[j] = out[j];
+  }
+}
+
+// ------------------------------------------------------------ launch
+
+// One work item per thread up to 2^22 blocks (2^30 work-items per launch,
+// inside HIP's 2^32 limit); larger launches grid-stride.
+unsigned grid_for(int64_t work) {
+  const int64_t blocks = (work + kBlock - 1) / kBlock;
+  return static_cast<unsigned>(blocks < (1 << 22) ? (blocks > 0 ? blocks : 1) : (1 << 22));
+}
+
+template <int WIN, int WOUT, int CH>
+hipError_t stream_launch(const KArgs &a, hipStream_t s) {
+  const dim3 grid(grid_for(a.work)), block(kBlock);
+  switch (a.rank) {
+  case 1:
+    hipLaunchKernelGGL((k_stream<WIN, WOUT, 1, CH>), grid, block, 0, s, a);
+    break;
+  case 2:
+    hipLaunchKernelGGL((k_stream<WIN, WOUT, 2, CH>), grid, block, 0, s, a);
+    break;
+  case 3:
+    hipLaunchKernelGGL((k_stream<WIN, WOUT, 3, CH>), grid, block, 0, s, a);
+    break;
+  case 4:
+    hipLaunchKernelGGL((k_stream<WIN, WOUT, 4, CH>), grid, block, 0, s, a);
+    break;
+  default:
+    hipLaunchKernelGGL((k_stream<WIN, WOUT, 0, CH>), grid, block, 0, s, a);
+  }
+  return hipGetLastError();
+}
+
+template <int WIN, int WOUT, int CH>
+hipError_t transpose_launch(const KArgs &a, hipStream_t s) {
+  hipLaunchKernelGGL((k_transpose<WIN, WOUT, CH>), dim3(static_cast<unsigned>(a.work)),
+                     dim3(kBlock), 0, s, a);
+  return hipGetLastError();
+}
+
+template <int WIN, int WOUT, int CH, int CP>
+hipError_t interleave_cp(const KArgs &a, hipStream_t s) {
+  if constexpr ((16 / WIN) * CP * WOUT % 16 == 0) {
+    hipLaunchKernelGGL((k_interleave<WIN, WOUT, CP, CH>), dim3(grid_for(a.work)), dim3(kBlock),
+                       0, s, a);
+    return hipGetLastError();
+  } else {
+    return hipErrorInvalidValue;
+  }
+}
+
+template <int WIN, int WOUT, int CH>
+hipError_t interleave_launch(const KArgs &a, hipStream_t s) {
+  switch (a.cpad) {
+  case 2:
+    return interleave_cp<WIN, WOUT, CH, 2>(a, s);
+  case 4:
+    return interleave_cp<WIN, WOUT, CH, 4>(a, s);
+  case 8:
+    return interleave_cp<WIN, WOUT, CH, 8>(a, s);
+  default:
+    return hipErrorInvalidValue;
+  }
+}
+
+// Instantiations are split over several translation units (one per family
+// and chain class) so the build compiles them in parallel.
+#define RELX_DISPATCH_FAST(NAME, FN)                                                       \
+  hipError_t NAME(const KArgs &a, hipStream_t s, bool &handled) {                          \
+    const int w = a.win * 8 + a.wout;                                                      \
+    handled = true;                                                                        \
+    switch (a.chain_code) {                                                                \
+    case kChainNone:                                                                       \
+      if (w == 9)                                                                          \
+        return FN<1, 1, kChainNone>(a, s);                                                 \
+      if (w == 18)                                                                         \
+        return FN<2, 2, kChainNone>(a, s);                                                 \
+      if (w == 36)                                                                         \
+        return FN<4, 4, kChainNone>(a, s);                                                 \
+      break;                                                                               \
+    case kChainF32F16:                                                                     \
+      if (w == 34)                                                                         \
+        return FN<4, 2, kChainF32F16>(a, s);                                               \
+      break;                                                                               \
+    case kChainF16F32:                                                                     \
+      if (w == 20)                                                                         \
+        return FN<2, 4, kChainF16F32>(a, s);                                               \
+      break;                                                                               \
+    case kChainDeqF16:                                                                     \
+      if (w == 10)                                                                         \
+        return FN<1, 2, kChainDeqF16>(a, s);                                               \
+      break;                                                                               \
+    case kChainDeq:                                                                        \
+      if (w == 12)                                                                         \
+        return FN<1, 4, kChainDeq>(a, s);                                                  \
+      break;                                                                               \
+    case kChainF16Quant:                                                                   \
+      if (w == 17)                                                                         \
+        return FN<2, 1, kChainF16Quant>(a, s);                                             \
+      break;                                                                               \
+    case kChainQuant:                                                                      \
+      if (w == 33)                                                                         \
+        return FN<4, 1, kChainQuant>(a, s);                                                \
+      break;                                                                               \
+    default:                                                                               \
+      break;                                                                               \
+    }                                                                                      \
+    handled = false;                                                                       \
+    return hipSuccess;                                                                     \
+  }
+
+#define RELX_DISPATCH_GENERIC(NAME, FN)                                                    \
+  hipError_t NAME(const KArgs &a, hipStream_t s) {                                         \
+    switch (a.win * 8 + a.wout) {                                                          \
+    case 9:                                                                                \
+      return FN<1, 1, kChainGeneric>(a, s);                                                \
+    case 10:                                                                               \
+      return FN<1, 2, kChainGeneric>(a, s);                                                \
+    case 12:                                                                               \
+      return FN<1, 4, kChainGeneric>(a, s);                                                \
+    case 17:                                                                               \
+      return FN<2, 1, kChainGeneric>(a, s);                                                \
+    case 18:                                                                               \
+      return FN<2, 2, kChainGeneric>(a, s);                                                \
+    case 20:                                                                               \
+      return FN<2, 4, kChainGeneric>(a, s);                                                \
+    case 33:                                                                               \
+      return FN<4, 1, kChainGeneric>(a, s);                                                \
+    case 34:                                                                               \
+      return FN<4, 2, kChainGeneric>(a, s);                                                \
+    case 36:                                                                               \
+      return FN<4, 4, kChainGeneric>(a, s);                                                \
+    default:                                                                               \
+      return hipErrorInvalidValue;                                                         \
+    }                                                                                      \
+  }
+
+} // namespace
+
+// Entry points of the per-family translation units.
+hipError_t stream_fast(const KArgs &a, hipStream_t s, bool &handled);
+hipError_t stream_generic(const KArgs &a, hipStream_t s);
+hipError_t transpose_fast(const KArgs &a, hipStream_t s, bool &handled);
+hipError_t transpose_generic(const KArgs &a, hipStream_t s);
+hipError_t interleave_fast(const KArgs &a, hipStream_t s, bool &handled);
+hipError_t interleave_generic(const KArgs &a, hipStream_t s);
+
+} // namespace relx

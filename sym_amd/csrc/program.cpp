@@ -302,8 +302,6 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
   for (int j = 0; j < a.res_rank && j < kMaxRank; ++j) {
     a.rs[j] = p.res_strides[static_cast<size_t>(j)];
     a.re[j] = b.result_extents[static_cast<size_t>(j)];
-    a.rs_div[j] = make_div(a.rs[j]);
-    a.re_div[j] = make_div(a.re[j]);
   }
   if (a.res_rank > kMaxRank)
     fail("unsupported_layout", "result rank above the device limit");
@@ -317,7 +315,12 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
     DevStage &d = ch.st[i - k];
     d.op = h.op;
     d.mode = h.mode;
-    d.dim = static_cast<uint8_t>(h.dim);
+    if (h.mode == kChanDim) {
+      d.ch_rs = p.res_strides[static_cast<size_t>(h.dim)];
+      d.ch_re = b.result_extents[static_cast<size_t>(h.dim)];
+      d.ch_rs_div = make_div(d.ch_rs);
+      d.ch_re_div = make_div(d.ch_re);
+    }
     d.len = static_cast<uint32_t>(h.len);
     d.scale_off = static_cast<uint32_t>(dp->pf.size());
     const std::vector<float> &f = h.op == kOpQuantize ? h.inv : h.scale;
@@ -411,10 +414,15 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
         for (int i = 0; i < r - 1; ++i)
           if (i != qa)
             ok = ok && a.ss[i] % VI == 0 && a.ds[i] % VO == 0;
+        int64_t tiles = (a.vext[qa] / 64) * (a.vext[r - 1] / 64);
+        for (int i = 0; i < r - 1; ++i)
+          if (i != qa)
+            tiles *= a.vext[i];
+        ok = ok && tiles < (int64_t{1} << 22); // one block per tile
         if (ok && channels_ok(VO)) {
           family = kFamTranspose;
-          a.qa = qa;
-          a.ca = r - 1;
+          dp->qa = qa;
+          dp->ca = r - 1;
         }
       }
     }
@@ -441,6 +449,29 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
     for (uint32_t i = k; i < nst; ++i)
       ch.st[i - k].vec = 0;
   dp->family = family;
+  {
+    // stage sequences with a compile-time kernel body
+    std::vector<uint8_t> ops;
+    for (uint32_t i = k; i < nst; ++i)
+      ops.push_back(p.stages[i].op);
+    using V8 = std::vector<uint8_t>;
+    int code = kChainGeneric;
+    if (ops.empty())
+      code = kChainNone;
+    else if (ops == V8{kOpF32toF16})
+      code = kChainF32F16;
+    else if (ops == V8{kOpF16toF32})
+      code = kChainF16F32;
+    else if (ops == V8{kOpDequantize, kOpF32toF16})
+      code = kChainDeqF16;
+    else if (ops == V8{kOpDequantize})
+      code = kChainDeq;
+    else if (ops == V8{kOpF16toF32, kOpQuantize})
+      code = kChainF16Quant;
+    else if (ops == V8{kOpQuantize})
+      code = kChainQuant;
+    a.chain_code = code;
+  }
   static const char *names[] = {"generic", "stream", "transpose", "interleave"};
   dp->kernel = names[family];
 
@@ -462,7 +493,7 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
         dp->chunk_stride = a.ss[ax];
         if (family == kFamStream && ax == r - 1)
           dp->chunk_align = V;
-        else if (family == kFamTranspose && (ax == a.qa || ax == a.ca))
+        else if (family == kFamTranspose && (ax == dp->qa || ax == dp->ca))
           dp->chunk_align = 64;
         else if (family == kFamInterleave && ax == r - 2)
           dp->chunk_align = a.vec;
@@ -492,6 +523,22 @@ KArgs box_args(const DeviceProgram &dp, int64_t v0, int64_t v1, bool first, bool
   int64_t box_total = 1;
   for (int i = 0; i < r; ++i)
     box_total *= a.box_ext[i];
+  // the axes outside a 2-D block, outer first (transpose / interleave)
+  auto batch = [&](int skip0, int skip1) {
+    int n = 0;
+    for (int i = 0; i < r; ++i) {
+      if (i == skip0 || i == skip1)
+        continue;
+      a.b_ext[n] = a.box_ext[i];
+      a.b_lo[n] = a.box_lo[i];
+      a.b_pad[n] = a.lo[i];
+      a.b_vext[n] = a.vext[i];
+      a.b_ss[n] = a.ss[i];
+      a.b_ds[n] = a.ds[i];
+      ++n;
+    }
+    a.nbatch = n;
+  };
   switch (dp.family) {
   case kFamStream: {
     for (int i = 0; i < r; ++i)
@@ -500,16 +547,31 @@ KArgs box_args(const DeviceProgram &dp, int64_t v0, int64_t v1, bool first, bool
     break;
   }
   case kFamTranspose: {
-    int64_t n = 1;
-    for (int i = 0; i < r; ++i)
-      n *= (i == a.qa || i == a.ca) ? a.box_ext[i] / 64 : a.box_ext[i];
+    const int qa = dp.qa, ca = dp.ca;
+    batch(qa, ca);
+    a.t_nq = a.box_ext[qa] / 64;
+    a.t_nc = a.box_ext[ca] / 64;
+    a.t_q0 = a.box_lo[qa];
+    a.t_c0 = a.box_lo[ca];
+    a.t_ssc = a.ss[ca];
+    a.t_dsq = a.ds[qa];
+    int64_t n = a.t_nq * a.t_nc;
+    for (int i = 0; i < a.nbatch; ++i)
+      n *= a.b_ext[i];
     a.work = n;
     break;
   }
   case kFamInterleave: {
-    int64_t n = a.box_ext[r - 2] / a.vec;
-    for (int i = 0; i < r - 2; ++i)
-      n *= a.box_ext[i];
+    const int pa = r - 2, ca = r - 1;
+    batch(pa, ca);
+    a.i_ngroups = a.box_ext[pa] / a.vec;
+    a.i_p0 = a.box_lo[pa];
+    a.i_ssc = a.ss[ca];
+    a.i_loc = a.lo[ca];
+    a.i_vc = a.vext[ca];
+    int64_t n = a.i_ngroups;
+    for (int i = 0; i < a.nbatch; ++i)
+      n *= a.b_ext[i];
     a.work = n;
     break;
   }

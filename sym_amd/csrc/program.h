@@ -6,6 +6,11 @@
 // after the last stage: an iteration box over the coalesced destination axes
 // (padded coordinates), the source strides of the valid region, the pad fill,
 // and the remaining value stages with their per-channel parameters.
+//
+// Every field a kernel reads is addressed with a compile-time index (arrays
+// only inside fully unrolled loops, per-stage and per-family scalars
+// precomputed here): a runtime index into the by-value argument block turns
+// each read into a vector-memory load on the kernel's critical path.
 #pragma once
 
 #include <cstdint>
@@ -29,8 +34,21 @@ enum DevOp : uint8_t {
 // How a stage picks its parameter entry.
 enum ChanMode : uint8_t {
   kChanNone = 0, // per tensor: entry 0
-  kChanDim = 1,  // the logical result coordinate along `dim`
+  kChanDim = 1,  // the logical result coordinate along one dimension
   kChanExpr = 2, // a channel expression over result coordinates (generic kernel)
+};
+
+// Stage sequences with a compile-time kernel body; anything else runs the
+// generic per-stage dispatch.
+enum ChainCode : int32_t {
+  kChainGeneric = 0,
+  kChainNone = 1,     // layout only
+  kChainF32F16 = 2,   // cast f32 -> f16
+  kChainF16F32 = 3,   // cast f16 -> f32
+  kChainDeqF16 = 4,   // dequantize -> cast f16 (fused, both roundings kept)
+  kChainDeq = 5,      // dequantize
+  kChainF16Quant = 6, // cast f16 -> f32 -> quantize
+  kChainQuant = 7,    // quantize
 };
 
 // Division by a runtime constant for n < 2^32: q = (umulhi(n, m) + n) >> s.
@@ -47,14 +65,14 @@ struct ChanToken {
 struct DevStage {
   uint8_t op;
   uint8_t mode;
-  uint8_t dim;       // kChanDim: result dimension
   uint8_t zp_per_ch; // zero point has one entry per channel
-  uint8_t vec;       // fast kernels: 0 channel constant across a vector, 1 +1 per element
-  uint8_t pad_[3];
+  uint8_t vec;       // vector kernels: 0 channel constant across a vector, 1 +1 per element
   uint32_t scale_off; // float param index (dequant scale / quant reciprocal)
   uint32_t zp_off;    // int param index
   uint32_t len;       // parameter entries
   int32_t tok_begin, tok_count;
+  int64_t ch_rs, ch_re; // kChanDim: result stride and extent of the channel dimension
+  FastDiv ch_rs_div, ch_re_div;
 };
 
 struct Chain {
@@ -71,7 +89,7 @@ enum Family : int32_t {
   kFamInterleave = 3, // planar -> interleaved with a small padded inner axis
 };
 
-// Launch arguments. All extents/strides are in elements of the coalesced
+// Launch arguments. Extents/strides are in elements of the coalesced
 // destination-order axes of the bound layout.
 struct KArgs {
   const uint8_t *src; // wire (device) at the program's boundary
@@ -82,6 +100,9 @@ struct KArgs {
   int32_t win, wout;  // element bytes of the wire and of the result
   int32_t has_fill;
   uint64_t fill;
+  int32_t idx32;      // every index of this launch fits in 32 bits
+  int32_t chain_code;
+  int64_t work;       // work items in this launch
   int64_t pext[kMaxRank]; // padded extents
   int64_t lo[kMaxRank];   // leading pad per axis
   int64_t vext[kMaxRank]; // valid extents
@@ -89,18 +110,30 @@ struct KArgs {
   int64_t ds[kMaxRank];   // destination strides (padded coordinates)
   int64_t box_lo[kMaxRank];
   int64_t box_ext[kMaxRank];
-  FastDiv box_div[kMaxRank]; // over box_ext (family-specific inner handling)
+  FastDiv box_div[kMaxRank]; // over the work decomposition of each axis
+  // result coordinates for channel expressions (generic kernel)
   int32_t res_rank;
-  int32_t idx32; // every index of this launch fits in 32 bits
-  int64_t rs[kMaxRank]; // result strides (dense, padded result)
-  int64_t re[kMaxRank]; // result extents
-  FastDiv rs_div[kMaxRank];
-  FastDiv re_div[kMaxRank];
-  int64_t work; // work items in this launch
-  // family parameters
-  int32_t qa, ca; // transpose: source-inner axis (dst row) and dst-inner axis
-  int32_t vec;    // stream: elements per vector; interleave: pixels per thread
-  int32_t cpad;   // interleave: padded inner extent
+  int32_t vec;  // stream: elements per vector; interleave: pixels per thread
+  int64_t rs[kMaxRank];
+  int64_t re[kMaxRank];
+  // transpose / interleave: the axes outside the 2-D block, outer first
+  int32_t nbatch;
+  int32_t cpad; // interleave: padded inner extent
+  int64_t b_ext[kMaxRank];  // box extent
+  int64_t b_lo[kMaxRank];   // box start (padded coordinate)
+  int64_t b_pad[kMaxRank];  // leading pad
+  int64_t b_vext[kMaxRank]; // valid extent
+  int64_t b_ss[kMaxRank];
+  int64_t b_ds[kMaxRank];
+  // transpose: source-inner axis q (destination rows) and destination-inner c
+  int64_t t_nq, t_nc;   // tiles along q and c in this box
+  int64_t t_q0, t_c0;   // box start along q and c
+  int64_t t_ssc, t_dsq; // source stride of c, destination stride of q
+  // interleave: pixel axis p (source-contiguous) and channel axis c
+  int64_t i_ngroups;   // pixel groups in the box
+  int64_t i_p0;        // box start along p
+  int64_t i_ssc;       // plane stride (source stride of c)
+  int64_t i_loc, i_vc; // leading pad and valid extent of c
   Chain chain;
 };
 

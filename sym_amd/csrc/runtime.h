@@ -46,6 +46,7 @@ struct DeviceProgram {
   int64_t wire_elems = 0, wire_bytes = 0, dst_elems = 0;
   int chunk_axis = -1;
   int64_t chunk_stride = 0, chunk_align = 1;
+  int qa = -1, ca = -1; // transpose: source-inner (destination row) and destination-inner axes
   std::vector<float> pf;
   std::vector<int32_t> pi;
 };

@@ -298,3 +298,44 @@ def test_context_stats_and_reuse(ctx):
     st = ctx.stats()
     assert st["calls"] > 0 and st["failures"] == 0 and not st["quarantined"]
     assert st["device_bytes"] > 0
+
+
+# ------------------------------------------------ double rounding regression
+
+def _double_rounding_rows(rng, want_rows=256):
+    """(q, scale) rows where f16(fl32(q*s)) differs from a single rounding of
+    the exact product to f16: a fused multiply+narrow would flip them."""
+    rows, scales = [], []
+    q_all = np.arange(-128, 128, dtype=np.int32)
+    while len(rows) < want_rows:
+        s = rng.uniform(1e-3, 2e-2, 4096).astype(np.float32)
+        exact = q_all[None, :].astype(np.float64) * s[:, None].astype(np.float64)
+        two = O.narrow_f32_f16_bits(exact.astype(np.float32).view(np.uint32))
+        one = exact.astype(np.float16).view(np.uint16)  # single rounding of the exact product
+        hit = np.argwhere(two != one)
+        for r, c in hit:
+            row = np.full(256, q_all[c], np.int8)
+            row[:] = rng.integers(-127, 128, 256)
+            row[0] = q_all[c]
+            rows.append(row)
+            scales.append(s[r])
+            if len(rows) >= want_rows:
+                break
+    return np.stack(rows), np.array(scales, np.float32)
+
+
+def test_dequant_f16_keeps_both_roundings(ctx):
+    rng = np.random.default_rng(99)
+    q, s = _double_rounding_rows(rng)
+    want = f16_bits(O.dequantize_s8_f32(q, s[:, None], np.int32(0)))
+    # stream family (C4 layout)
+    out, _, b = run_h2d(ctx, W.c4_plan().blob, {"s0": q.shape[0], "s1": q.shape[1]},
+                        W.param("scale", s), q, "double rounding, stream")
+    assert b.kernel == "stream"
+    assert np.array_equal(out.view(np.uint16).reshape(q.shape), want)
+    # transpose family (C3 layout): source [256 cols x rows] with per-column scales
+    qt = np.ascontiguousarray(q.T)
+    out, _, b = run_h2d(ctx, W.c3_plan().blob, {"s0": qt.shape[0], "s1": qt.shape[1]},
+                        W.param("scale", s), qt, "double rounding, transpose")
+    assert b.kernel == "transpose"
+    assert np.array_equal(out.view(np.uint16).reshape(q.shape), want)
