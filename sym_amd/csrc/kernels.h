@@ -48,21 +48,27 @@ __device__ __forceinline__ uint32_t op_f32_f16(uint32_t b) {
   // The binary32 value must exist before it is narrowed: without this
   // barrier the backend folds a producing multiply and the narrowing into
   // v_fma_mixlo_f16 (one rounding), breaking dequantize -> cast, whose
-  // contract keeps both roundings.
+  // contract keeps both roundings. v_cvt_f16_f32 itself rounds to nearest
+  // even and encodes NaN as sign | 0x7e00 | payload >> 13 -- the reference's
+  // encoding (checked on gfx950 for every binary32 NaN).
   asm volatile("" : "+v"(f));
-  const _Float16 h = static_cast<_Float16>(f);
-  uint32_t r = __builtin_bit_cast(unsigned short, h);
-  if ((b & 0x7fffffffu) > 0x7f800000u) // NaN: quiet, top payload bits kept
-    r = ((b >> 16) & 0x8000u) | 0x7e00u | ((b >> 13) & 0x3ffu);
-  return r;
+  return __builtin_bit_cast(unsigned short, static_cast<_Float16>(f));
 }
 
+// Exact binary16 -> binary32. The hardware quiets signalling NaNs; the
+// reference keeps the payload as is, so NaNs are rebuilt.
 __device__ __forceinline__ uint32_t op_f16_f32(uint32_t h) {
   const _Float16 x = __builtin_bit_cast(_Float16, static_cast<unsigned short>(h));
   uint32_t r = __float_as_uint(static_cast<float>(x));
   if ((h & 0x7c00u) == 0x7c00u && (h & 0x3ffu)) // NaN: payload shifted, not quieted
     r = ((h & 0x8000u) << 16) | 0x7f800000u | ((h & 0x3ffu) << 13);
   return r;
+}
+
+// Widening whose NaN payload is never observed (a following quantize maps
+// every NaN to -128).
+__device__ __forceinline__ float op_f16_f32_value(uint32_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(h)));
 }
 
 __device__ __forceinline__ uint32_t op_f32_bf16(uint32_t b) {
@@ -72,11 +78,19 @@ __device__ __forceinline__ uint32_t op_f32_bf16(uint32_t b) {
   return static_cast<uint32_t>((w + 0x7fffu + ((w >> 16) & 1u)) >> 16);
 }
 
-__device__ __forceinline__ uint32_t op_quant(uint32_t b, float inv) {
-  float y = __uint_as_float(b) * inv;
-  y = __builtin_fmaxf(y, -128.0f); // maxNum: NaN -> -128
+// symmetric_rne: t = fl32(x * inv); maxNum(t, -128) then minNum(t, 127)
+// (NaN -> -128); round half to even. Adding 1.5 * 2^23 rounds the clamped
+// value to the nearest even integer in the low mantissa bits, whose low byte
+// is the two's-complement code (equal to rint + convert on all 2^32 inputs).
+__device__ __forceinline__ uint32_t quant_value(float x, float inv) {
+  float y = x * inv;
+  y = __builtin_fmaxf(y, -128.0f);
   y = __builtin_fminf(y, 127.0f);
-  return static_cast<uint32_t>(static_cast<int32_t>(__builtin_rintf(y))) & 0xffu;
+  return __float_as_uint(y + 12582912.0f) & 0xffu;
+}
+
+__device__ __forceinline__ uint32_t op_quant(uint32_t b, float inv) {
+  return quant_value(__uint_as_float(b), inv);
 }
 
 __device__ __forceinline__ uint32_t op_dequant(uint32_t b, float scale, int32_t zp) {
@@ -353,11 +367,11 @@ __device__ __forceinline__ void chain_vec(const KArgs &a, uint32_t (&v)[V], int6
       const float inv = a.pf[s.scale_off + c];
 #pragma unroll
       for (int e = 0; e < V; ++e)
-        v[e] = op_quant(op_f16_f32(v[e]), inv);
+        v[e] = quant_value(op_f16_f32_value(v[e]), inv);
     } else {
 #pragma unroll
       for (int e = 0; e < V; ++e)
-        v[e] = op_quant(op_f16_f32(v[e]), a.pf[s.scale_off + c + e]);
+        v[e] = quant_value(op_f16_f32_value(v[e]), a.pf[s.scale_off + c + e]);
     }
   } else if constexpr (CH == kChainQuant) {
     stage_vec<V>(a, a.chain.st[0], v, o);
@@ -486,13 +500,21 @@ __device__ __forceinline__ void batch_offsets(const KArgs &a, int64_t rest, int6
   sbase = 0;
   dbase = 0;
   pad = false;
+  uint32_t r32 = static_cast<uint32_t>(rest);
 #pragma unroll
   for (int k = kMaxRank - 1; k >= 0; --k) {
     if (k >= a.nbatch)
       continue;
-    const int64_t e = a.b_ext[k];
-    const int64_t p = rest % e + a.b_lo[k];
-    rest /= e;
+    int64_t ck;
+    if (a.idx32) {
+      const uint32_t q = k > 0 ? fdiv(r32, a.b_div[k]) : 0u;
+      ck = r32 - q * a.b_div[k].d;
+      r32 = q;
+    } else {
+      ck = rest % a.b_ext[k];
+      rest /= a.b_ext[k];
+    }
+    const int64_t p = ck + a.b_lo[k];
     dbase += p * a.b_ds[k];
     const int64_t v = p - a.b_pad[k];
     if (v < 0 || v >= a.b_vext[k])
@@ -520,16 +542,22 @@ __global__ __launch_bounds__(kBlock) void k_transpose(KArgs a) {
   bool unused;
   batch_offsets(a, rest, sbase, dbase, unused); // transposes carry no pads
   const int64_t q0 = a.t_q0 + tq * kTile, c0 = a.t_c0 + tc * kTile;
-  // load: source rows c (stride t_ssc), contiguous q
+  // load: source rows c (stride t_ssc), contiguous q; all loads in flight
+  // before the first LDS write
+  vec4 in[NI];
 #pragma unroll
   for (int j = 0; j < NI; ++j) {
     const int vid = threadIdx.x + j * kBlock;
     const int row = vid / VPRI, cv = vid % VPRI;
-    const vec4 *p = reinterpret_cast<const vec4 *>(
+    in[j] = *reinterpret_cast<const vec4 *>(
         a.src + (sbase + (c0 + row) * a.t_ssc + q0 + cv * VI) * WIN);
-    const vec4 in = *p;
+  }
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    const int vid = threadIdx.x + j * kBlock;
+    const int row = vid / VPRI, cv = vid % VPRI;
     uint32_t v[VI];
-    unpack<WIN, VI>(&in, v);
+    unpack<WIN, VI>(&in[j], v);
 #pragma unroll
     for (int e = 0; e < VI; ++e)
       tile[row * kPitch + cv * VI + e] = v[e];
@@ -566,24 +594,40 @@ __global__ __launch_bounds__(kBlock) void k_interleave(KArgs a) {
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < a.work;
        i += stride) {
-    const int64_t g = i % a.i_ngroups;
+    int64_t g, rest;
+    if (a.idx32) {
+      const uint32_t q = fdiv(static_cast<uint32_t>(i), a.i_ngroups_div);
+      g = static_cast<uint32_t>(i) - q * a.i_ngroups_div.d;
+      rest = q;
+    } else {
+      g = i % a.i_ngroups;
+      rest = i / a.i_ngroups;
+    }
     int64_t sbase, dbase;
     bool pad;
-    batch_offsets(a, i / a.i_ngroups, sbase, dbase, pad);
+    batch_offsets(a, rest, sbase, dbase, pad);
     const int64_t p0 = a.i_p0 + g * G; // pixel axis is unpadded
-    uint32_t px[CP][G];
+    // every plane's load is issued before any is used, so a thread keeps all
+    // of them in flight at once
+    vec4 in[CP];
+    bool valid[CP];
 #pragma unroll
     for (int ch = 0; ch < CP; ++ch) {
       const int64_t vc = ch - a.i_loc;
-      if (pad || vc < 0 || vc >= a.i_vc) {
+      valid[ch] = !pad && vc >= 0 && vc < a.i_vc;
+      if (valid[ch])
+        in[ch] = *reinterpret_cast<const vec4 *>(a.src + (sbase + vc * a.i_ssc + p0) * WIN);
+    }
+    uint32_t px[CP][G];
+#pragma unroll
+    for (int ch = 0; ch < CP; ++ch) {
+      if (!valid[ch]) {
 #pragma unroll
         for (int e = 0; e < G; ++e)
           px[ch][e] = static_cast<uint32_t>(a.fill);
       } else {
-        const vec4 in =
-            *reinterpret_cast<const vec4 *>(a.src + (sbase + vc * a.i_ssc + p0) * WIN);
         uint32_t v[G];
-        unpack<WIN, G>(&in, v);
+        unpack<WIN, G>(&in[ch], v);
         chain_vec<CH, G>(a, v, 0);
 #pragma unroll
         for (int e = 0; e < G; ++e)

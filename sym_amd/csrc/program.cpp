@@ -535,6 +535,7 @@ KArgs box_args(const DeviceProgram &dp, int64_t v0, int64_t v1, bool first, bool
       a.b_vext[n] = a.vext[i];
       a.b_ss[n] = a.ss[i];
       a.b_ds[n] = a.ds[i];
+      a.b_div[n] = make_div(a.box_ext[i]);
       ++n;
     }
     a.nbatch = n;
@@ -565,6 +566,7 @@ KArgs box_args(const DeviceProgram &dp, int64_t v0, int64_t v1, bool first, bool
     const int pa = r - 2, ca = r - 1;
     batch(pa, ca);
     a.i_ngroups = a.box_ext[pa] / a.vec;
+    a.i_ngroups_div = make_div(a.i_ngroups);
     a.i_p0 = a.box_lo[pa];
     a.i_ssc = a.ss[ca];
     a.i_loc = a.lo[ca];

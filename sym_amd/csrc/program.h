@@ -125,12 +125,14 @@ struct KArgs {
   int64_t b_vext[kMaxRank]; // valid extent
   int64_t b_ss[kMaxRank];
   int64_t b_ds[kMaxRank];
+  FastDiv b_div[kMaxRank];
   // transpose: source-inner axis q (destination rows) and destination-inner c
   int64_t t_nq, t_nc;   // tiles along q and c in this box
   int64_t t_q0, t_c0;   // box start along q and c
   int64_t t_ssc, t_dsq; // source stride of c, destination stride of q
   // interleave: pixel axis p (source-contiguous) and channel axis c
   int64_t i_ngroups;   // pixel groups in the box
+  FastDiv i_ngroups_div;
   int64_t i_p0;        // box start along p
   int64_t i_ssc;       // plane stride (source stride of c)
   int64_t i_loc, i_vc; // leading pad and valid extent of c
