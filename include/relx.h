@@ -218,6 +218,17 @@ int relx_relayout_device(relx_ctx *ctx, const relx_bound *bound, int wire_bounda
 int relx_host_stage(const relx_bound *bound, int host_stages, const void *src, void *wire,
                     int threads, relx_err *err);
 
+/* Host-side check of every kernel launch relx_execute_h2d would make for
+ * this bound plan with the wire at `wire_boundary` and chunks of
+ * `chunk_bytes` (0 = the default), and of relx_relayout_device's launch:
+ * every access inside the wire and the result, 16-byte vectors aligned,
+ * every parameter index inside its table. Runs on the CPU with no device.
+ * `launches` (optional) receives the number checked. The same check runs
+ * before every launch when the environment variable RELX_VERIFY_LAUNCHES is
+ * set. No counterpart in the reference: it backs this library's tests. */
+int relx_verify_launches(const relx_bound *bound, int wire_boundary, int64_t chunk_bytes,
+                         int64_t *launches, relx_err *err);
+
 /* Block until every call on the context has completed. */
 int relx_ctx_synchronize(relx_ctx *ctx, relx_err *err);
 

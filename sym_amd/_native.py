@@ -96,6 +96,7 @@ SIGNATURES = {
                                     ctypes.POINTER(relx_report), _E]),
     "relx_relayout_device": (_I, [_VP, _VP, _I, _VP, _VP, _U64, _E]),
     "relx_host_stage": (_I, [_VP, _I, _VP, _VP, _I, _E]),
+    "relx_verify_launches": (_I, [_VP, _I, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64), _E]),
     "relx_ctx_synchronize": (_I, [_VP, _E]),
     "relx_host_alloc": (_I, [_SZ, ctypes.POINTER(_VP), _E]),
     "relx_host_free": (_I, [_VP]),

@@ -300,6 +300,20 @@ int relx_relayout_device(relx_ctx *ctx, const relx_bound *bound, int wire_bounda
   });
 }
 
+int relx_verify_launches(const relx_bound *bound, int wire_boundary, int64_t chunk_bytes,
+                         int64_t *launches, relx_err *err) {
+  return guarded(err, [&] {
+    if (!bound)
+      throw relx::Error("invalid_argument", "null argument");
+    if (wire_boundary < 0)
+      throw relx::Error("invalid_boundary", "negative wire boundary");
+    const int64_t n = relx::verify_launches(const_cast<relx::BoundHandle &>(bound->h),
+                                            static_cast<uint32_t>(wire_boundary), chunk_bytes);
+    if (launches)
+      *launches = n;
+  });
+}
+
 int relx_host_stage(const relx_bound *bound, int host_stages, const void *src, void *wire,
                     int threads, relx_err *err) {
   return guarded(err, [&] {

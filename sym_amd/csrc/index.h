@@ -1,0 +1,62 @@
+// index.h - index arithmetic shared by the fast kernels and the host-side
+// launch verifier (program.cpp), so both derive exactly the same offsets.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "program.h"
+
+namespace relx {
+
+// n / d for n < 2^32: q = (umulhi(n, m) + n) >> s.
+__host__ __device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv &f) {
+  const uint32_t hi = static_cast<uint32_t>((static_cast<uint64_t>(n) * f.m) >> 32);
+  return static_cast<uint32_t>((static_cast<uint64_t>(hi) + n) >> f.s);
+}
+
+// Parameter entry of a stage for dense result offset `o` (fast kernels:
+// the result has fewer than 2^32 elements whenever a stage is per-channel;
+// per-tensor stages carry rs = re = 1, which yields entry 0 for any o).
+__host__ __device__ __forceinline__ uint32_t chan_of(const DevStage &s, int64_t o) {
+  const uint32_t q = fdiv(static_cast<uint32_t>(o), s.ch_rs_div);
+  return q - fdiv(q, s.ch_re_div) * s.ch_re_div.d;
+}
+
+// Decompose box-relative work index `i` over levels lv[0..L) (lv[0]
+// outermost, needing no division) into source/destination offsets added to
+// sof/dof. Returns true when any coordinate lies in a pad.
+template <int L>
+__host__ __device__ __forceinline__ bool decompose(const Level *lv, uint32_t i, int64_t &sof,
+                                                   int64_t &dof) {
+  bool pad = false;
+  uint32_t rem = i;
+#pragma unroll
+  for (int k = L - 1; k >= 0; --k) {
+    uint32_t u = rem;
+    if (k > 0) {
+      const uint32_t q = fdiv(rem, lv[k].div);
+      u = rem - q * lv[k].div.d;
+      rem = q;
+    }
+    const int64_t uu = static_cast<int64_t>(u);
+    pad |= static_cast<uint64_t>(uu - lv[k].vmin) >= static_cast<uint64_t>(lv[k].vext);
+    sof += uu * lv[k].ss;
+    dof += uu * lv[k].ds;
+  }
+  return pad;
+}
+
+// Map a linear block id so that the blocks one XCD runs (ids congruent mod 8)
+// take a contiguous run of tiles: neighbouring tiles share source cache lines.
+__host__ __device__ __forceinline__ uint32_t xcd_tile(uint32_t b, uint32_t n) {
+  constexpr uint32_t kXcd = 8;
+  if (n < kXcd)
+    return b;
+  const uint32_t per = n / kXcd, extra = n % kXcd, x = b % kXcd, j = b / kXcd;
+  // XCD x owns tiles [x*per + min(x, extra), ...) of length per + (x < extra)
+  return x * per + (x < extra ? x : extra) + j;
+}
+
+} // namespace relx

@@ -18,14 +18,16 @@
 //   interleave planar -> interleaved with a small padded inner axis
 //              (NCHW -> NHWC + pad): per-plane 16-byte loads, packed pixels
 // The common stage sequences get a compile-time body (ChainCode); the rest
-// dispatch per stage. Plain (cached) global accesses throughout: on gfx950
-// nontemporal stores of multi-vector lanes measured ~40% slower.
+// dispatch per stage. Fast kernels index in 32 bits relative to their launch
+// box (the host splits boxes of 2^31 or more work items) and form 64-bit
+// element offsets from the per-level strides.
 #pragma once
 
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
 
+#include "index.h"
 #include "program.h"
 
 namespace relx {
@@ -36,10 +38,6 @@ constexpr int kBlock = 256;
 // Native 16-byte vector.
 typedef uint32_t vec4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv &f) {
-  const uint32_t hi = __umulhi(n, f.m);
-  return static_cast<uint32_t>((static_cast<uint64_t>(hi) + n) >> f.s);
-}
 
 // ------------------------------------------------------------ value ops
 
@@ -116,15 +114,27 @@ __device__ __forceinline__ uint32_t apply(const DevStage &s, uint32_t x, uint32_
   }
 }
 
-// Parameter entry of a kChanDim stage for dense result offset `o`.
-__device__ __forceinline__ uint32_t chan_of(const DevStage &s, int64_t o, int idx32) {
-  if (s.mode != kChanDim)
-    return 0u;
-  if (idx32) {
-    const uint32_t q = fdiv(static_cast<uint32_t>(o), s.ch_rs_div);
-    return q - fdiv(q, s.ch_re_div) * s.ch_re_div.d;
-  }
-  return static_cast<uint32_t>((o / s.ch_rs) % s.ch_re);
+// Cache policy of the fast kernels' global accesses (nontemporal or not),
+// per family and element widths.
+#ifndef RELX_NT_LOAD
+#define RELX_NT_LOAD(FAM, WIN, WOUT) false
+#endif
+#ifndef RELX_NT_STORE
+#define RELX_NT_STORE(FAM, WIN, WOUT) false
+#endif
+
+template <bool NT> __device__ __forceinline__ vec4 ld16(const vec4 *p) {
+  if constexpr (NT)
+    return __builtin_nontemporal_load(p);
+  else
+    return *p;
+}
+
+template <bool NT> __device__ __forceinline__ void st16(vec4 *p, const vec4 &v) {
+  if constexpr (NT)
+    __builtin_nontemporal_store(v, p);
+  else
+    *p = v;
 }
 
 // --------------------------------------------------------- element access
@@ -199,7 +209,7 @@ __device__ int64_t eval_channel(const KArgs &a, const DevStage &s, int64_t o) {
 // One element per thread; runtime indices are fine here (correctness path).
 __global__ __launch_bounds__(kBlock) __attribute__((unused)) void k_generic(KArgs a, int32_t *status) {
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < a.work;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < a.work64;
        i += stride) {
     int64_t rem = i, dof = 0, sof = 0;
     bool pad = false;
@@ -216,7 +226,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((unused)) void k_generic(KArg
     }
     uint64_t x;
     if (pad) {
-      x = a.fill;
+      x = a.fill64;
     } else {
       x = load_el(a.src + sof * a.win, a.win);
       for (int k = 0; k < a.chain.n; ++k) {
@@ -280,7 +290,7 @@ __device__ __forceinline__ void pack(const uint32_t (&v)[V], vec4 *out) {
 template <int V>
 __device__ __forceinline__ void stage_vec(const KArgs &a, const DevStage &s, uint32_t (&v)[V],
                                           int64_t o) {
-  const uint32_t c = chan_of(s, o, a.idx32);
+  const uint32_t c = chan_of(s, o);
   switch (s.op) {
   case kOpF32toF16:
 #pragma unroll
@@ -345,7 +355,7 @@ __device__ __forceinline__ void chain_vec(const KArgs &a, uint32_t (&v)[V], int6
       v[e] = op_f16_f32(v[e]);
   } else if constexpr (CH == kChainDeqF16) {
     const DevStage &s = a.chain.st[0];
-    const uint32_t c = chan_of(s, o, a.idx32);
+    const uint32_t c = chan_of(s, o);
     if (s.vec == 0) {
       const float sc = a.pf[s.scale_off + c];
       const int32_t zp = a.pi[s.zp_off + (s.zp_per_ch ? c : 0u)];
@@ -362,7 +372,7 @@ __device__ __forceinline__ void chain_vec(const KArgs &a, uint32_t (&v)[V], int6
     stage_vec<V>(a, a.chain.st[0], v, o);
   } else if constexpr (CH == kChainF16Quant) {
     const DevStage &s = a.chain.st[1];
-    const uint32_t c = chan_of(s, o, a.idx32);
+    const uint32_t c = chan_of(s, o);
     if (s.vec == 0) {
       const float inv = a.pf[s.scale_off + c];
 #pragma unroll
@@ -387,85 +397,30 @@ __device__ __forceinline__ void chain_vec(const KArgs &a, uint32_t (&v)[V], int6
 
 // ---------------------------------------------------------------- stream
 
-// Box decomposition of vector `i` into padded coordinates (the innermost
-// box coordinate counts vectors of `inner_mul` elements). RANK > 0 fixes the
-// rank at compile time; 0 reads it. Returns true when any coordinate lies in
-// a pad. Loops are unrolled over kMaxRank so every argument index is static.
-template <int RANK>
-__device__ __forceinline__ bool locate(const KArgs &a, int64_t i, int inner_mul, int64_t &sof,
-                                       int64_t &dof) {
-  constexpr int KMAX = RANK > 0 ? RANK : kMaxRank;
-  const int rank = RANK > 0 ? RANK : a.rank;
-  bool pad = false;
-  sof = 0;
-  dof = 0;
-  if (a.idx32) {
-    uint32_t rem = static_cast<uint32_t>(i);
-#pragma unroll
-    for (int k = KMAX - 1; k >= 0; --k) {
-      if (RANK == 0 && k >= rank)
-        continue;
-      uint32_t ck = rem;
-      if (k > 0) { // the outermost axis needs no division
-        const uint32_t q = fdiv(rem, a.box_div[k]);
-        ck = rem - q * a.box_div[k].d;
-        rem = q;
-      }
-      if (k == rank - 1)
-        ck *= inner_mul;
-      const int64_t p = static_cast<int64_t>(ck) + a.box_lo[k];
-      dof += p * a.ds[k];
-      const int64_t v = p - a.lo[k];
-      if (v < 0 || v >= a.vext[k])
-        pad = true;
-      else
-        sof += v * a.ss[k];
-    }
-  } else {
-    int64_t rem = i;
-#pragma unroll
-    for (int k = KMAX - 1; k >= 0; --k) {
-      if (RANK == 0 && k >= rank)
-        continue;
-      const int64_t e = k == rank - 1 ? a.box_ext[k] / inner_mul : a.box_ext[k];
-      int64_t ck = rem % e;
-      rem /= e;
-      if (k == rank - 1)
-        ck *= inner_mul;
-      const int64_t p = ck + a.box_lo[k];
-      dof += p * a.ds[k];
-      const int64_t v = p - a.lo[k];
-      if (v < 0 || v >= a.vext[k])
-        pad = true;
-      else
-        sof += v * a.ss[k];
-    }
-  }
-  return pad;
-}
-
 // One vector of V = 16/min(width) elements per thread: the narrower side
 // moves exactly 16 bytes and the wider side 32 or 64, all lane-contiguous.
-template <int WIN, int WOUT, int RANK, int CH>
+// The innermost level counts vectors.
+template <int WIN, int WOUT, int L, int CH>
 __global__ __launch_bounds__(kBlock) void k_stream(KArgs a) {
   constexpr int V = 16 / (WIN < WOUT ? WIN : WOUT);
   constexpr int NI = V * WIN / 16, NO = V * WOUT / 16;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < a.work;
-       i += stride) {
-    int64_t sof, dof;
-    const bool pad = locate<RANK>(a, i, V, sof, dof);
+  constexpr bool NTL = RELX_NT_LOAD(kFamStream, WIN, WOUT);
+  constexpr bool NTS = RELX_NT_STORE(kFamStream, WIN, WOUT);
+  const uint32_t stride = gridDim.x * kBlock;
+  for (uint32_t i = blockIdx.x * kBlock + threadIdx.x; i < a.work; i += stride) {
+    int64_t sof = a.sbase, dof = a.dbase;
+    const bool pad = decompose<L>(a.lv, i, sof, dof);
     uint32_t v[V];
     if (pad) {
 #pragma unroll
       for (int e = 0; e < V; ++e)
-        v[e] = static_cast<uint32_t>(a.fill);
+        v[e] = a.fill;
     } else {
       vec4 in[NI];
       const vec4 *src = reinterpret_cast<const vec4 *>(a.src + sof * WIN);
 #pragma unroll
       for (int j = 0; j < NI; ++j)
-        in[j] = src[j];
+        in[j] = ld16<NTL>(src + j);
       unpack<WIN, V>(in, v);
       chain_vec<CH, V>(a, v, dof);
     }
@@ -474,7 +429,7 @@ __global__ __launch_bounds__(kBlock) void k_stream(KArgs a) {
     vec4 *dst = reinterpret_cast<vec4 *>(a.dst + dof * WOUT);
 #pragma unroll
     for (int j = 0; j < NO; ++j)
-      dst[j] = out[j];
+      st16<NTS>(dst + j, out[j]);
   }
 }
 
@@ -483,65 +438,26 @@ __global__ __launch_bounds__(kBlock) void k_stream(KArgs a) {
 constexpr int kTile = 64;
 constexpr int kPitch = kTile + 1;
 
-// Map a linear block id so that the blocks one XCD runs (ids congruent mod 8)
-// take a contiguous run of tiles: neighbouring tiles share source cache lines.
-__device__ __forceinline__ uint32_t xcd_tile(uint32_t b, uint32_t n) {
-  constexpr uint32_t kXcd = 8;
-  if (n < kXcd)
-    return b;
-  const uint32_t per = n / kXcd, extra = n % kXcd, x = b % kXcd, j = b / kXcd;
-  // XCD x owns tiles [x*per + min(x, extra), ...) of length per + (x < extra)
-  return x * per + (x < extra ? x : extra) + j;
-}
-
-// Batch offsets of linear batch index `rest` (row-major over b_ext).
-__device__ __forceinline__ void batch_offsets(const KArgs &a, int64_t rest, int64_t &sbase,
-                                              int64_t &dbase, bool &pad) {
-  sbase = 0;
-  dbase = 0;
-  pad = false;
-  uint32_t r32 = static_cast<uint32_t>(rest);
-#pragma unroll
-  for (int k = kMaxRank - 1; k >= 0; --k) {
-    if (k >= a.nbatch)
-      continue;
-    int64_t ck;
-    if (a.idx32) {
-      const uint32_t q = k > 0 ? fdiv(r32, a.b_div[k]) : 0u;
-      ck = r32 - q * a.b_div[k].d;
-      r32 = q;
-    } else {
-      ck = rest % a.b_ext[k];
-      rest /= a.b_ext[k];
-    }
-    const int64_t p = ck + a.b_lo[k];
-    dbase += p * a.b_ds[k];
-    const int64_t v = p - a.b_pad[k];
-    if (v < 0 || v >= a.b_vext[k])
-      pad = true;
-    else
-      sbase += v * a.b_ss[k];
-  }
-}
-
+// One 64x64 tile per block: [c][q] source rows (q contiguous) into LDS,
+// out as [q][c] destination rows (c contiguous). Stages run on the way out.
 template <int WIN, int WOUT, int CH>
 __global__ __launch_bounds__(kBlock) void k_transpose(KArgs a) {
   __shared__ uint32_t tile[kTile * kPitch]; // [c][q]
   constexpr int VI = 16 / WIN, VO = 16 / WOUT;
   constexpr int VPRI = kTile / VI, VPRO = kTile / VO;
   constexpr int NI = kTile * VPRI / kBlock, NO = kTile * VPRO / kBlock;
+  constexpr bool NTL = RELX_NT_LOAD(kFamTranspose, WIN, WOUT);
+  constexpr bool NTS = RELX_NT_STORE(kFamTranspose, WIN, WOUT);
   const uint32_t t = xcd_tile(blockIdx.x, gridDim.x);
   if (t >= a.work)
     return;
-  int64_t rest = t;
-  const int64_t tq = rest % a.t_nq;
-  rest /= a.t_nq;
-  const int64_t tc = rest % a.t_nc;
-  rest /= a.t_nc;
-  int64_t sbase, dbase;
-  bool unused;
-  batch_offsets(a, rest, sbase, dbase, unused); // transposes carry no pads
-  const int64_t q0 = a.t_q0 + tq * kTile, c0 = a.t_c0 + tc * kTile;
+  const uint32_t r1 = fdiv(t, a.t_nq);
+  const uint32_t tq = t - r1 * a.t_nq.d;
+  const uint32_t r2 = fdiv(r1, a.t_nc);
+  const uint32_t tc = r1 - r2 * a.t_nc.d;
+  int64_t sbase = a.sbase, dbase = a.dbase;
+  decompose<kBatchLevels>(a.lv, r2, sbase, dbase); // transposes carry no pads
+  const int64_t q0 = static_cast<int64_t>(tq) * kTile, c0 = static_cast<int64_t>(tc) * kTile;
   // load: source rows c (stride t_ssc), contiguous q; all loads in flight
   // before the first LDS write
   vec4 in[NI];
@@ -549,8 +465,8 @@ __global__ __launch_bounds__(kBlock) void k_transpose(KArgs a) {
   for (int j = 0; j < NI; ++j) {
     const int vid = threadIdx.x + j * kBlock;
     const int row = vid / VPRI, cv = vid % VPRI;
-    in[j] = *reinterpret_cast<const vec4 *>(
-        a.src + (sbase + (c0 + row) * a.t_ssc + q0 + cv * VI) * WIN);
+    in[j] = ld16<NTL>(reinterpret_cast<const vec4 *>(
+        a.src + (sbase + (c0 + row) * a.t_ssc + q0 + cv * VI) * WIN));
   }
 #pragma unroll
   for (int j = 0; j < NI; ++j) {
@@ -567,16 +483,16 @@ __global__ __launch_bounds__(kBlock) void k_transpose(KArgs a) {
 #pragma unroll
   for (int j = 0; j < NO; ++j) {
     const int vid = threadIdx.x + j * kBlock;
-    const int q = vid / VPRO, cv = vid % VPRO;
+    const int row = vid / VPRO, cv = vid % VPRO;
     uint32_t v[VO];
 #pragma unroll
     for (int e = 0; e < VO; ++e)
-      v[e] = tile[(cv * VO + e) * kPitch + q];
-    const int64_t o = dbase + (q0 + q) * a.t_dsq + c0 + cv * VO;
-    chain_vec<CH, VO>(a, v, o);
+      v[e] = tile[(cv * VO + e) * kPitch + row];
+    const int64_t dof = dbase + (q0 + row) * a.t_dsq + c0 + cv * VO;
+    chain_vec<CH, VO>(a, v, dof);
     vec4 out;
     pack<WOUT, VO>(v, &out);
-    *reinterpret_cast<vec4 *>(a.dst + o * WOUT) = out;
+    st16<NTS>(reinterpret_cast<vec4 *>(a.dst + dof * WOUT), out);
   }
 }
 
@@ -591,32 +507,26 @@ __global__ __launch_bounds__(kBlock) void k_interleave(KArgs a) {
   constexpr int G = 16 / WIN;
   constexpr int NO = G * CP * WOUT / 16;
   static_assert(G * CP * WOUT % 16 == 0, "packed pixels must fill whole vectors");
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < a.work;
-       i += stride) {
-    int64_t g, rest;
-    if (a.idx32) {
-      const uint32_t q = fdiv(static_cast<uint32_t>(i), a.i_ngroups_div);
-      g = static_cast<uint32_t>(i) - q * a.i_ngroups_div.d;
-      rest = q;
-    } else {
-      g = i % a.i_ngroups;
-      rest = i / a.i_ngroups;
-    }
-    int64_t sbase, dbase;
-    bool pad;
-    batch_offsets(a, rest, sbase, dbase, pad);
-    const int64_t p0 = a.i_p0 + g * G; // pixel axis is unpadded
+  constexpr bool NTL = RELX_NT_LOAD(kFamInterleave, WIN, WOUT);
+  constexpr bool NTS = RELX_NT_STORE(kFamInterleave, WIN, WOUT);
+  const uint32_t stride = gridDim.x * kBlock;
+  for (uint32_t i = blockIdx.x * kBlock + threadIdx.x; i < a.work; i += stride) {
+    const uint32_t rest = fdiv(i, a.i_ng);
+    const uint32_t g = i - rest * a.i_ng.d;
+    int64_t sbase = a.sbase, dbase = a.dbase;
+    const bool pad = decompose<kBatchLevels>(a.lv, rest, sbase, dbase);
+    const int64_t p0 = static_cast<int64_t>(g) * G; // pixel axis is unpadded
     // every plane's load is issued before any is used, so a thread keeps all
     // of them in flight at once
     vec4 in[CP];
     bool valid[CP];
 #pragma unroll
     for (int ch = 0; ch < CP; ++ch) {
-      const int64_t vc = ch - a.i_loc;
-      valid[ch] = !pad && vc >= 0 && vc < a.i_vc;
+      const int32_t vc = ch - a.i_loc;
+      valid[ch] = !pad && static_cast<uint32_t>(vc) < static_cast<uint32_t>(a.i_vc);
       if (valid[ch])
-        in[ch] = *reinterpret_cast<const vec4 *>(a.src + (sbase + vc * a.i_ssc + p0) * WIN);
+        in[ch] = ld16<NTL>(
+            reinterpret_cast<const vec4 *>(a.src + (sbase + vc * a.i_ssc + p0) * WIN));
     }
     uint32_t px[CP][G];
 #pragma unroll
@@ -624,7 +534,7 @@ __global__ __launch_bounds__(kBlock) void k_interleave(KArgs a) {
       if (!valid[ch]) {
 #pragma unroll
         for (int e = 0; e < G; ++e)
-          px[ch][e] = static_cast<uint32_t>(a.fill);
+          px[ch][e] = a.fill;
       } else {
         uint32_t v[G];
         unpack<WIN, G>(&in[ch], v);
@@ -645,15 +555,16 @@ __global__ __launch_bounds__(kBlock) void k_interleave(KArgs a) {
     vec4 *dst = reinterpret_cast<vec4 *>(a.dst + (dbase + p0 * CP) * WOUT);
 #pragma unroll
     for (int j = 0; j < NO; ++j)
-      dst[j] = out[j];
+      st16<NTS>(dst + j, out[j]);
   }
 }
 
 // ------------------------------------------------------------ launch
 
 // One work item per thread up to 2^22 blocks (2^30 work-items per launch,
-// inside HIP's 2^32 limit); larger launches grid-stride.
-unsigned grid_for(int64_t work) {
+// inside HIP's 2^32 limit); larger launches grid-stride. Fast-kernel work
+// stays below 2^31, so a 32-bit index plus the grid stride cannot wrap.
+__attribute__((unused)) unsigned grid_for(int64_t work) {
   const int64_t blocks = (work + kBlock - 1) / kBlock;
   return static_cast<unsigned>(blocks < (1 << 22) ? (blocks > 0 ? blocks : 1) : (1 << 22));
 }
@@ -661,21 +572,21 @@ unsigned grid_for(int64_t work) {
 template <int WIN, int WOUT, int CH>
 hipError_t stream_launch(const KArgs &a, hipStream_t s) {
   const dim3 grid(grid_for(a.work)), block(kBlock);
-  switch (a.rank) {
+  switch (a.nlev) {
   case 1:
     hipLaunchKernelGGL((k_stream<WIN, WOUT, 1, CH>), grid, block, 0, s, a);
     break;
   case 2:
     hipLaunchKernelGGL((k_stream<WIN, WOUT, 2, CH>), grid, block, 0, s, a);
     break;
-  case 3:
-    hipLaunchKernelGGL((k_stream<WIN, WOUT, 3, CH>), grid, block, 0, s, a);
-    break;
   case 4:
     hipLaunchKernelGGL((k_stream<WIN, WOUT, 4, CH>), grid, block, 0, s, a);
     break;
+  case 8:
+    hipLaunchKernelGGL((k_stream<WIN, WOUT, 8, CH>), grid, block, 0, s, a);
+    break;
   default:
-    hipLaunchKernelGGL((k_stream<WIN, WOUT, 0, CH>), grid, block, 0, s, a);
+    return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }

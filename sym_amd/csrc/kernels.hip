@@ -8,7 +8,7 @@ namespace relx {
 // Launch one box of a program. `status` is a device int the generic kernel
 // sets when a channel index falls outside its parameter table.
 hipError_t launch_box(int family, const KArgs &a, int32_t *status, hipStream_t s) {
-  if (a.work <= 0)
+  if (a.work64 <= 0)
     return hipSuccess;
   bool handled = false;
   hipError_t e = hipSuccess;
@@ -23,7 +23,7 @@ hipError_t launch_box(int family, const KArgs &a, int32_t *status, hipStream_t s
     e = interleave_fast(a, s, handled);
     return handled ? e : interleave_generic(a, s);
   default:
-    hipLaunchKernelGGL(k_generic, dim3(grid_for(a.work)), dim3(kBlock), 0, s, a, status);
+    hipLaunchKernelGGL(k_generic, dim3(grid_for(a.work64)), dim3(kBlock), 0, s, a, status);
     return hipGetLastError();
   }
 }

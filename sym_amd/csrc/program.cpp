@@ -11,7 +11,10 @@
 #include "runtime.h"
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
+
+#include "index.h"
 
 namespace relx {
 
@@ -295,7 +298,8 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
   }
   uint64_t fill = 0;
   a.has_fill = fill_at(b, p, nst, fill) ? 1 : 0;
-  a.fill = fill;
+  a.fill64 = fill;
+  a.fill = static_cast<uint32_t>(fill);
 
   // result coordinates (channels); layout plans have none
   a.res_rank = static_cast<int32_t>(b.result_extents.size());
@@ -315,11 +319,15 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
     DevStage &d = ch.st[i - k];
     d.op = h.op;
     d.mode = h.mode;
+    d.ch_rs_div = make_div(1); // per tensor: entry 0
+    d.ch_re_div = make_div(1);
     if (h.mode == kChanDim) {
       d.ch_rs = p.res_strides[static_cast<size_t>(h.dim)];
       d.ch_re = b.result_extents[static_cast<size_t>(h.dim)];
-      d.ch_rs_div = make_div(d.ch_rs);
-      d.ch_re_div = make_div(d.ch_re);
+      if (d.ch_rs < (int64_t{1} << 32) && d.ch_re < (int64_t{1} << 32)) {
+        d.ch_rs_div = make_div(d.ch_rs);
+        d.ch_re_div = make_div(d.ch_re);
+      }
     }
     d.len = static_cast<uint32_t>(h.len);
     d.scale_off = static_cast<uint32_t>(dp->pf.size());
@@ -380,10 +388,12 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
   const bool dense = dense_dst(L, pext);
   int family = kFamGeneric;
   const int V = widths_ok ? 16 / std::min(win, wout) : 0;
+  // per-channel stages in the fast kernels index with a 32-bit result offset
+  const bool off32 = dp->dst_elems < (int64_t{1} << 32);
   auto channels_ok = [&](int64_t vlen) {
     for (uint32_t i = k; i < nst; ++i) {
       const int m = vec_mode(p.stages[i], p, b, vlen);
-      if (m < 0)
+      if (m < 0 || (p.stages[i].mode == kChanDim && !off32))
         return false;
       ch.st[i - k].vec = static_cast<uint8_t>(m);
     }
@@ -398,11 +408,12 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
       if (ok && channels_ok(V)) {
         family = kFamStream;
         a.vec = V;
+        a.nlev = r <= 1 ? 1 : r <= 2 ? 2 : r <= 4 ? 4 : 8;
       }
     }
     // transpose: dst-inner axis has a source stride, another axis is
     // source-contiguous; tile-aligned extents, no pads
-    if (family == kFamGeneric && !any_pad && r >= 2 && a.ss[r - 1] != 1) {
+    if (family == kFamGeneric && !any_pad && r >= 2 && r - 2 <= kBatchLevels && a.ss[r - 1] != 1) {
       int qa = -1;
       for (int i = 0; i < r - 1; ++i)
         if (a.ss[i] == 1 && a.vext[i] > 1)
@@ -427,8 +438,8 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
       }
     }
     // interleave: [batch..., P, C(pad)] planar source
-    if (family == kFamGeneric && r >= 2 && a.ss[r - 1] != 1 && a.ss[r - 2] == 1 &&
-        a.ds[r - 2] == pext[static_cast<size_t>(r - 1)]) {
+    if (family == kFamGeneric && r >= 2 && r - 2 <= kBatchLevels && a.ss[r - 1] != 1 &&
+        a.ss[r - 2] == 1 && a.ds[r - 2] == pext[static_cast<size_t>(r - 1)]) {
       const int64_t cp = pext[static_cast<size_t>(r - 1)];
       const int G = 16 / win;
       bool pa_pad = lo[static_cast<size_t>(r - 2)] != 0 || pext[static_cast<size_t>(r - 2)] != a.vext[r - 2];
@@ -497,93 +508,394 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
           dp->chunk_align = 64;
         else if (family == kFamInterleave && ax == r - 2)
           dp->chunk_align = a.vec;
+        // an interleave launch writes every channel of its pixels, so its
+        // boxes never split the channel axis
+        if (family == kFamInterleave && ax == r - 1)
+          dp->chunk_axis = -1;
       }
     }
   }
   return dp;
 }
 
-// Launch arguments for valid coordinates [v0, v1) of the chunk axis (the
-// whole box when the axis is -1). The first/last chunk also cover the axis'
-// leading/trailing pad.
-KArgs box_args(const DeviceProgram &dp, int64_t v0, int64_t v1, bool first, bool last) {
+namespace {
+
+struct Box {
+  int64_t lo[kMaxRank], ext[kMaxRank];
+};
+
+// Work items of a box for the program's family.
+int64_t box_work(const DeviceProgram &dp, const Box &b) {
+  const KArgs &a = dp.base;
+  const int r = a.rank;
+  int64_t n = 1;
+  for (int i = 0; i < r; ++i) {
+    int64_t e = b.ext[i];
+    if (dp.family == kFamStream && i == r - 1)
+      e /= a.vec;
+    else if (dp.family == kFamTranspose && (i == dp.qa || i == dp.ca))
+      e /= 64;
+    else if (dp.family == kFamInterleave && i == r - 2)
+      e /= a.vec;
+    else if (dp.family == kFamInterleave && i == r - 1)
+      e = 1;
+    n *= e;
+  }
+  return n;
+}
+
+// Coordinates a split of axis i must keep together (0: never split).
+int64_t split_align(const DeviceProgram &dp, int i) {
+  const int r = dp.base.rank;
+  if (dp.family == kFamStream && i == r - 1)
+    return dp.base.vec;
+  if (dp.family == kFamTranspose && (i == dp.qa || i == dp.ca))
+    return 64;
+  if (dp.family == kFamInterleave && i == r - 2)
+    return dp.base.vec;
+  if (dp.family == kFamInterleave && i == r - 1)
+    return 0;
+  return 1;
+}
+
+// Split a fast-family box into boxes of fewer than 2^31 work items along the
+// outermost splittable axis (recursing inwards when one slab is too large).
+void split_box(const DeviceProgram &dp, const Box &b, std::vector<Box> &out) {
+  const int64_t w = box_work(dp, b);
+  if (dp.family == kFamGeneric || w < kMaxLaunchWork) {
+    out.push_back(b);
+    return;
+  }
+  for (int i = 0; i < dp.base.rank; ++i) {
+    const int64_t al = split_align(dp, i);
+    if (al == 0 || b.ext[i] <= al)
+      continue;
+    const int64_t groups = b.ext[i] / al; // the box extent is a multiple of al
+    const int64_t per = w / groups;       // work items per aligned group
+    const int64_t take = std::max<int64_t>(1, (kMaxLaunchWork - 1) / per) * al;
+    for (int64_t o = 0; o < b.ext[i]; o += take) {
+      Box c = b;
+      c.lo[i] = b.lo[i] + o;
+      c.ext[i] = std::min(take, b.ext[i] - o);
+      split_box(dp, c, out);
+    }
+    return;
+  }
+  fail("unsupported_layout", "a launch box cannot be split below 2^31 work items");
+}
+
+Level trivial_level() {
+  Level l{};
+  l.div = make_div(1);
+  l.vmin = 0;
+  l.vext = 1;
+  return l;
+}
+
+// Level of axis i counting units of `unit` coordinates (unit > 1 only on
+// unpadded axes whose box start is a multiple of unit).
+Level axis_level(const KArgs &a, const Box &b, int i, int64_t unit) {
+  Level l{};
+  l.div = make_div(b.ext[i] / unit);
+  l.ss = a.ss[i] * unit;
+  l.ds = a.ds[i] * unit;
+  l.vmin = (a.lo[i] - b.lo[i]) / unit;
+  l.vext = a.vext[i] / unit;
+  return l;
+}
+
+KArgs launch_args(const DeviceProgram &dp, const Box &b) {
   KArgs a = dp.base;
   const int r = a.rank;
   for (int i = 0; i < r; ++i) {
-    a.box_lo[i] = 0;
-    a.box_ext[i] = a.pext[i];
+    a.box_lo[i] = b.lo[i];
+    a.box_ext[i] = b.ext[i];
+  }
+  // box origin: destination offset of its first padded coordinate, source
+  // offset of the valid coordinate it corresponds to (interleave channels are
+  // addressed by the kernel itself)
+  a.sbase = 0;
+  a.dbase = 0;
+  for (int i = 0; i < r; ++i) {
+    if (dp.family == kFamInterleave && i == r - 1)
+      continue;
+    a.sbase += (b.lo[i] - a.lo[i]) * a.ss[i];
+    a.dbase += b.lo[i] * a.ds[i];
+  }
+  for (int i = 0; i < kMaxRank; ++i)
+    a.lv[i] = trivial_level();
+  const int64_t work = box_work(dp, b);
+  a.work = static_cast<uint32_t>(work);
+  a.work64 = work;
+  // batch levels of the 2-D families: every axis but skip0/skip1, outer first
+  auto batch = [&](int skip0, int skip1) {
+    int idx[kMaxRank], n = 0;
+    for (int i = 0; i < r; ++i)
+      if (i != skip0 && i != skip1)
+        idx[n++] = i;
+    for (int j = 0; j < n; ++j)
+      a.lv[kBatchLevels - n + j] = axis_level(a, b, idx[j], 1);
+  };
+  switch (dp.family) {
+  case kFamStream:
+    for (int i = 0; i < r; ++i)
+      a.lv[a.nlev - r + i] = axis_level(a, b, i, i == r - 1 ? a.vec : 1);
+    break;
+  case kFamTranspose:
+    batch(dp.qa, dp.ca);
+    a.t_nq = make_div(b.ext[dp.qa] / 64);
+    a.t_nc = make_div(b.ext[dp.ca] / 64);
+    a.t_ssc = a.ss[dp.ca];
+    a.t_dsq = a.ds[dp.qa];
+    break;
+  case kFamInterleave:
+    batch(r - 2, r - 1);
+    a.i_ng = make_div(b.ext[r - 2] / a.vec);
+    a.i_ssc = a.ss[r - 1];
+    a.i_loc = static_cast<int32_t>(a.lo[r - 1]);
+    a.i_vc = static_cast<int32_t>(a.vext[r - 1]);
+    break;
+  default: {
+    int64_t n = 1;
+    for (int i = 0; i < r; ++i)
+      n *= b.ext[i];
+    a.work64 = n;
+  }
+  }
+  return a;
+}
+
+} // namespace
+
+// Launch arguments for valid coordinates [v0, v1) of the chunk axis (the
+// whole box when the axis is -1). The first/last chunk also cover the axis'
+// leading/trailing pad. One entry per launch.
+std::vector<KArgs> box_launches(const DeviceProgram &dp, int64_t v0, int64_t v1, bool first,
+                                bool last) {
+  const KArgs &a = dp.base;
+  Box b{};
+  for (int i = 0; i < a.rank; ++i) {
+    b.lo[i] = 0;
+    b.ext[i] = a.pext[i];
   }
   if (dp.chunk_axis >= 0) {
     const int ax = dp.chunk_axis;
     const int64_t plo = first ? 0 : v0 + a.lo[ax];
     const int64_t phi = last ? a.pext[ax] : v1 + a.lo[ax];
-    a.box_lo[ax] = plo;
-    a.box_ext[ax] = phi - plo;
+    b.lo[ax] = plo;
+    b.ext[ax] = phi - plo;
   }
-  int64_t box_total = 1;
-  for (int i = 0; i < r; ++i)
-    box_total *= a.box_ext[i];
-  // the axes outside a 2-D block, outer first (transpose / interleave)
-  auto batch = [&](int skip0, int skip1) {
-    int n = 0;
-    for (int i = 0; i < r; ++i) {
-      if (i == skip0 || i == skip1)
-        continue;
-      a.b_ext[n] = a.box_ext[i];
-      a.b_lo[n] = a.box_lo[i];
-      a.b_pad[n] = a.lo[i];
-      a.b_vext[n] = a.vext[i];
-      a.b_ss[n] = a.ss[i];
-      a.b_ds[n] = a.ds[i];
-      a.b_div[n] = make_div(a.box_ext[i]);
-      ++n;
+  std::vector<Box> boxes;
+  split_box(dp, b, boxes);
+  std::vector<KArgs> out;
+  out.reserve(boxes.size());
+  for (const Box &x : boxes)
+    if (box_work(dp, x) > 0)
+      out.push_back(launch_args(dp, x));
+  return out;
+}
+
+namespace {
+
+[[noreturn]] void bad_launch(const DeviceProgram &dp, const std::string &what) {
+  fail("internal_launch_check", std::string(dp.kernel) + " launch: " + what);
+}
+
+template <int L>
+bool decompose_n(const Level *lv, uint32_t i, int64_t &sof, int64_t &dof) {
+  return decompose<L>(lv, i, sof, dof);
+}
+
+bool decompose_rt(int n, const Level *lv, uint32_t i, int64_t &sof, int64_t &dof) {
+  switch (n) {
+  case 1:
+    return decompose_n<1>(lv, i, sof, dof);
+  case 2:
+    return decompose_n<2>(lv, i, sof, dof);
+  case 3:
+    return decompose_n<3>(lv, i, sof, dof);
+  case 4:
+    return decompose_n<4>(lv, i, sof, dof);
+  default:
+    return decompose_n<8>(lv, i, sof, dof);
+  }
+}
+
+struct Checker {
+  const DeviceProgram &dp;
+  const KArgs &a;
+  int64_t wire, dst; // elements
+  size_t npf, npi;
+
+  void src_run(int64_t off, int64_t n, bool vec16) const {
+    if (off < 0 || off + n > wire)
+      bad_launch(dp, "source run [" + std::to_string(off) + ", " + std::to_string(off + n) +
+                         ") outside " + std::to_string(wire) + " wire elements");
+    if (vec16 && (off * a.win) % 16 != 0)
+      bad_launch(dp, "unaligned 16-byte source access at element " + std::to_string(off));
+  }
+  void dst_run(int64_t off, int64_t n, bool vec16) const {
+    if (off < 0 || off + n > dst)
+      bad_launch(dp, "destination run [" + std::to_string(off) + ", " + std::to_string(off + n) +
+                         ") outside " + std::to_string(dst) + " result elements");
+    if (vec16 && (off * a.wout) % 16 != 0)
+      bad_launch(dp, "unaligned 16-byte destination access at element " + std::to_string(off));
+  }
+  // channels of V consecutive result elements from dense offset o, as the
+  // fast kernels index them (constant, or +1 per element)
+  void channels(int64_t o, int V) const {
+    for (int k = 0; k < a.chain.n; ++k) {
+      const DevStage &s = a.chain.st[k];
+      const uint32_t c = chan_of(s, o);
+      const uint32_t last = chan_of(s, o + V - 1);
+      const uint32_t want = s.vec ? c + static_cast<uint32_t>(V - 1) : c;
+      if (last != want)
+        bad_launch(dp, "channel pattern of stage " + std::to_string(k) + " breaks inside a vector");
+      const bool reads_params = s.op == kOpQuantize || s.op == kOpDequantize;
+      if (want >= s.len ||
+          (reads_params && (s.scale_off + want >= npf ||
+                            s.zp_off + (s.zp_per_ch ? want : 0u) >= npi)))
+        bad_launch(dp, "parameter index outside its table at stage " + std::to_string(k));
     }
-    a.nbatch = n;
-  };
+  }
+};
+
+} // namespace
+
+void verify_launch(const DeviceProgram &dp, const KArgs &a) {
+  const Checker ck{dp, a, dp.wire_elems, dp.dst_elems, dp.pf.size(), dp.pi.size()};
+  const int win = a.win, wout = a.wout;
   switch (dp.family) {
   case kFamStream: {
-    for (int i = 0; i < r; ++i)
-      a.box_div[i] = make_div(i == r - 1 ? a.box_ext[i] / a.vec : a.box_ext[i]);
-    a.work = box_total / a.vec;
+    if (a.work64 >= kMaxLaunchWork || a.work != a.work64)
+      bad_launch(dp, "work above 2^31");
+    const int V = a.vec;
+    for (uint32_t i = 0; i < a.work; ++i) {
+      int64_t sof = a.sbase, dof = a.dbase;
+      const bool pad = decompose_rt(a.nlev, a.lv, i, sof, dof);
+      ck.dst_run(dof, V, true);
+      if (!pad) {
+        ck.src_run(sof, V, true);
+        ck.channels(dof, V);
+      }
+    }
     break;
   }
   case kFamTranspose: {
-    const int qa = dp.qa, ca = dp.ca;
-    batch(qa, ca);
-    a.t_nq = a.box_ext[qa] / 64;
-    a.t_nc = a.box_ext[ca] / 64;
-    a.t_q0 = a.box_lo[qa];
-    a.t_c0 = a.box_lo[ca];
-    a.t_ssc = a.ss[ca];
-    a.t_dsq = a.ds[qa];
-    int64_t n = a.t_nq * a.t_nc;
-    for (int i = 0; i < a.nbatch; ++i)
-      n *= a.b_ext[i];
-    a.work = n;
+    if (a.work64 > (int64_t{1} << 22) || a.work != a.work64)
+      bad_launch(dp, "more tiles than one launch takes");
+    const int VO = 16 / wout;
+    for (uint32_t t = 0; t < a.work; ++t) {
+      const uint32_t r1 = fdiv(t, a.t_nq);
+      const uint32_t tq = t - r1 * a.t_nq.d;
+      const uint32_t r2 = fdiv(r1, a.t_nc);
+      const uint32_t tc = r1 - r2 * a.t_nc.d;
+      int64_t sbase = a.sbase, dbase = a.dbase;
+      if (decompose_rt(kBatchLevels, a.lv, r2, sbase, dbase))
+        bad_launch(dp, "a transpose tile reaches a pad");
+      const int64_t q0 = int64_t{tq} * 64, c0 = int64_t{tc} * 64;
+      for (int row = 0; row < 64; row += 63) {
+        ck.src_run(sbase + (c0 + row) * a.t_ssc + q0, 64, true);
+        ck.dst_run(dbase + (q0 + row) * a.t_dsq + c0, 64, true);
+      }
+      if ((a.t_ssc * win) % 16 != 0 || (a.t_dsq * wout) % 16 != 0)
+        bad_launch(dp, "row strides break 16-byte alignment");
+      for (int row = 0; row < 64; ++row)
+        for (int cv = 0; cv < 64; cv += VO)
+          ck.channels(dbase + (q0 + row) * a.t_dsq + c0 + cv, VO);
+    }
     break;
   }
   case kFamInterleave: {
-    const int pa = r - 2, ca = r - 1;
-    batch(pa, ca);
-    a.i_ngroups = a.box_ext[pa] / a.vec;
-    a.i_ngroups_div = make_div(a.i_ngroups);
-    a.i_p0 = a.box_lo[pa];
-    a.i_ssc = a.ss[ca];
-    a.i_loc = a.lo[ca];
-    a.i_vc = a.vext[ca];
-    int64_t n = a.i_ngroups;
-    for (int i = 0; i < a.nbatch; ++i)
-      n *= a.b_ext[i];
-    a.work = n;
+    if (a.work64 >= kMaxLaunchWork || a.work != a.work64)
+      bad_launch(dp, "work above 2^31");
+    const int G = a.vec, CP = a.cpad;
+    for (int k = 0; k < a.chain.n; ++k)
+      if (a.chain.st[k].mode != kChanNone)
+        bad_launch(dp, "per-channel stage in an interleave program");
+    if ((a.i_ssc * win) % 16 != 0)
+      bad_launch(dp, "plane stride breaks 16-byte alignment");
+    for (uint32_t i = 0; i < a.work; ++i) {
+      const uint32_t rest = fdiv(i, a.i_ng);
+      const uint32_t g = i - rest * a.i_ng.d;
+      int64_t sbase = a.sbase, dbase = a.dbase;
+      const bool pad = decompose_rt(kBatchLevels, a.lv, rest, sbase, dbase);
+      const int64_t p0 = int64_t{g} * G;
+      ck.dst_run(dbase + p0 * CP, int64_t{G} * CP, true);
+      for (int c = 0; c < CP; ++c) {
+        const int32_t vc = c - a.i_loc;
+        if (!pad && static_cast<uint32_t>(vc) < static_cast<uint32_t>(a.i_vc))
+          ck.src_run(sbase + vc * a.i_ssc + p0, G, true);
+      }
+    }
     break;
   }
-  default:
-    for (int i = 0; i < r; ++i)
-      a.box_div[i] = make_div(a.box_ext[i]);
-    a.work = box_total;
+  default: {
+    for (int64_t i = 0; i < a.work64; ++i) {
+      int64_t rem = i, dof = 0, sof = 0;
+      bool pad = false;
+      for (int k = a.rank - 1; k >= 0; --k) {
+        const int64_t p = rem % a.box_ext[k] + a.box_lo[k];
+        rem /= a.box_ext[k];
+        dof += p * a.ds[k];
+        const int64_t v = p - a.lo[k];
+        if (v < 0 || v >= a.vext[k])
+          pad = true;
+        else
+          sof += v * a.ss[k];
+      }
+      ck.dst_run(dof, 1, false);
+      if (!pad)
+        ck.src_run(sof, 1, false);
+    }
   }
-  a.idx32 = (box_total < (int64_t{1} << 32) && dp.dst_elems < (int64_t{1} << 32)) ? 1 : 0;
-  return a;
+  }
+}
+
+namespace {
+
+bool verify_enabled() {
+  static const bool on = [] {
+    const char *v = std::getenv("RELX_VERIFY_LAUNCHES");
+    return v && *v && std::strcmp(v, "0") != 0;
+  }();
+  return on;
+}
+
+} // namespace
+
+int64_t launch_program(const DeviceProgram &dp, int64_t v0, int64_t v1, bool first, bool last,
+                       const void *src, void *dst, const float *pf, const int32_t *pi,
+                       int32_t *status, hipStream_t s) {
+  // the fast kernels move 16-byte vectors: buffers that are not 16-byte
+  // aligned take the element-wise kernel
+  const bool aligned = reinterpret_cast<uintptr_t>(src) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(dst) % 16 == 0;
+  int64_t n = 0;
+  for (KArgs &a : box_launches(dp, v0, v1, first, last)) {
+    int family = dp.family;
+    if (!aligned && family != kFamGeneric) {
+      family = kFamGeneric;
+      int64_t e = 1;
+      for (int i = 0; i < a.rank; ++i)
+        e *= a.box_ext[i];
+      a.work64 = e;
+    }
+    if (verify_enabled()) {
+      DeviceProgram view = dp;
+      view.family = family;
+      verify_launch(view, a);
+    }
+    a.src = static_cast<const uint8_t *>(src);
+    a.dst = static_cast<uint8_t *>(dst);
+    a.pf = pf;
+    a.pi = pi;
+    const hipError_t e = launch_box(family, a, status, s);
+    if (e != hipSuccess)
+      fail("backend_failure", std::string("kernel launch: ") + hipGetErrorString(e));
+    ++n;
+  }
+  return n;
 }
 
 } // namespace relx

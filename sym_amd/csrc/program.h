@@ -7,10 +7,12 @@
 // (padded coordinates), the source strides of the valid region, the pad fill,
 // and the remaining value stages with their per-channel parameters.
 //
-// Every field a kernel reads is addressed with a compile-time index (arrays
-// only inside fully unrolled loops, per-stage and per-family scalars
-// precomputed here): a runtime index into the by-value argument block turns
-// each read into a vector-memory load on the kernel's critical path.
+// Every field a fast kernel reads is addressed with a compile-time index
+// (arrays only inside fully unrolled loops of fixed trip count, per-stage and
+// per-family scalars precomputed here) and read before any branch: a runtime
+// index into the by-value argument block turns a read into a vector-memory
+// load, and a read under a branch serialises its scalar load behind the
+// branch -- both on the kernel's critical path.
 #pragma once
 
 #include <cstdint>
@@ -70,9 +72,12 @@ struct DevStage {
   uint32_t scale_off; // float param index (dequant scale / quant reciprocal)
   uint32_t zp_off;    // int param index
   uint32_t len;       // parameter entries
-  int32_t tok_begin, tok_count;
-  int64_t ch_rs, ch_re; // kChanDim: result stride and extent of the channel dimension
+  // Fast kernels: channel = (o / rs) mod re for a dense result offset o < 2^32;
+  // per-tensor stages carry rs = re = 1 (channel 0).
   FastDiv ch_rs_div, ch_re_div;
+  // Generic kernel: the same map in 64 bits, or a token range (kChanExpr).
+  int64_t ch_rs, ch_re;
+  int32_t tok_begin, tok_count;
 };
 
 struct Chain {
@@ -89,20 +94,55 @@ enum Family : int32_t {
   kFamInterleave = 3, // planar -> interleaved with a small padded inner axis
 };
 
-// Launch arguments. Extents/strides are in elements of the coalesced
-// destination-order axes of the bound layout.
+// Decomposition levels of the batch axes of the 2-D families.
+constexpr int kBatchLevels = 3;
+// Work items per launch of a fast kernel stay below this (32-bit indexing);
+// the host splits larger boxes.
+constexpr int64_t kMaxLaunchWork = int64_t{1} << 31;
+
+// One level of a fast kernel's index decomposition. A box-relative
+// coordinate u in [0, div.d) adds u * ss to the source and u * ds to the
+// destination offset (elements); it lies in the valid (unpadded) region iff
+// (u - vmin) < vext as unsigned 64-bit numbers. Unused outer levels have
+// d = 1 and zero strides.
+struct Level {
+  FastDiv div;
+  int64_t ss, ds;
+  int64_t vmin, vext;
+};
+
+// Launch arguments (by value). The fast families read only the first block,
+// unconditionally at entry, so its scalar loads issue together.
 struct KArgs {
+  // ---- fast families
   const uint8_t *src; // wire (device) at the program's boundary
   uint8_t *dst;       // result (device)
   const float *pf;    // float parameters
   const int32_t *pi;  // int parameters
+  uint32_t work;      // work items of this launch (< 2^31)
+  uint32_t fill;      // pad fill bits (fast families move elements of at most 4 bytes)
+  int64_t sbase, dbase; // element offsets of the box origin (source: of its valid origin)
+  Level lv[kMaxRank];   // stream: box axes (innermost in vectors); 2-D families: batch axes
+  // transpose: tiles along the source-inner axis q (destination rows) and
+  // the destination-inner axis c
+  FastDiv t_nq, t_nc;
+  int64_t t_ssc, t_dsq; // source stride of c, destination stride of q
+  // interleave: pixel groups along the source-contiguous axis p; channel axis c
+  FastDiv i_ng;
+  int64_t i_ssc;        // plane stride (source stride of c)
+  int32_t i_loc, i_vc;  // leading pad and valid extent of c
+  Chain chain;
+  // ---- generic kernel and host bookkeeping (coalesced destination axes)
   int32_t rank;
-  int32_t win, wout;  // element bytes of the wire and of the result
+  int32_t win, wout; // element bytes of the wire and of the result
   int32_t has_fill;
-  uint64_t fill;
-  int32_t idx32;      // every index of this launch fits in 32 bits
   int32_t chain_code;
-  int64_t work;       // work items in this launch
+  int32_t nlev;      // stream: decomposition levels (1, 2, 4 or 8)
+  int32_t cpad;      // interleave: padded inner extent
+  int32_t vec;       // stream: elements per vector; interleave: pixels per thread
+  int32_t res_rank;
+  int64_t work64;    // generic: elements of the box
+  uint64_t fill64;
   int64_t pext[kMaxRank]; // padded extents
   int64_t lo[kMaxRank];   // leading pad per axis
   int64_t vext[kMaxRank]; // valid extents
@@ -110,33 +150,8 @@ struct KArgs {
   int64_t ds[kMaxRank];   // destination strides (padded coordinates)
   int64_t box_lo[kMaxRank];
   int64_t box_ext[kMaxRank];
-  FastDiv box_div[kMaxRank]; // over the work decomposition of each axis
-  // result coordinates for channel expressions (generic kernel)
-  int32_t res_rank;
-  int32_t vec;  // stream: elements per vector; interleave: pixels per thread
-  int64_t rs[kMaxRank];
+  int64_t rs[kMaxRank]; // result strides and extents (channel expressions)
   int64_t re[kMaxRank];
-  // transpose / interleave: the axes outside the 2-D block, outer first
-  int32_t nbatch;
-  int32_t cpad; // interleave: padded inner extent
-  int64_t b_ext[kMaxRank];  // box extent
-  int64_t b_lo[kMaxRank];   // box start (padded coordinate)
-  int64_t b_pad[kMaxRank];  // leading pad
-  int64_t b_vext[kMaxRank]; // valid extent
-  int64_t b_ss[kMaxRank];
-  int64_t b_ds[kMaxRank];
-  FastDiv b_div[kMaxRank];
-  // transpose: source-inner axis q (destination rows) and destination-inner c
-  int64_t t_nq, t_nc;   // tiles along q and c in this box
-  int64_t t_q0, t_c0;   // box start along q and c
-  int64_t t_ssc, t_dsq; // source stride of c, destination stride of q
-  // interleave: pixel axis p (source-contiguous) and channel axis c
-  int64_t i_ngroups;   // pixel groups in the box
-  FastDiv i_ngroups_div;
-  int64_t i_p0;        // box start along p
-  int64_t i_ssc;       // plane stride (source stride of c)
-  int64_t i_loc, i_vc; // leading pad and valid extent of c
-  Chain chain;
 };
 
 } // namespace relx

@@ -351,31 +351,11 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
   ensure_wire(ctx, wire_total);
 
   // Chunk plan per member: units of the chunk axis per chunk.
-  const int64_t default_chunk = int64_t{8} << 20;
-  const int64_t want_chunk = opt.chunk_bytes > 0 ? opt.chunk_bytes : default_chunk;
   size_t max_slot = 0;
-  struct Plan1 {
-    int64_t units, per_chunk, unit_wire, unit_src;
-  };
-  std::vector<Plan1> plans;
+  std::vector<ChunkPlan> plans;
   for (const Member &m : ms) {
     const DeviceProgram &dp = *m.dp;
-    Plan1 p{};
-    const uint32_t sw = m.h->bound->typed ? m.h->bound->source_type.width()
-                                          : m.h->bound->layout.element_size;
-    if (dp.chunk_axis >= 0) {
-      p.units = dp.base.vext[dp.chunk_axis];
-      p.unit_wire = dp.chunk_stride * dp.base.win;
-      p.unit_src = dp.chunk_stride * sw;
-      int64_t per = std::max<int64_t>(1, want_chunk / std::max<int64_t>(1, p.unit_wire));
-      per = std::max<int64_t>(dp.chunk_align, per / dp.chunk_align * dp.chunk_align);
-      p.per_chunk = std::min(per, p.units);
-    } else {
-      p.units = 1;
-      p.per_chunk = 1;
-      p.unit_wire = dp.wire_bytes;
-      p.unit_src = dp.wire_elems * sw;
-    }
+    const ChunkPlan p = chunk_plan(dp, source_width(*m.h->bound), opt.chunk_bytes);
     if (!m.direct)
       max_slot = std::max(max_slot, static_cast<size_t>(p.per_chunk * p.unit_wire));
     plans.push_back(p);
@@ -407,7 +387,7 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
   for (size_t mi = 0; mi < ms.size(); ++mi) {
     Member &m = ms[mi];
     const DeviceProgram &dp = *m.dp;
-    const Plan1 &p = plans[mi];
+    const ChunkPlan &p = plans[mi];
     const BoundHandle::DevParams par = m.h->device_params(ctx.device, m.k);
     const uint32_t sw = m.h->bound->typed ? m.h->bound->source_type.width()
                                           : m.h->bound->layout.element_size;
@@ -440,14 +420,9 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
       ev = (ev + 1) % kChunkEvents;
       HIPCHECK(hipEventRecord(ce, ctx.copy));
       HIPCHECK(hipStreamWaitEvent(ctx.compute, ce, 0));
-      KArgs a = box_args(dp, v0, v1, v0 == 0, v1 == p.units);
-      a.src = wire;
-      a.dst = m.dst;
-      a.pf = par.pf;
-      a.pi = par.pi;
-      HIPCHECK(launch_box(dp.family, a, ctx.status, ctx.compute));
+      launches += launch_program(dp, v0, v1, v0 == 0, v1 == p.units, wire, m.dst, par.pf, par.pi,
+                                 ctx.status, ctx.compute);
       ++chunks;
-      ++launches;
     }
     if (m.report) {
       relx_report &r = *m.report;
@@ -545,17 +520,55 @@ void destroy_context(Context &ctx) {
   ctx.workers.reset();
 }
 
+uint32_t source_width(const Bound &b) {
+  return b.typed ? b.source_type.width() : b.layout.element_size;
+}
+
+ChunkPlan chunk_plan(const DeviceProgram &dp, uint32_t src_width, int64_t chunk_bytes) {
+  const int64_t want_chunk = chunk_bytes > 0 ? chunk_bytes : kDefaultChunkBytes;
+  ChunkPlan p{};
+  if (dp.chunk_axis >= 0) {
+    p.units = dp.base.vext[dp.chunk_axis];
+    p.unit_wire = dp.chunk_stride * dp.base.win;
+    p.unit_src = dp.chunk_stride * src_width;
+    int64_t per = std::max<int64_t>(1, want_chunk / std::max<int64_t>(1, p.unit_wire));
+    per = std::max<int64_t>(dp.chunk_align, per / dp.chunk_align * dp.chunk_align);
+    p.per_chunk = std::min(per, p.units);
+  } else {
+    p.units = 1;
+    p.per_chunk = 1;
+    p.unit_wire = dp.wire_bytes;
+    p.unit_src = dp.wire_elems * src_width;
+  }
+  return p;
+}
+
+int64_t verify_launches(BoundHandle &h, uint32_t k, int64_t chunk_bytes) {
+  const DeviceProgram &dp = h.program(k);
+  const ChunkPlan p = chunk_plan(dp, source_width(*h.bound), chunk_bytes);
+  int64_t n = 0;
+  for (int64_t v0 = 0; v0 < p.units; v0 += p.per_chunk) {
+    const int64_t v1 = std::min(p.units, v0 + p.per_chunk);
+    for (const KArgs &a : box_launches(dp, v0, v1, v0 == 0, v1 == p.units)) {
+      verify_launch(dp, a);
+      ++n;
+    }
+  }
+  if (dp.chunk_axis >= 0 && p.units > p.per_chunk)
+    for (const KArgs &a : box_launches(dp, 0, 0, true, true)) { // the device-resident launch
+      verify_launch(dp, a);
+      ++n;
+    }
+  return n;
+}
+
 void relayout_device(Context &ctx, BoundHandle &h, uint32_t k, const void *wire, void *dst,
                      hipStream_t stream) {
   DeviceGuard guard(ctx.device);
   const DeviceProgram &dp = h.program(k);
   const BoundHandle::DevParams par = h.device_params(ctx.device, k);
-  KArgs a = box_args(dp, 0, 0, true, true);
-  a.src = static_cast<const uint8_t *>(wire);
-  a.dst = static_cast<uint8_t *>(dst);
-  a.pf = par.pf;
-  a.pi = par.pi;
-  HIPCHECK(launch_box(dp.family, a, ctx.status, stream ? stream : ctx.compute));
+  launch_program(dp, 0, 0, true, true, wire, dst, par.pf, par.pi, ctx.status,
+                 stream ? stream : ctx.compute);
 }
 
 double measure_h2d(int device, size_t bytes, int iters, int rounds) {

@@ -55,8 +55,26 @@ void prepare_stages(const Bound &b, Prepared &p);
 bool fill_at(const Bound &b, const Prepared &p, uint32_t to, uint64_t &bits);
 uint64_t host_apply(const HostStage &s, uint64_t x, int64_t c);
 std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, uint32_t k);
-KArgs box_args(const DeviceProgram &dp, int64_t v0, int64_t v1, bool first, bool last);
+std::vector<KArgs> box_launches(const DeviceProgram &dp, int64_t v0, int64_t v1, bool first,
+                                bool last);
+// Launch the program over valid chunk-axis coordinates [v0, v1) (the whole
+// box when it has no chunk axis); returns the number of kernel launches.
+int64_t launch_program(const DeviceProgram &dp, int64_t v0, int64_t v1, bool first, bool last,
+                       const void *src, void *dst, const float *pf, const int32_t *pi,
+                       int32_t *status, hipStream_t s);
 hipError_t launch_box(int family, const KArgs &a, int32_t *status, hipStream_t s);
+// Host-side check that one launch stays inside the wire and the result, with
+// aligned vectors and parameter indices inside their tables (throws Error).
+void verify_launch(const DeviceProgram &dp, const KArgs &a);
+
+// Chunk schedule of one program: `units` valid coordinates of the chunk axis
+// (1 without one), `per_chunk` per chunk, wire/source bytes per unit.
+struct ChunkPlan {
+  int64_t units, per_chunk, unit_wire, unit_src;
+};
+constexpr int64_t kDefaultChunkBytes = int64_t{8} << 20;
+uint32_t source_width(const Bound &b);
+ChunkPlan chunk_plan(const DeviceProgram &dp, uint32_t src_width, int64_t chunk_bytes);
 
 // ------------------------------------------------------------ workers
 
@@ -102,6 +120,10 @@ struct BoundHandle {
   DevParams device_params(int device, uint32_t k);
   ~BoundHandle();
 };
+
+// verify_launch over every launch of the chunk schedule for `chunk_bytes`
+// (and the whole-box launch of the device-resident path); returns the count.
+int64_t verify_launches(BoundHandle &h, uint32_t k, int64_t chunk_bytes);
 
 struct Context {
   int device = 0;

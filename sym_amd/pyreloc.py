@@ -285,6 +285,18 @@ class Context:
             pass
 
 
+def verify_launches(bound, wire_boundary=0, chunk_bytes=0):
+    """Check on the host every kernel launch the executor would make for
+    `bound` (wire at `wire_boundary`, chunks of `chunk_bytes`); returns the
+    number of launches checked, raises TransferError on a violation."""
+    err = N.relx_err()
+    n = ctypes.c_int64(0)
+    if N.lib().relx_verify_launches(bound._h, int(wire_boundary), int(chunk_bytes),
+                                    ctypes.byref(n), ctypes.byref(err)):
+        _raise(err)
+    return n.value
+
+
 def host_stage(bound, host_stages, src_ptr, wire_ptr, threads=8):
     err = N.relx_err()
     if N.lib().relx_host_stage(bound._h, int(host_stages), src_ptr, wire_ptr, int(threads),

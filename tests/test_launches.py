@@ -1,0 +1,78 @@
+"""Every kernel launch the executor would make stays inside its buffers.
+
+relx_verify_launches walks each launch of the chunk schedule (and the
+device-resident whole-box launch) with the kernels' own index arithmetic
+and checks every access against the wire and result extents, 16-byte
+alignment of vector accesses and parameter-table bounds. Runs on the CPU:
+corpus plans at every wire boundary, every configuration at full size, and
+several chunk sizes."""
+import numpy as np
+import pytest
+
+from sym_amd import pyreloc as P
+from sym_amd import workloads as W
+from tests import golden_io as G
+
+CHUNKS = [0, 1 << 16, 3 << 20]
+
+
+def _check(bound, boundaries, chunks=CHUNKS):
+    total = 0
+    for k in boundaries:
+        for c in chunks:
+            total += P.verify_launches(bound, k, c)
+    assert total > 0
+
+
+@pytest.mark.parametrize("meta,blob", G.typed_fixtures(), ids=[m["name"] for m, _ in G.typed_fixtures()])
+def test_typed_corpus_launches(meta, blob):
+    plan = P.load_typed_plan(blob)
+    for b in meta["bindings"]:
+        bd = P.bind_typed(plan, b["symbols"], G.fixture_params(meta))
+        _check(bd, range(len(bd.footprints())))
+
+
+@pytest.mark.parametrize("meta,blob", G.layout_fixtures(), ids=[m["name"] for m, _ in G.layout_fixtures()])
+def test_layout_corpus_launches(meta, blob):
+    plan = P.load_plan(blob)
+    bindings = [{}] if not meta["symbols"] else \
+        [{n: c["multiple_of"] * f for n, c in meta["symbols"].items()} for f in (1, 2, 3)]
+    for binding in bindings:
+        _check(P.bind(plan, binding), [0])
+
+
+@pytest.mark.parametrize("n", W.C1_SIZES)
+def test_c1_launches(n):
+    b = P.Bound(P.Plan(W.c1_plan().blob), {"s0": n})
+    assert b.kernel == ("transpose" if n % 4096 == 0 else "generic") or n < 4096
+    _check(b, [0])
+
+
+@pytest.mark.parametrize("n", [32, 1, 3])
+def test_c2_launches(n):
+    b = P.Bound(P.Plan(W.c2_plan(n=n).blob), {}, {})
+    assert b.kernel == "interleave"
+    _check(b, [0, 1])
+
+
+def test_c3_launches():
+    b = P.Bound(P.Plan(W.c3_plan().blob), {"s0": 4096, "s1": 11008},
+                W.param("scale", np.ones(11008, np.float32)))
+    assert b.kernel == "transpose"
+    _check(b, [0])
+
+
+@pytest.mark.parametrize("rows,cols", [(14336, 4096), (4096, 14336)])
+def test_c4_launches(rows, cols):
+    b = P.Bound(P.Plan(W.c4_plan().blob), {"s0": rows, "s1": cols},
+                W.param("scale", np.ones(rows, np.float32)))
+    assert b.kernel == "stream"
+    _check(b, [0])
+
+
+@pytest.mark.parametrize("bs,seq", W.C5_SHAPES)
+def test_c5_launches(bs, seq):
+    b = P.Bound(P.Plan(W.c5_plan().blob), {"B": bs, "S": seq},
+                W.param("scale", np.ones(32, np.float32)))
+    big = bs * seq >= 64 * 1024
+    _check(b, [0, 1], chunks=[0] if big else CHUNKS)
