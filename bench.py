@@ -42,6 +42,10 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--report", action="store_true", help="one JSON line per config")
     ap.add_argument("--configs", default="c1,c2,c3,c4,c5")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run a plain copy of known size, then each config's kernel (for rocprofv3 --pmc)")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="turn two rocprofv3 --pmc runs of --traffic-probe into profiles/traffic.json")
     return ap.parse_args()
 
 
@@ -57,7 +61,7 @@ def torch_mod():
 class Case:
     """One workload: a bound plan plus host inputs for it."""
 
-    def __init__(self, name, workload, blob, symbols, params, src, extra=None):
+    def __init__(self, name, workload, blob, symbols, params, src, extra=None, widths=(0, 0)):
         from sym_amd import pyreloc as P
         self.name, self.workload = name, workload
         self.plan = P.Plan(blob)
@@ -69,27 +73,35 @@ class Case:
         self.out_bytes = b.destination_bytes if self.plan.typed else b.total_bytes
         self.wire_bytes = self.src.nbytes  # boundary-0 wire (device programs start there)
         self.kernel = b.kernel
+        self.win, self.wout = widths  # element bytes of the wire and the result
 
 
 def make_case(name):
     from sym_amd import workloads as W
+    if name == "c4":
+        pool = W.c4_pool(experts=1)
+        q, sc = pool[0][0]
+        return Case(name, "C4 MoE expert matrix int8 gate [14336,4096] -> per-row dequant -> f16",
+                    W.c4_plan().blob, {"s0": q.shape[0], "s1": q.shape[1]}, W.param("scale", sc), q,
+                    widths=(1, 2))
     if name == "c1":
         n = 16777216
         return Case(name, "C1 README plan f32[N=16777216] -> [N/64,64] -> transpose [64,N/64]",
-                    W.c1_plan().blob, {"s0": n}, None, W.c1_input(n))
+                    W.c1_plan().blob, {"s0": n}, None, W.c1_input(n), widths=(4, 4))
     if name == "c2":
         return Case(name, "C2 image batch f32 NCHW [32,3,224,224] -> pad C 3->4 -> NHWC -> f16",
-                    W.c2_plan().blob, {}, {}, W.c2_input())
+                    W.c2_plan().blob, {}, {}, W.c2_input(), widths=(4, 2))
     if name == "c3":
         q, s = W.c3_input()
         return Case(name, "C3 int8 weight [4096,11008] -> dequant(scale[11008]) -> f16 -> [11008,4096]",
-                    W.c3_plan().blob, {"s0": 4096, "s1": 11008}, W.param("scale", s), q)
+                    W.c3_plan().blob, {"s0": 4096, "s1": 11008}, W.param("scale", s), q,
+                    widths=(1, 2))
     if name.startswith("c5"):
         b, s = (64, 4096) if name == "c5" else tuple(int(v) for v in name[3:].split("x"))
         x, sc = W.c5_input(b, s)
         return Case(name, "C5 f16 [%d,%d,32,128] -> [B,32,S,128] -> f32 -> int8 (per-head scale)"
                     % (b, s), W.c5_plan().blob, {"B": b, "S": s}, W.param("scale", sc), x,
-                    {"B": b, "S": s})
+                    {"B": b, "S": s}, widths=(2, 1))
     raise ValueError(name)
 
 
@@ -196,12 +208,87 @@ def cpu_baseline(case, seconds, threads):
                       % (n, case.name.upper(), case.out_bytes, el)}
 
 
-def traffic_for(kernel_key):
+def traffic_for(config):
+    """HBM bytes per launch of the config's kernel from the committed PMC
+    summary (profiles/traffic.json), or None."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        return json.load(f).get(kernel_key)
+        entry = json.load(f).get("configs", {}).get(config)
+    return None if entry is None else entry["traffic_bytes"]
+
+
+# Calibration copy of the traffic probe: one device-to-device copy of this
+# many bytes reads and writes exactly this many bytes of HBM.
+CALIBRATION_BYTES = 256 << 20
+
+
+def traffic_probe(torch, ctx, names):
+    """A plain copy of known size, then 20 launches of each config's kernel
+    over rotating buffer sets; prints which kernel each config launches."""
+    a = torch.empty(CALIBRATION_BYTES, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    a.random_(0, 256)
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    del a, b
+    kernels = {}
+    for name in names:
+        case = make_case(name)
+        device_rate(torch, ctx, case.bound, case.wire_bytes, case.out_bytes, 20, 2)
+        bi = case.bound
+        kernels[name] = {"family": case.kernel, "wire_bytes": case.wire_bytes,
+                         "output_bytes": case.out_bytes,
+                         "algorithmic_bytes": case.wire_bytes + case.out_bytes + bi.parameter_bytes,
+                         "win": case.win, "wout": case.wout}
+    print(json.dumps({"calibration_bytes": CALIBRATION_BYTES, "kernels": kernels}), flush=True)
+
+
+def _pmc_rows(d, counter):
+    """(kernel name, counter value in bytes) per dispatch from a rocprofv3
+    --pmc CSV directory (values are KiB per dispatch)."""
+    import csv
+    import glob
+    rows = []
+    for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                if r.get("Counter_Name") == counter:
+                    rows.append((r["Kernel_Name"], float(r["Counter_Value"]) * 1024.0))
+    return rows
+
+
+def summarize_pmc(fetch_dir, write_dir, probe):
+    """Scale each kernel's FETCH_SIZE / WRITE_SIZE by what the counters read
+    for the calibration copy and write profiles/traffic.json."""
+    out = {"calibration_bytes": probe["calibration_bytes"], "configs": {}}
+    med = {}
+    for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        rows = _pmc_rows(d, counter)
+        cal = [v for k, v in rows if "copyBuffer" in k and v > probe["calibration_bytes"] / 4]
+        if not cal:
+            raise SystemExit("no calibration copy dispatches for %s in %s" % (counter, d))
+        factor = probe["calibration_bytes"] / float(np.median(cal))
+        out[counter + "_calibration_factor"] = round(factor, 4)
+        for name, info in probe["kernels"].items():
+            pat = "k_%s<%d, %d" % (info["family"], info["win"], info["wout"])
+            vals = [v for k, v in rows if pat in k]
+            if vals:
+                med.setdefault(name, {})[counter] = float(np.median(vals)) * factor
+                med[name]["kernel"] = next(k for k, v in rows if pat in k)
+                med[name]["dispatches"] = len(vals)
+    for name, m in med.items():
+        if "FETCH_SIZE" in m and "WRITE_SIZE" in m:
+            alg = probe["kernels"][name]["algorithmic_bytes"]
+            t = m["FETCH_SIZE"] + m["WRITE_SIZE"]
+            out["configs"][name] = {"kernel": m["kernel"], "dispatches": m["dispatches"],
+                                    "fetch_bytes": round(m["FETCH_SIZE"]),
+                                    "write_bytes": round(m["WRITE_SIZE"]),
+                                    "traffic_bytes": round(t), "algorithmic_bytes": alg,
+                                    "traffic_over_algorithmic": round(t / alg, 4)}
+    return out
 
 
 # --------------------------------------------------------------- report
@@ -284,6 +371,20 @@ def c4_report(torch, ctx, P, args, h2d_ceiling):
 
 def main():
     args = parse()
+    if args.summarize_pmc:
+        probe = None
+        for d in args.summarize_pmc:
+            p = os.path.join(d, "probe.json")
+            if os.path.exists(p):
+                with open(p) as f:
+                    probe = json.load(f)
+        if probe is None:
+            sys.exit("probe.json (the --traffic-probe output line) missing from the PMC directories")
+        res = summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], probe)
+        with open(os.path.join(ROOT, "profiles", "traffic.json"), "w") as f:
+            json.dump(res, f, indent=1)
+        print(json.dumps(res))
+        return
     if args.gpus != 1:
         sys.exit("bench.py measures one GPU: this build runs the path on one MI355X only "
                  "(every GPU box here has one GPU); got --gpus %d" % args.gpus)
@@ -291,6 +392,11 @@ def main():
     from sym_amd import pyreloc as P
     ctx = P.Context(0)
     h2d_ceiling = P.measure_h2d(0, 256 << 20, 20, 3)
+
+    if args.traffic_probe:
+        traffic_probe(torch, ctx, args.configs.split(","))
+        ctx.close()
+        return
 
     if args.report:
         print(json.dumps({"pinned_h2d_ceiling_GBps": round(h2d_ceiling, 2),
@@ -338,14 +444,14 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32->f16",
+        "dtype": "f32",
         "data": "synthetic (seed 20260710, N(0,1) fp32)",
-        "config": {"workload": case.workload, "kernel": "interleave",
+        "config": {"workload": case.workload, "kernel": "interleave", "result_dtype": "f16",
                    "output_bytes": case.out_bytes, "wire_bytes_per_step": case.wire_bytes,
                    "value_definition": "output bytes / step time, wire resident in HBM"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_for("c2_interleave"), "kernel_ms": round(ms_step, 5),
+                     "traffic": traffic_for("c2"), "kernel_ms": round(ms_step, 5),
                      "kernel_ms_per_launch_events": round(kms, 5),
                      "algorithmic_bytes": alg},
         "e2e": {"pinned_h2d_ceiling_GBps": round(h2d_ceiling, 2),

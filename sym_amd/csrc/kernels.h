@@ -114,13 +114,26 @@ __device__ __forceinline__ uint32_t apply(const DevStage &s, uint32_t x, uint32_
   }
 }
 
-// Cache policy of the fast kernels' global accesses (nontemporal or not),
-// per family and element widths.
+// Cache policy of the fast kernels' global accesses: nontemporal (streamed
+// past the caches) or plain, per family, element widths and `run` (16-byte
+// vectors one thread moves back to back), as measured on gfx950 over the
+// configurations and a width sweep. Streaming pays where a thread moves one
+// vector per access group; runs of two or more consecutive vectors measured
+// faster through the cache. Transposes read 64 elements per tile row: with
+// one-byte elements that is half a 128-byte line whose other half a
+// neighbouring tile reads, so those loads stay cached; narrowing transposes
+// store through the cache.
+constexpr bool nt_load_policy(int fam, int win, int wout, int run) {
+  return fam == kFamTranspose ? win >= 2 : run == 1;
+}
+constexpr bool nt_store_policy(int fam, int win, int wout, int run) {
+  return fam == kFamTranspose ? wout >= win : run == 1;
+}
 #ifndef RELX_NT_LOAD
-#define RELX_NT_LOAD(FAM, WIN, WOUT) false
+#define RELX_NT_LOAD(FAM, WIN, WOUT, RUN) nt_load_policy(FAM, WIN, WOUT, RUN)
 #endif
 #ifndef RELX_NT_STORE
-#define RELX_NT_STORE(FAM, WIN, WOUT) false
+#define RELX_NT_STORE(FAM, WIN, WOUT, RUN) nt_store_policy(FAM, WIN, WOUT, RUN)
 #endif
 
 template <bool NT> __device__ __forceinline__ vec4 ld16(const vec4 *p) {
@@ -397,15 +410,16 @@ __device__ __forceinline__ void chain_vec(const KArgs &a, uint32_t (&v)[V], int6
 
 // ---------------------------------------------------------------- stream
 
-// One vector of V = 16/min(width) elements per thread: the narrower side
-// moves exactly 16 bytes and the wider side 32 or 64, all lane-contiguous.
-// The innermost level counts vectors.
+// One vector of V = 16/min(width) elements per work item and thread: the
+// narrower side moves exactly 16 bytes and the wider side 32 or 64, all
+// lane-contiguous. The innermost level counts vectors. (Two or four items per
+// thread, all loads first, measured slower on gfx950.)
 template <int WIN, int WOUT, int L, int CH>
 __global__ __launch_bounds__(kBlock) void k_stream(KArgs a) {
   constexpr int V = 16 / (WIN < WOUT ? WIN : WOUT);
   constexpr int NI = V * WIN / 16, NO = V * WOUT / 16;
-  constexpr bool NTL = RELX_NT_LOAD(kFamStream, WIN, WOUT);
-  constexpr bool NTS = RELX_NT_STORE(kFamStream, WIN, WOUT);
+  constexpr bool NTL = RELX_NT_LOAD(kFamStream, WIN, WOUT, NI);
+  constexpr bool NTS = RELX_NT_STORE(kFamStream, WIN, WOUT, NO);
   const uint32_t stride = gridDim.x * kBlock;
   for (uint32_t i = blockIdx.x * kBlock + threadIdx.x; i < a.work; i += stride) {
     int64_t sof = a.sbase, dof = a.dbase;
@@ -446,8 +460,8 @@ __global__ __launch_bounds__(kBlock) void k_transpose(KArgs a) {
   constexpr int VI = 16 / WIN, VO = 16 / WOUT;
   constexpr int VPRI = kTile / VI, VPRO = kTile / VO;
   constexpr int NI = kTile * VPRI / kBlock, NO = kTile * VPRO / kBlock;
-  constexpr bool NTL = RELX_NT_LOAD(kFamTranspose, WIN, WOUT);
-  constexpr bool NTS = RELX_NT_STORE(kFamTranspose, WIN, WOUT);
+  constexpr bool NTL = RELX_NT_LOAD(kFamTranspose, WIN, WOUT, 1);
+  constexpr bool NTS = RELX_NT_STORE(kFamTranspose, WIN, WOUT, 1);
   const uint32_t t = xcd_tile(blockIdx.x, gridDim.x);
   if (t >= a.work)
     return;
@@ -507,8 +521,8 @@ __global__ __launch_bounds__(kBlock) void k_interleave(KArgs a) {
   constexpr int G = 16 / WIN;
   constexpr int NO = G * CP * WOUT / 16;
   static_assert(G * CP * WOUT % 16 == 0, "packed pixels must fill whole vectors");
-  constexpr bool NTL = RELX_NT_LOAD(kFamInterleave, WIN, WOUT);
-  constexpr bool NTS = RELX_NT_STORE(kFamInterleave, WIN, WOUT);
+  constexpr bool NTL = RELX_NT_LOAD(kFamInterleave, WIN, WOUT, 1);
+  constexpr bool NTS = RELX_NT_STORE(kFamInterleave, WIN, WOUT, NO);
   const uint32_t stride = gridDim.x * kBlock;
   for (uint32_t i = blockIdx.x * kBlock + threadIdx.x; i < a.work; i += stride) {
     const uint32_t rest = fdiv(i, a.i_ng);
