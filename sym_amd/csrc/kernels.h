@@ -117,12 +117,14 @@ __device__ __forceinline__ uint32_t apply(const DevStage &s, uint32_t x, uint32_
 // Cache policy of the fast kernels' global accesses: nontemporal (streamed
 // past the caches) or plain, per family, element widths and `run` (16-byte
 // vectors one thread moves back to back), as measured on gfx950 over the
-// configurations and a width sweep. Streaming pays where a thread moves one
-// vector per access group; runs of two or more consecutive vectors measured
-// faster through the cache. Transposes read 64 elements per tile row: with
-// one-byte elements that is half a 128-byte line whose other half a
-// neighbouring tile reads, so those loads stay cached; narrowing transposes
-// store through the cache.
+// configurations and a width sweep. Every byte is touched once, so streaming
+// pays where each access instruction of a wave covers one contiguous run (the
+// stream kernel always, the interleave's plane loads); a thread writing two or
+// more consecutive vectors (the interleave's packed pixels) measured faster
+// through the cache. Transposes read 64 elements per tile row: with one-byte
+// elements that is half a 128-byte line whose other half a neighbouring tile
+// reads, so those loads stay cached; narrowing transposes store through the
+// cache.
 constexpr bool nt_load_policy(int fam, int win, int wout, int run) {
   return fam == kFamTranspose ? win >= 2 : run == 1;
 }
@@ -148,6 +150,46 @@ template <bool NT> __device__ __forceinline__ void st16(vec4 *p, const vec4 &v) 
     __builtin_nontemporal_store(v, p);
   else
     *p = v;
+}
+
+typedef uint32_t vec2 __attribute__((ext_vector_type(2)));
+
+// NB-byte (4, 8 or 16) access into the low words of a 16-byte vector.
+template <int NB, bool NT> __device__ __forceinline__ vec4 ld_n(const uint8_t *p) {
+  vec4 r = {0u, 0u, 0u, 0u};
+  if constexpr (NB == 16) {
+    r = ld16<NT>(reinterpret_cast<const vec4 *>(p));
+  } else if constexpr (NB == 8) {
+    const vec2 *q = reinterpret_cast<const vec2 *>(p);
+    const vec2 t = NT ? __builtin_nontemporal_load(q) : *q;
+    r.x = t.x;
+    r.y = t.y;
+  } else {
+    static_assert(NB == 4, "4, 8 or 16 bytes");
+    const uint32_t *q = reinterpret_cast<const uint32_t *>(p);
+    r.x = NT ? __builtin_nontemporal_load(q) : *q;
+  }
+  return r;
+}
+
+template <int NB, bool NT> __device__ __forceinline__ void st_n(uint8_t *p, const vec4 &v) {
+  if constexpr (NB == 16) {
+    st16<NT>(reinterpret_cast<vec4 *>(p), v);
+  } else if constexpr (NB == 8) {
+    vec2 *q = reinterpret_cast<vec2 *>(p);
+    const vec2 t = {v.x, v.y};
+    if constexpr (NT)
+      __builtin_nontemporal_store(t, q);
+    else
+      *q = t;
+  } else {
+    static_assert(NB == 4, "4, 8 or 16 bytes");
+    uint32_t *q = reinterpret_cast<uint32_t *>(p);
+    if constexpr (NT)
+      __builtin_nontemporal_store(v.x, q);
+    else
+      *q = v.x;
+  }
 }
 
 // --------------------------------------------------------- element access
@@ -410,40 +452,61 @@ __device__ __forceinline__ void chain_vec(const KArgs &a, uint32_t (&v)[V], int6
 
 // ---------------------------------------------------------------- stream
 
-// One vector of V = 16/min(width) elements per work item and thread: the
-// narrower side moves exactly 16 bytes and the wider side 32 or 64, all
-// lane-contiguous. The innermost level counts vectors. (Two or four items per
-// thread, all loads first, measured slower on gfx950.)
+// Stream work items hold V = 16/max(win, wout) elements: the wider side
+// moves 16 bytes per item, the narrower 8 or 4. Each lane takes U items 64
+// apart, so every load and store instruction of a wave covers one contiguous
+// run (a lane-contiguous run of two 16-byte vectors per lane measured ~15%
+// slower for widening stages). The innermost level counts items.
+#ifndef RELX_STREAM_ITEMS
+#define RELX_STREAM_ITEMS(WIN, WOUT) 2
+#endif
+
+template <int WIN, int WOUT> constexpr int stream_items() {
+  return RELX_STREAM_ITEMS(WIN, WOUT);
+}
+
 template <int WIN, int WOUT, int L, int CH>
 __global__ __launch_bounds__(kBlock) void k_stream(KArgs a) {
-  constexpr int V = 16 / (WIN < WOUT ? WIN : WOUT);
-  constexpr int NI = V * WIN / 16, NO = V * WOUT / 16;
-  constexpr bool NTL = RELX_NT_LOAD(kFamStream, WIN, WOUT, NI);
-  constexpr bool NTS = RELX_NT_STORE(kFamStream, WIN, WOUT, NO);
-  const uint32_t stride = gridDim.x * kBlock;
-  for (uint32_t i = blockIdx.x * kBlock + threadIdx.x; i < a.work; i += stride) {
-    int64_t sof = a.sbase, dof = a.dbase;
-    const bool pad = decompose<L>(a.lv, i, sof, dof);
-    uint32_t v[V];
-    if (pad) {
+  constexpr int V = 16 / (WIN > WOUT ? WIN : WOUT);
+  constexpr int BI = V * WIN, BO = V * WOUT;
+  constexpr int U = stream_items<WIN, WOUT>();
+  static_assert(U == 1 || U == 2, "the 32-bit index covers at most two items per lane");
+  constexpr bool NTL = RELX_NT_LOAD(kFamStream, WIN, WOUT, 1);
+  constexpr bool NTS = RELX_NT_STORE(kFamStream, WIN, WOUT, 1);
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = (blockIdx.x * kBlock + threadIdx.x) >> 6;
+  const uint32_t stride = gridDim.x * (kBlock / 64) * (64 * U);
+  for (uint32_t base = wave * (64 * U) + lane; base < a.work; base += stride) {
+    int64_t sof[U], dof[U];
+    bool pad[U], live[U];
+    vec4 in[U];
 #pragma unroll
-      for (int e = 0; e < V; ++e)
-        v[e] = a.fill;
-    } else {
-      vec4 in[NI];
-      const vec4 *src = reinterpret_cast<const vec4 *>(a.src + sof * WIN);
-#pragma unroll
-      for (int j = 0; j < NI; ++j)
-        in[j] = ld16<NTL>(src + j);
-      unpack<WIN, V>(in, v);
-      chain_vec<CH, V>(a, v, dof);
+    for (int u = 0; u < U; ++u) {
+      const uint32_t i = base + 64u * u;
+      live[u] = u == 0 || i < a.work;
+      sof[u] = a.sbase;
+      dof[u] = a.dbase;
+      pad[u] = decompose<L>(a.lv, live[u] ? i : base, sof[u], dof[u]);
+      if (live[u] && !pad[u])
+        in[u] = ld_n<BI, NTL>(a.src + sof[u] * WIN);
     }
-    vec4 out[NO];
-    pack<WOUT, V>(v, out);
-    vec4 *dst = reinterpret_cast<vec4 *>(a.dst + dof * WOUT);
 #pragma unroll
-    for (int j = 0; j < NO; ++j)
-      st16<NTS>(dst + j, out[j]);
+    for (int u = 0; u < U; ++u) {
+      if (!live[u])
+        break;
+      uint32_t v[V];
+      if (pad[u]) {
+#pragma unroll
+        for (int e = 0; e < V; ++e)
+          v[e] = a.fill;
+      } else {
+        unpack<WIN, V>(&in[u], v);
+        chain_vec<CH, V>(a, v, dof[u]);
+      }
+      vec4 out = {0u, 0u, 0u, 0u};
+      pack<WOUT, V>(v, &out);
+      st_n<BO, NTS>(a.dst + dof[u] * WOUT, out);
+    }
   }
 }
 
@@ -585,7 +648,8 @@ __attribute__((unused)) unsigned grid_for(int64_t work) {
 
 template <int WIN, int WOUT, int CH>
 hipError_t stream_launch(const KArgs &a, hipStream_t s) {
-  const dim3 grid(grid_for(a.work)), block(kBlock);
+  constexpr int U = stream_items<WIN, WOUT>();
+  const dim3 grid(grid_for((a.work + U - 1) / U)), block(kBlock);
   switch (a.nlev) {
   case 1:
     hipLaunchKernelGGL((k_stream<WIN, WOUT, 1, CH>), grid, block, 0, s, a);

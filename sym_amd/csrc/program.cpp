@@ -387,7 +387,8 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
   const bool widths_ok = (win == 1 || win == 2 || win == 4) && (wout == 1 || wout == 2 || wout == 4);
   const bool dense = dense_dst(L, pext);
   int family = kFamGeneric;
-  const int V = widths_ok ? 16 / std::min(win, wout) : 0;
+  // stream items: 16 bytes on the wider side
+  const int V = widths_ok ? 16 / std::max(win, wout) : 0;
   // per-channel stages in the fast kernels index with a 32-bit result offset
   const bool off32 = dp->dst_elems < (int64_t{1} << 32);
   auto channels_ok = [&](int64_t vlen) {
@@ -727,19 +728,23 @@ struct Checker {
   int64_t wire, dst; // elements
   size_t npf, npi;
 
-  void src_run(int64_t off, int64_t n, bool vec16) const {
+  // n elements from `off`, accessed as one vector of n * width bytes when
+  // `vec` (which must then be aligned to its size)
+  void src_run(int64_t off, int64_t n, bool vec) const {
     if (off < 0 || off + n > wire)
       bad_launch(dp, "source run [" + std::to_string(off) + ", " + std::to_string(off + n) +
                          ") outside " + std::to_string(wire) + " wire elements");
-    if (vec16 && (off * a.win) % 16 != 0)
-      bad_launch(dp, "unaligned 16-byte source access at element " + std::to_string(off));
+    if (vec && (off * a.win) % (n * a.win) != 0)
+      bad_launch(dp, "unaligned " + std::to_string(n * a.win) + "-byte source access at element " +
+                         std::to_string(off));
   }
-  void dst_run(int64_t off, int64_t n, bool vec16) const {
+  void dst_run(int64_t off, int64_t n, bool vec) const {
     if (off < 0 || off + n > dst)
       bad_launch(dp, "destination run [" + std::to_string(off) + ", " + std::to_string(off + n) +
                          ") outside " + std::to_string(dst) + " result elements");
-    if (vec16 && (off * a.wout) % 16 != 0)
-      bad_launch(dp, "unaligned 16-byte destination access at element " + std::to_string(off));
+    if (vec && (off * a.wout) % (n * a.wout) != 0)
+      bad_launch(dp, "unaligned " + std::to_string(n * a.wout) +
+                         "-byte destination access at element " + std::to_string(off));
   }
   // channels of V consecutive result elements from dense offset o, as the
   // fast kernels index them (constant, or +1 per element)
