@@ -576,63 +576,83 @@ __global__ __launch_bounds__(kBlock) void k_transpose(KArgs a) {
 // ------------------------------------------------------------ interleave
 
 // Axes: [batch..., P, C] with C (padded to CP) innermost in the destination
-// and a plane stride in the source; P contiguous in the source. Each thread
-// takes G = 16/WIN consecutive pixels: one 16-byte load per valid plane, one
-// packed run of G*CP output elements. Stages are per tensor.
+// and a plane stride in the source; P contiguous in the source. A work item
+// is G consecutive pixels (interleave_pixels): one 4-16 byte load per valid
+// plane, one packed run of G*CP output elements (16 bytes when a pixel allows).
+// Each lane takes U items 64 apart, so every plane load and every store
+// instruction of a wave covers one contiguous run. Stages are per tensor.
 template <int WIN, int WOUT, int CP, int CH>
 __global__ __launch_bounds__(kBlock) void k_interleave(KArgs a) {
-  constexpr int G = 16 / WIN;
-  constexpr int NO = G * CP * WOUT / 16;
-  static_assert(G * CP * WOUT % 16 == 0, "packed pixels must fill whole vectors");
+  constexpr int G = interleave_pixels(WIN, WOUT, CP);
+  constexpr int BI = G * WIN, BO = G * CP * WOUT;
+  static_assert(BO == 4 || BO == 8 || BO % 16 == 0, "packed pixels must fill a store");
+  constexpr int NO = BO >= 16 ? BO / 16 : 1;
+  constexpr int U = 2;
   constexpr bool NTL = RELX_NT_LOAD(kFamInterleave, WIN, WOUT, 1);
   constexpr bool NTS = RELX_NT_STORE(kFamInterleave, WIN, WOUT, NO);
-  const uint32_t stride = gridDim.x * kBlock;
-  for (uint32_t i = blockIdx.x * kBlock + threadIdx.x; i < a.work; i += stride) {
-    const uint32_t rest = fdiv(i, a.i_ng);
-    const uint32_t g = i - rest * a.i_ng.d;
-    int64_t sbase = a.sbase, dbase = a.dbase;
-    const bool pad = decompose<kBatchLevels>(a.lv, rest, sbase, dbase);
-    const int64_t p0 = static_cast<int64_t>(g) * G; // pixel axis is unpadded
-    // every plane's load is issued before any is used, so a thread keeps all
-    // of them in flight at once
-    vec4 in[CP];
-    bool valid[CP];
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = (blockIdx.x * kBlock + threadIdx.x) >> 6;
+  const uint32_t stride = gridDim.x * (kBlock / 64) * (64 * U);
+  for (uint32_t base = wave * (64 * U) + lane; base < a.work; base += stride) {
+    vec4 in[U][CP];
+    bool valid[U][CP], live[U];
+    int64_t dbase[U], p0[U];
+    // every plane load of both items is issued before any is used
 #pragma unroll
-    for (int ch = 0; ch < CP; ++ch) {
-      const int32_t vc = ch - a.i_loc;
-      valid[ch] = !pad && static_cast<uint32_t>(vc) < static_cast<uint32_t>(a.i_vc);
-      if (valid[ch])
-        in[ch] = ld16<NTL>(
-            reinterpret_cast<const vec4 *>(a.src + (sbase + vc * a.i_ssc + p0) * WIN));
-    }
-    uint32_t px[CP][G];
+    for (int u = 0; u < U; ++u) {
+      const uint32_t i0 = base + 64u * u;
+      live[u] = u == 0 || i0 < a.work;
+      const uint32_t i = live[u] ? i0 : base;
+      const uint32_t rest = fdiv(i, a.i_ng);
+      const uint32_t g = i - rest * a.i_ng.d;
+      int64_t sbase = a.sbase;
+      dbase[u] = a.dbase;
+      const bool pad = decompose<kBatchLevels>(a.lv, rest, sbase, dbase[u]);
+      p0[u] = static_cast<int64_t>(g) * G; // the pixel axis is unpadded
 #pragma unroll
-    for (int ch = 0; ch < CP; ++ch) {
-      if (!valid[ch]) {
-#pragma unroll
-        for (int e = 0; e < G; ++e)
-          px[ch][e] = a.fill;
-      } else {
-        uint32_t v[G];
-        unpack<WIN, G>(&in[ch], v);
-        chain_vec<CH, G>(a, v, 0);
-#pragma unroll
-        for (int e = 0; e < G; ++e)
-          px[ch][e] = v[e];
+      for (int ch = 0; ch < CP; ++ch) {
+        const int32_t vc = ch - a.i_loc;
+        valid[u][ch] = live[u] && !pad && static_cast<uint32_t>(vc) < static_cast<uint32_t>(a.i_vc);
+        if (valid[u][ch])
+          in[u][ch] = ld_n<BI, NTL>(a.src + (sbase + vc * a.i_ssc + p0[u]) * WIN);
       }
     }
-    uint32_t flat[G * CP];
+    // one body per item with a compile-time index (a runtime-indexed loop
+    // the unroller gives up on would move `in` to scratch memory)
+    auto emit = [&](auto uc) {
+      constexpr int u = decltype(uc)::value;
+      uint32_t flat[G * CP];
 #pragma unroll
-    for (int e = 0; e < G; ++e)
+      for (int ch = 0; ch < CP; ++ch) {
+        uint32_t v[G];
+        if (!valid[u][ch]) {
 #pragma unroll
-      for (int ch = 0; ch < CP; ++ch)
-        flat[e * CP + ch] = px[ch][e];
-    vec4 out[NO];
-    pack<WOUT, G * CP>(flat, out);
-    vec4 *dst = reinterpret_cast<vec4 *>(a.dst + (dbase + p0 * CP) * WOUT);
+          for (int e = 0; e < G; ++e)
+            v[e] = a.fill;
+        } else {
+          unpack<WIN, G>(&in[u][ch], v);
+          chain_vec<CH, G>(a, v, 0);
+        }
 #pragma unroll
-    for (int j = 0; j < NO; ++j)
-      st16<NTS>(dst + j, out[j]);
+        for (int e = 0; e < G; ++e)
+          flat[e * CP + ch] = v[e];
+      }
+      vec4 out[NO];
+      out[0] = vec4{0u, 0u, 0u, 0u};
+      pack<WOUT, G * CP>(flat, out);
+      uint8_t *dst = a.dst + (dbase[u] + p0[u] * CP) * WOUT;
+      if constexpr (BO >= 16) {
+#pragma unroll
+        for (int j = 0; j < NO; ++j)
+          st16<NTS>(reinterpret_cast<vec4 *>(dst) + j, out[j]);
+      } else {
+        st_n<BO, NTS>(dst, out[0]);
+      }
+    };
+    static_assert(U == 2, "two items per lane");
+    emit(std::integral_constant<int, 0>{});
+    if (live[1])
+      emit(std::integral_constant<int, 1>{});
   }
 }
 
@@ -678,9 +698,10 @@ hipError_t transpose_launch(const KArgs &a, hipStream_t s) {
 
 template <int WIN, int WOUT, int CH, int CP>
 hipError_t interleave_cp(const KArgs &a, hipStream_t s) {
-  if constexpr ((16 / WIN) * CP * WOUT % 16 == 0) {
-    hipLaunchKernelGGL((k_interleave<WIN, WOUT, CP, CH>), dim3(grid_for(a.work)), dim3(kBlock),
-                       0, s, a);
+  constexpr int BO = interleave_pixels(WIN, WOUT, CP) * CP * WOUT;
+  if constexpr (BO == 4 || BO == 8 || BO % 16 == 0) {
+    hipLaunchKernelGGL((k_interleave<WIN, WOUT, CP, CH>), dim3(grid_for((a.work + 1) / 2)),
+                       dim3(kBlock), 0, s, a);
     return hipGetLastError();
   } else {
     return hipErrorInvalidValue;

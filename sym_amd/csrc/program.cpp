@@ -442,10 +442,11 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
     if (family == kFamGeneric && r >= 2 && r - 2 <= kBatchLevels && a.ss[r - 1] != 1 &&
         a.ss[r - 2] == 1 && a.ds[r - 2] == pext[static_cast<size_t>(r - 1)]) {
       const int64_t cp = pext[static_cast<size_t>(r - 1)];
-      const int G = 16 / win;
+      const int G = interleave_pixels(win, wout, static_cast<int>(cp));
+      const int64_t bo = G * cp * wout;
       bool pa_pad = lo[static_cast<size_t>(r - 2)] != 0 || pext[static_cast<size_t>(r - 2)] != a.vext[r - 2];
       bool ok = (cp == 2 || cp == 4 || cp == 8) && !pa_pad && a.vext[r - 2] % G == 0 &&
-                a.ss[r - 1] % G == 0 && (G * cp * wout) % 16 == 0;
+                a.ss[r - 1] % G == 0 && (bo == 4 || bo == 8 || bo % 16 == 0);
       for (int i = 0; i < r - 2; ++i)
         ok = ok && a.ss[i] % G == 0;
       for (uint32_t i = k; i < nst; ++i)
@@ -818,8 +819,10 @@ void verify_launch(const DeviceProgram &dp, const KArgs &a) {
     for (int k = 0; k < a.chain.n; ++k)
       if (a.chain.st[k].mode != kChanNone)
         bad_launch(dp, "per-channel stage in an interleave program");
-    if ((a.i_ssc * win) % 16 != 0)
-      bad_launch(dp, "plane stride breaks 16-byte alignment");
+    if ((a.i_ssc * win) % (G * win) != 0)
+      bad_launch(dp, "plane stride breaks the alignment of plane loads");
+    if (G != interleave_pixels(win, wout, CP))
+      bad_launch(dp, "pixels per item disagree with the kernel");
     for (uint32_t i = 0; i < a.work; ++i) {
       const uint32_t rest = fdiv(i, a.i_ng);
       const uint32_t g = i - rest * a.i_ng.d;

@@ -94,6 +94,20 @@ enum Family : int32_t {
   kFamInterleave = 3, // planar -> interleaved with a small padded inner axis
 };
 
+// Pixels per interleave work item: the packed output of an item fills one
+// 16-byte vector when a pixel is at most 16 bytes, and each plane is read in
+// one access of 4 to 16 bytes.
+constexpr int interleave_pixels(int win, int wout, int cp) {
+  int g = 16 / (cp * wout);
+  if (g < 1)
+    g = 1;
+  if (g * win < 4)
+    g = 4 / win;
+  if (g * win > 16)
+    g = 16 / win;
+  return g;
+}
+
 // Decomposition levels of the batch axes of the 2-D families.
 constexpr int kBatchLevels = 3;
 // Work items per launch of a fast kernel stay below this (32-bit indexing);
