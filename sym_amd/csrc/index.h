@@ -49,7 +49,7 @@ __host__ __device__ __forceinline__ bool decompose(const Level *lv, uint32_t i, 
 }
 
 // Map a linear block id so that the blocks one XCD runs (ids congruent mod 8)
-// take a contiguous run of tiles: neighbouring tiles share source cache lines.
+// take a contiguous run of the tile order.
 __host__ __device__ __forceinline__ uint32_t xcd_tile(uint32_t b, uint32_t n) {
   constexpr uint32_t kXcd = 8;
   if (n < kXcd)
@@ -57,6 +57,28 @@ __host__ __device__ __forceinline__ uint32_t xcd_tile(uint32_t b, uint32_t n) {
   const uint32_t per = n / kXcd, extra = n % kXcd, x = b % kXcd, j = b / kXcd;
   // XCD x owns tiles [x*per + min(x, extra), ...) of length per + (x < extra)
   return x * per + (x < extra ? x : extra) + j;
+}
+
+// Tile t of a transpose launch -> (q-tile, c-tile, batch index). Within a
+// batch element's plane of nq x nc tiles, whole groups of g q-tiles come
+// first (q fastest, then c), then the partial group of the remaining q-tiles.
+__host__ __device__ __forceinline__ void tile_of(const KArgs &a, uint32_t t, uint32_t &tq,
+                                                 uint32_t &tc, uint32_t &batch) {
+  batch = fdiv(t, a.t_plane);
+  const uint32_t tp = t - batch * a.t_plane.d;
+  const uint32_t nc = a.t_group.d / a.t_g.d;
+  if (tp < a.t_full * nc) {
+    const uint32_t grp = fdiv(tp, a.t_group);
+    const uint32_t r = tp - grp * a.t_group.d;
+    const uint32_t c = fdiv(r, a.t_g);
+    tq = grp * a.t_g.d + (r - c * a.t_g.d);
+    tc = c;
+  } else {
+    const uint32_t r = tp - a.t_full * nc;
+    const uint32_t c = fdiv(r, a.t_tail);
+    tq = a.t_full + (r - c * a.t_tail.d);
+    tc = c;
+  }
 }
 
 } // namespace relx

@@ -14,7 +14,8 @@
 //              16/min(width) elements per thread (16-byte loads/stores)
 //   transpose  batched 2-D transpose through a 64x64 LDS tile (32-bit
 //              words, row pitch 65: conflict-free for every element width
-//              pairing), XCD-grouped tile order
+//              pairing), tiles visited in groups of destination rows (XCD-grouped
+//              for one-byte sources)
 //   interleave planar -> interleaved with a small padded inner axis
 //              (NCHW -> NHWC + pad): per-plane 16-byte loads, packed pixels
 // The common stage sequences get a compile-time body (ChainCode); the rest
@@ -525,13 +526,11 @@ __global__ __launch_bounds__(kBlock) void k_transpose(KArgs a) {
   constexpr int NI = kTile * VPRI / kBlock, NO = kTile * VPRO / kBlock;
   constexpr bool NTL = RELX_NT_LOAD(kFamTranspose, WIN, WOUT, 1);
   constexpr bool NTS = RELX_NT_STORE(kFamTranspose, WIN, WOUT, 1);
-  const uint32_t t = xcd_tile(blockIdx.x, gridDim.x);
+  const uint32_t t = a.t_xcd ? xcd_tile(blockIdx.x, gridDim.x) : blockIdx.x;
   if (t >= a.work)
     return;
-  const uint32_t r1 = fdiv(t, a.t_nq);
-  const uint32_t tq = t - r1 * a.t_nq.d;
-  const uint32_t r2 = fdiv(r1, a.t_nc);
-  const uint32_t tc = r1 - r2 * a.t_nc.d;
+  uint32_t tq, tc, r2;
+  tile_of(a, t, tq, tc, r2);
   int64_t sbase = a.sbase, dbase = a.dbase;
   decompose<kBatchLevels>(a.lv, r2, sbase, dbase); // transposes carry no pads
   const int64_t q0 = static_cast<int64_t>(tq) * kTile, c0 = static_cast<int64_t>(tc) * kTile;

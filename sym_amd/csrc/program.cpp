@@ -645,8 +645,18 @@ KArgs launch_args(const DeviceProgram &dp, const Box &b) {
     break;
   case kFamTranspose:
     batch(dp.qa, dp.ca);
-    a.t_nq = make_div(b.ext[dp.qa] / 64);
-    a.t_nc = make_div(b.ext[dp.ca] / 64);
+    {
+      const int64_t nq = b.ext[dp.qa] / 64, nc = b.ext[dp.ca] / 64;
+      const bool bytes = a.win == 1;
+      const int64_t g = bytes ? nq : std::min<int64_t>(kTileGroup, nq);
+      const int64_t full = nq / g * g;
+      a.t_plane = make_div(nq * nc);
+      a.t_group = make_div(g * nc);
+      a.t_g = make_div(g);
+      a.t_tail = make_div(nq - full > 0 ? nq - full : 1);
+      a.t_full = static_cast<uint32_t>(full);
+      a.t_xcd = bytes ? 1u : 0u;
+    }
     a.t_ssc = a.ss[dp.ca];
     a.t_dsq = a.ds[dp.qa];
     break;
@@ -791,11 +801,20 @@ void verify_launch(const DeviceProgram &dp, const KArgs &a) {
     if (a.work64 > (int64_t{1} << 22) || a.work != a.work64)
       bad_launch(dp, "more tiles than one launch takes");
     const int VO = 16 / wout;
-    for (uint32_t t = 0; t < a.work; ++t) {
-      const uint32_t r1 = fdiv(t, a.t_nq);
-      const uint32_t tq = t - r1 * a.t_nq.d;
-      const uint32_t r2 = fdiv(r1, a.t_nc);
-      const uint32_t tc = r1 - r2 * a.t_nc.d;
+    std::vector<bool> seen(a.work, false); // the order must be a bijection
+    for (uint32_t blk = 0; blk < a.work; ++blk) { // grid = one block per tile
+      const uint32_t t = a.t_xcd ? xcd_tile(blk, a.work) : blk;
+      if (t >= a.work)
+        bad_launch(dp, "a block maps past the last tile");
+      uint32_t tq, tc, r2;
+      tile_of(a, t, tq, tc, r2);
+      const uint32_t nc = a.t_group.d / a.t_g.d, nq = a.t_plane.d / nc;
+      if (tq >= nq || tc >= nc)
+        bad_launch(dp, "tile coordinates outside the plane");
+      const size_t id = (static_cast<size_t>(r2) * nq + tq) * nc + tc;
+      if (id >= seen.size() || seen[id])
+        bad_launch(dp, "the tile order visits a tile twice");
+      seen[id] = true;
       int64_t sbase = a.sbase, dbase = a.dbase;
       if (decompose_rt(kBatchLevels, a.lv, r2, sbase, dbase))
         bad_launch(dp, "a transpose tile reaches a pad");

@@ -108,6 +108,17 @@ constexpr int interleave_pixels(int win, int wout, int cp) {
   return g;
 }
 
+// Transpose tiles are visited in groups of this many q-tiles (destination
+// rows), c-tiles within a group: the blocks in flight write long runs of
+// few destination rows and read runs of kTileGroup tile rows. One-byte
+// sources (a tile row is half a 128-byte line, the other half belongs to the
+// next q-tile) instead walk q fastest with each XCD on a contiguous run, so
+// both halves of a line meet in one L2.
+#ifndef RELX_TILE_GROUP
+#define RELX_TILE_GROUP 16
+#endif
+constexpr uint32_t kTileGroup = RELX_TILE_GROUP;
+
 // Decomposition levels of the batch axes of the 2-D families.
 constexpr int kBatchLevels = 3;
 // Work items per launch of a fast kernel stay below this (32-bit indexing);
@@ -138,8 +149,12 @@ struct KArgs {
   int64_t sbase, dbase; // element offsets of the box origin (source: of its valid origin)
   Level lv[kMaxRank];   // stream: box axes (innermost in vectors); 2-D families: batch axes
   // transpose: tiles along the source-inner axis q (destination rows) and
-  // the destination-inner axis c
-  FastDiv t_nq, t_nc;
+  // the destination-inner axis c, visited in groups of g q-tiles (see
+  // tile_of): plane = nq * nc tiles, group = g * nc tiles, g, tail = the
+  // q-tiles of the last, partial group
+  FastDiv t_plane, t_group, t_g, t_tail;
+  uint32_t t_full; // q-tiles in whole groups
+  uint32_t t_xcd;  // 1: each XCD takes a contiguous run of the order
   int64_t t_ssc, t_dsq; // source stride of c, destination stride of q
   // interleave: pixel groups along the source-contiguous axis p; channel axis c
   FastDiv i_ng;
