@@ -26,12 +26,13 @@ __host__ __device__ __forceinline__ uint32_t chan_of(const DevStage &s, int64_t 
 
 // Decompose box-relative work index `i` over levels lv[0..L) (lv[0]
 // outermost, needing no division) into source/destination offsets added to
-// sof/dof. Returns true when any coordinate lies in a pad.
+// sof/dof (32-bit arithmetic: the relative spans are below 2^31). Returns true
+// when any coordinate lies in a pad.
 template <int L>
 __host__ __device__ __forceinline__ bool decompose(const Level *lv, uint32_t i, int64_t &sof,
                                                    int64_t &dof) {
   bool pad = false;
-  uint32_t rem = i;
+  uint32_t rem = i, s = 0, d = 0;
 #pragma unroll
   for (int k = L - 1; k >= 0; --k) {
     uint32_t u = rem;
@@ -40,11 +41,12 @@ __host__ __device__ __forceinline__ bool decompose(const Level *lv, uint32_t i, 
       u = rem - q * lv[k].div.d;
       rem = q;
     }
-    const int64_t uu = static_cast<int64_t>(u);
-    pad |= static_cast<uint64_t>(uu - lv[k].vmin) >= static_cast<uint64_t>(lv[k].vext);
-    sof += uu * lv[k].ss;
-    dof += uu * lv[k].ds;
+    pad |= u - lv[k].vlo >= lv[k].vcnt;
+    s += u * lv[k].ss;
+    d += u * lv[k].ds;
   }
+  sof += s;
+  dof += d;
   return pad;
 }
 

@@ -560,49 +560,93 @@ int64_t split_align(const DeviceProgram &dp, int i) {
   return 1;
 }
 
-// Split a fast-family box into boxes of fewer than 2^31 work items along the
-// outermost splittable axis (recursing inwards when one slab is too large).
+// Axes whose coordinates the decomposition levels carry (the others are the
+// 2-D block of the transpose/interleave kernels).
+bool level_axis(const DeviceProgram &dp, int i) {
+  const int r = dp.base.rank;
+  if (dp.family == kFamTranspose)
+    return i != dp.qa && i != dp.ca;
+  if (dp.family == kFamInterleave)
+    return i < r - 2;
+  return true;
+}
+
+// Largest element offset the levels of box b reach from its base, on the
+// source and the destination side; contrib[i] the larger of axis i's two.
+int64_t level_span(const DeviceProgram &dp, const Box &b, int64_t *contrib) {
+  int64_t ss = 0, ds = 0;
+  for (int i = 0; i < dp.base.rank; ++i) {
+    contrib[i] = 0;
+    if (!level_axis(dp, i) || b.ext[i] <= 1)
+      continue;
+    const int64_t s = (b.ext[i] - 1) * dp.base.ss[i], d = (b.ext[i] - 1) * dp.base.ds[i];
+    ss += s;
+    ds += d;
+    contrib[i] = std::max(s, d);
+  }
+  return std::max(ss, ds);
+}
+
+// Split a fast-family box until it has fewer than 2^31 work items and level
+// spans below 2^31 elements: halve (keeping alignment) the splittable axis
+// with the largest span contribution, or the outermost one for work alone.
 void split_box(const DeviceProgram &dp, const Box &b, std::vector<Box> &out) {
-  const int64_t w = box_work(dp, b);
-  if (dp.family == kFamGeneric || w < kMaxLaunchWork) {
+  if (dp.family == kFamGeneric) {
     out.push_back(b);
     return;
   }
+  int64_t contrib[kMaxRank];
+  const bool wide = level_span(dp, b, contrib) >= kMaxLaunchWork;
+  if (!wide && box_work(dp, b) < kMaxLaunchWork) {
+    out.push_back(b);
+    return;
+  }
+  int axis = -1;
   for (int i = 0; i < dp.base.rank; ++i) {
     const int64_t al = split_align(dp, i);
     if (al == 0 || b.ext[i] <= al)
       continue;
-    const int64_t groups = b.ext[i] / al; // the box extent is a multiple of al
-    const int64_t per = w / groups;       // work items per aligned group
-    const int64_t take = std::max<int64_t>(1, (kMaxLaunchWork - 1) / per) * al;
-    for (int64_t o = 0; o < b.ext[i]; o += take) {
-      Box c = b;
-      c.lo[i] = b.lo[i] + o;
-      c.ext[i] = std::min(take, b.ext[i] - o);
-      split_box(dp, c, out);
-    }
-    return;
+    if (axis < 0 || (wide && contrib[i] > contrib[axis]))
+      axis = i;
   }
-  fail("unsupported_layout", "a launch box cannot be split below 2^31 work items");
+  if (axis < 0)
+    fail("unsupported_layout", "a launch box cannot be split below 2^31 elements");
+  const int64_t al = split_align(dp, axis);
+  const int64_t half = (b.ext[axis] / al + 1) / 2 * al; // extents are multiples of al
+  Box c = b;
+  c.ext[axis] = half;
+  split_box(dp, c, out);
+  c.lo[axis] = b.lo[axis] + half;
+  c.ext[axis] = b.ext[axis] - half;
+  split_box(dp, c, out);
 }
 
 Level trivial_level() {
   Level l{};
   l.div = make_div(1);
-  l.vmin = 0;
-  l.vext = 1;
+  l.vlo = 0;
+  l.vcnt = 1;
   return l;
 }
 
 // Level of axis i counting units of `unit` coordinates (unit > 1 only on
-// unpadded axes whose box start is a multiple of unit).
+// unpadded axes whose box start is a multiple of unit). The valid units of
+// the box are [vlo, vlo + vcnt).
 Level axis_level(const KArgs &a, const Box &b, int i, int64_t unit) {
   Level l{};
-  l.div = make_div(b.ext[i] / unit);
-  l.ss = a.ss[i] * unit;
-  l.ds = a.ds[i] * unit;
-  l.vmin = (a.lo[i] - b.lo[i]) / unit;
-  l.vext = a.vext[i] / unit;
+  const int64_t n = b.ext[i] / unit;
+  l.div = make_div(n);
+  const int64_t vmin = (a.lo[i] - b.lo[i]) / unit, vmax = vmin + a.vext[i] / unit;
+  const int64_t lo = std::min(std::max<int64_t>(vmin, 0), n), hi = std::min(std::max<int64_t>(vmax, 0), n);
+  l.vlo = static_cast<uint32_t>(lo);
+  l.vcnt = static_cast<uint32_t>(hi - lo);
+  if (n > 1) { // a single coordinate never moves the offset
+    const int64_t ss = a.ss[i] * unit, ds = a.ds[i] * unit;
+    if (ss >= kMaxLaunchWork || ds >= kMaxLaunchWork || n >= kMaxLaunchWork)
+      fail("internal_launch_check", "a level stride exceeds 32 bits");
+    l.ss = static_cast<uint32_t>(ss);
+    l.ds = static_cast<uint32_t>(ds);
+  }
   return l;
 }
 
@@ -780,6 +824,17 @@ struct Checker {
 
 void verify_launch(const DeviceProgram &dp, const KArgs &a) {
   const Checker ck{dp, a, dp.wire_elems, dp.dst_elems, dp.pf.size(), dp.pi.size()};
+  if (dp.family != kFamGeneric) { // the levels' 32-bit offsets cannot wrap
+    int64_t ss = 0, ds = 0;
+    for (const Level &l : a.lv) {
+      ss += (int64_t{l.div.d} - 1) * l.ss;
+      ds += (int64_t{l.div.d} - 1) * l.ds;
+      if (int64_t{l.vlo} + l.vcnt > l.div.d)
+        bad_launch(dp, "a level's valid range leaves its extent");
+    }
+    if (ss >= kMaxLaunchWork || ds >= kMaxLaunchWork)
+      bad_launch(dp, "level offsets exceed 31 bits");
+  }
   const int win = a.win, wout = a.wout;
   switch (dp.family) {
   case kFamStream: {

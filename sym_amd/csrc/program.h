@@ -121,19 +121,21 @@ constexpr uint32_t kTileGroup = RELX_TILE_GROUP;
 
 // Decomposition levels of the batch axes of the 2-D families.
 constexpr int kBatchLevels = 3;
-// Work items per launch of a fast kernel stay below this (32-bit indexing);
-// the host splits larger boxes.
+// Work items per launch of a fast kernel, and the source and destination
+// element spans its decomposition levels reach, stay below this (32-bit
+// indexing); the host splits larger boxes.
 constexpr int64_t kMaxLaunchWork = int64_t{1} << 31;
 
 // One level of a fast kernel's index decomposition. A box-relative
 // coordinate u in [0, div.d) adds u * ss to the source and u * ds to the
-// destination offset (elements); it lies in the valid (unpadded) region iff
-// (u - vmin) < vext as unsigned 64-bit numbers. Unused outer levels have
-// d = 1 and zero strides.
+// destination offset (elements, relative to the launch's base offsets: the
+// host keeps every launch's relative spans below 2^31); it lies in the valid
+// (unpadded) region iff (u - vlo) < vcnt as unsigned 32-bit numbers. Unused
+// outer levels have d = 1 and zero strides.
 struct Level {
   FastDiv div;
-  int64_t ss, ds;
-  int64_t vmin, vext;
+  uint32_t ss, ds;
+  uint32_t vlo, vcnt;
 };
 
 // Launch arguments (by value). The fast families read only the first block,
