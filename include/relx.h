@@ -118,6 +118,9 @@ typedef struct relx_bound_info {
   int result_rank;
   int64_t result_extents[RELX_MAX_RANK];
   char kernel[32]; /* device kernel family the program runs */
+  int host_stages_max;  /* leading per-tensor stages a host may apply */
+  int host_stages_auto; /* of those, the narrowing ones applied for a pageable source */
+  int64_t wire_bytes_at[RELX_MAX_STAGES + 1]; /* H2D wire (source layout) at boundary k */
 } relx_bound_info;
 
 int relx_bound_query(const relx_bound *bound, relx_bound_info *out);

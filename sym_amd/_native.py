@@ -41,7 +41,9 @@ class relx_bound_info(ctypes.Structure):
                 ("source_width", ctypes.c_int), ("result_width", ctypes.c_int),
                 ("source_rank", ctypes.c_int), ("source_extents", _I64R),
                 ("result_rank", ctypes.c_int), ("result_extents", _I64R),
-                ("kernel", ctypes.c_char * 32)]
+                ("kernel", ctypes.c_char * 32), ("host_stages_max", ctypes.c_int),
+                ("host_stages_auto", ctypes.c_int),
+                ("wire_bytes_at", ctypes.c_int64 * (RELX_MAX_STAGES + 1))]
 
 
 class relx_ctx_stats(ctypes.Structure):

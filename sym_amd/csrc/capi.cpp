@@ -176,6 +176,22 @@ int relx_bound_query(const relx_bound *bound, relx_bound_info *out) {
   out->result_rank = static_cast<int>(b.result_extents.size());
   for (int i = 0; i < out->result_rank && i < RELX_MAX_RANK; ++i)
     out->result_extents[i] = b.result_extents[static_cast<size_t>(i)];
+  out->host_stages_max = 0;
+  for (const relx::HostStage &st : bound->h.prep.stages) {
+    if (st.mode != relx::kChanNone)
+      break;
+    ++out->host_stages_max;
+  }
+  out->host_stages_auto = static_cast<int>(relx::auto_host_stages(bound->h));
+  {
+    int64_t elems = 1;
+    for (int64_t e : b.source_extents)
+      elems *= e;
+    const auto &st = bound->h.prep.stages;
+    for (size_t k = 0; k <= st.size() && k <= RELX_MAX_STAGES; ++k)
+      out->wire_bytes_at[k] =
+          elems * (k == 0 ? static_cast<int64_t>(out->source_width) : st[k - 1].out_width);
+  }
   try {
     const relx::DeviceProgram &dp = const_cast<relx::BoundHandle &>(bound->h).program(0);
     std::snprintf(out->kernel, sizeof(out->kernel), "%s", dp.kernel);

@@ -264,6 +264,8 @@ bool probe_pinned(const void *p) {
 // Leading stages the host applies while staging: per-tensor stages that do
 // not widen the element (so the wire shrinks or stays), stopping at the
 // first per-channel or widening stage.
+} // namespace
+
 uint32_t auto_host_stages(const BoundHandle &h) {
   if (!h.bound->typed)
     return 0;
@@ -277,6 +279,8 @@ uint32_t auto_host_stages(const BoundHandle &h) {
   }
   return k;
 }
+
+namespace {
 
 struct Member {
   BoundHandle *h;

@@ -121,6 +121,10 @@ struct BoundHandle {
   ~BoundHandle();
 };
 
+// Leading per-tensor narrowing stages applied on the host for a pageable
+// source (halving PCIe bytes where a cast narrows).
+uint32_t auto_host_stages(const BoundHandle &h);
+
 // verify_launch over every launch of the chunk schedule for `chunk_bytes`
 // (and the whole-box launch of the device-resident path); returns the count.
 int64_t verify_launches(BoundHandle &h, uint32_t k, int64_t chunk_bytes);

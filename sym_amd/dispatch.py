@@ -1,0 +1,336 @@
+"""Typed dispatch in the shape of the reference's pyreloc dispatch API.
+
+The reference prepares a single-use request from a bound typed plan and two
+buffer views, selects one "implementation row", and executes it
+(libreloc/python/PyDispatch.cpp:86-235,517-901; libreloc/src/Dispatch.cpp:
+1147-1218,1382-1532,1983-2046). Its rows include CPU executors; this build
+has exactly one kind of row, the device relayout, offered at each wire
+boundary a host may reach with per-tensor stages:
+
+    hip_relayout        the source bytes cross PCIe; every stage on the GPU
+    hip_relayout@k      the host applies stages [0, k) while staging
+
+Names, argument meaning and error codes follow the reference so that
+`reloc_torch.dispatch` can call these functions in place of `_pyreloc`'s.
+Requests whose policy asks for a CPU executor ("original_cpu"), a forced
+row this build lacks, or the D2H direction raise
+TransferError("implementation_unavailable" / "direction_mismatch").
+"""
+import threading
+
+from . import pyreloc as P
+from .pyreloc import TransferError
+
+POLICIES = ("auto", "original_cpu")
+_KINDS = {"host": "host", "cuda": "cuda", "device": "cuda"}
+
+
+class BufferView:
+    """Memory seen as a strided tensor (reference pyreloc.BufferView,
+    libreloc/python/PyTransfer.cpp:62-76,312-330): base address, capacity
+    in bytes from the base, byte offset of element 0, extents, strides in
+    elements, element size in bytes, kind "host" or "cuda", device ordinal."""
+
+    def __init__(self, base, capacity_bytes, offset_bytes, extents, strides, element_size,
+                 kind, device=-1):
+        if kind not in _KINDS:
+            raise ValueError("kind must be 'host' or 'cuda', got %r" % (kind,))
+        extents, strides = [int(e) for e in extents], [int(s) for s in strides]
+        if len(extents) != len(strides):
+            raise ValueError("extents and strides differ in rank")
+        self.base = int(base)
+        self.capacity_bytes = int(capacity_bytes)
+        self.offset_bytes = int(offset_bytes)
+        self.extents = extents
+        self.strides = strides
+        self.element_size = int(element_size)
+        self.kind = _KINDS[kind]
+        self.device = int(device)
+
+    @property
+    def address(self):
+        return self.base + self.offset_bytes
+
+    def is_dense(self):
+        """Row-major dense (the only layout typed dispatch accepts)."""
+        running = 1
+        for e, s in zip(reversed(self.extents), reversed(self.strides)):
+            if e != 1 and s != running:
+                return False
+            running *= e
+        return True
+
+    def span_bytes(self):
+        """Bytes from the base the view can reach (offset included)."""
+        if any(e == 0 for e in self.extents):
+            return self.offset_bytes
+        last = sum((e - 1) * s for e, s in zip(self.extents, self.strides))
+        return self.offset_bytes + (last + 1) * self.element_size
+
+    def __repr__(self):
+        return "BufferView(%s, extents=%s, strides=%s, element_size=%d)" % (
+            self.kind, self.extents, self.strides, self.element_size)
+
+
+def _label(k):
+    return "hip_relayout" if k == 0 else "hip_relayout@%d" % k
+
+
+def _row(bound, k):
+    wire = bound.info.wire_bytes_at[k]  # the source layout, staged to boundary k
+    return {"implementation": _label(k), "wire_boundary": k, "wire_result_layout": False,
+            "wire_bytes": wire, "device_temp_bytes": wire, "method": "device_relayout"}
+
+
+def query_capability(bound, direction, device):
+    """Eligible and excluded rows (reference query_capability,
+    libreloc/src/Dispatch.cpp:1382-1532)."""
+    if device not in ("host", "cuda"):
+        raise ValueError("device must be 'host' or 'cuda', got '%s'" % device)
+    if direction not in ("h2d", "d2h"):
+        raise ValueError("direction must be 'h2d' or 'd2h', got '%s'" % direction)
+    if not bound.typed:
+        raise TransferError("typed_unsupported", "layout plans dispatch through execute_transfer")
+    if direction == "d2h":
+        return {"eligible": [], "excluded": [{"implementation": "hip_relayout",
+                                              "reason": "direction_unsupported"}]}
+    if device == "host":
+        return {"eligible": [], "excluded": [{"implementation": "hip_relayout",
+                                              "reason": "host_destination"}]}
+    rows = [_row(bound, k) for k in range(bound.info.host_stages_max + 1)]
+    excluded = [{"implementation": _label(k), "reason": "per_channel_stage_on_host"}
+                for k in range(bound.info.host_stages_max + 1, bound.stage_count + 1)]
+    return {"eligible": rows, "excluded": excluded}
+
+
+class DispatchTemplate:
+    """Bound plan + selected row, reusable for many views (reference
+    DispatchTemplate, libreloc/include/reloc/Dispatch.h:104-124)."""
+
+    def __init__(self, bound, direction, capability, selection, threads):
+        self.bound = bound
+        self.program = bound
+        self.direction = direction
+        self.capability = capability
+        self.selection = selection
+        self.threads = threads
+
+
+class DispatchRequest:
+    """Single-use request: template + validated views (reference
+    DispatchRequest, libreloc/include/reloc/Dispatch.h:126-175)."""
+
+    def __init__(self, template, source, destination):
+        self.template = template
+        self.source = source
+        self.destination = destination
+        self.selected = dict(template.selection)
+        self.report = {}
+        self.executing = False
+        self.consumed = False
+        self._lock = threading.Lock()
+
+
+def _select(bound, direction, capability, policy, implementation):
+    if policy not in POLICIES:
+        raise ValueError("policy must be 'auto' or 'original_cpu', got '%s'" % policy)
+    if direction != "h2d":
+        raise TransferError("direction_mismatch", "this build runs host-to-device dispatch only")
+    if policy == "original_cpu":
+        raise TransferError("implementation_unavailable",
+                            "no CPU executor row: every plan runs on the device")
+    labels = [r["implementation"] for r in capability["eligible"]]
+    if implementation:
+        if implementation not in labels:
+            raise TransferError("implementation_unavailable",
+                                "row '%s' is not eligible (eligible: %s)" % (implementation,
+                                                                           ", ".join(labels)))
+        return {"implementation": implementation, "policy": policy, "placement_reason": "forced",
+                "host_stages": labels.index(implementation)}
+    auto = bound.info.host_stages_auto
+    return {"implementation": _label(auto), "policy": policy,
+            "placement_reason": "device_relayout", "host_stages": -1}
+
+
+def prepare_dispatch_template(bound, direction, device="cuda", *, policy="auto", calibration=None,
+                              threads=8, implementation=""):
+    """Validate the program, enumerate the rows and select one; allocates
+    and launches nothing (reference prepare_dispatch_template)."""
+    if int(threads) < 1:
+        raise ValueError("threads must be >= 1")
+    capability = query_capability(bound, direction, device)
+    selection = _select(bound, direction, capability, policy, implementation)
+    return DispatchTemplate(bound, direction, capability, selection, int(threads))
+
+
+def _check_views(bound, source, destination, direction):
+    info = bound.info
+    if direction == "h2d" and (source.kind != "host" or destination.kind != "cuda"):
+        raise TransferError("direction_mismatch",
+                            "h2d moves a host source into a cuda destination, got %s -> %s"
+                            % (source.kind, destination.kind))
+    for name, view, extents, width in (
+            ("source", source, list(info.source_extents[:info.source_rank]), info.source_width),
+            ("destination", destination, list(info.result_extents[:info.result_rank]),
+             info.result_width)):
+        if view.extents != extents or view.element_size != width:
+            raise TransferError("plan_mismatch", "%s view is %s x %d B, the plan needs %s x %d B"
+                                % (name, view.extents, view.element_size, extents, width))
+        if not view.is_dense():
+            raise TransferError("invalid_view", "%s view is not dense row-major" % name)
+        if view.span_bytes() > view.capacity_bytes:
+            raise TransferError("insufficient_capacity", "%s view reaches %d bytes of %d"
+                                % (name, view.span_bytes(), view.capacity_bytes))
+
+
+def prepare_dispatch_from_template(template, source, destination):
+    _check_views(template.bound, source, destination, template.direction)
+    return DispatchRequest(template, source, destination)
+
+
+def prepare_dispatch(bound, source, destination, direction, *, policy="auto", calibration=None,
+                     threads=8, implementation=""):
+    """Template + views in one step (reference prepare_dispatch,
+    libreloc/python/PyDispatch.cpp:131-157)."""
+    t = prepare_dispatch_template(bound, direction, "cuda", policy=policy, calibration=calibration,
+                                  threads=threads, implementation=implementation)
+    return prepare_dispatch_from_template(t, source, destination)
+
+
+class Resources(P.Context):
+    """Retained streams, pinned ring and device wire scratch reused across
+    requests (reference dispatch::Resources,
+    libreloc/src/DispatchResources.cpp:44,552-686)."""
+
+
+_default = {}
+_default_lock = threading.Lock()
+
+
+def _resources_for(device):
+    with _default_lock:
+        ctx = _default.get(device)
+        if ctx is None:
+            ctx = _default[device] = Resources(device)
+        return ctx
+
+
+def _pinning(pinning):
+    if pinning not in ("auto", "pinned", "pageable"):
+        raise ValueError("pinning must be auto, pinned or pageable")
+    # the source's own memory kind is probed; staging always goes through the
+    # context's pinned ring
+    return -1
+
+
+def _report(rep, request):
+    sel = request.selected
+    return {"implementation": rep["implementation"], "policy": sel["policy"],
+            "placement_reason": sel["placement_reason"], "method": "device_relayout",
+            "wire_boundary": rep["wire_boundary"], "source_bytes": rep["source_bytes"],
+            "wire_bytes": rep["wire_bytes"], "destination_bytes": rep["destination_bytes"],
+            "parameter_bytes": rep["parameter_bytes"],
+            "payload_bytes_transferred": rep["payload_bytes_transferred"],
+            "device_temp_bytes": rep["wire_bytes"], "artifact_version": 1, "executed": True,
+            "host_pipeline": "pinned_ring" if not rep["direct_dma"] else "direct_dma",
+            "host_kernel": "host_stages" if rep["wire_boundary"] else "copy",
+            "host_chunks": rep["chunks"], "host_chunk_bytes": 0, "host_buffers": 0,
+            "kernel_launches": rep["kernel_launches"], "staging": []}
+
+
+def execute_dispatch(request, *, caller_stream=None, n_buffers=2, n_streams=2, gather_threads=1,
+                     gather_pool=None, pinning="auto", min_pinned_bytes=None,
+                     direct_dense_upload=True, pipeline=True, chunk_size=0, resources=None,
+                     owners=None):
+    """Run the selected row and block until it completed; returns the report
+    (reference execute_dispatch, libreloc/python/PyDispatch.cpp:159-235)."""
+    if not request._lock.acquire(blocking=False) or request.executing:
+        raise TransferError("already_executed", "typed request is executing")
+    try:
+        if request.consumed:
+            raise TransferError("already_executed", "typed request was already executed")
+        if n_buffers < 1:
+            raise ValueError("n_buffers must be >= 1")
+        if n_streams < 1:
+            raise ValueError("n_streams must be >= 1")
+        if gather_threads < 0:
+            raise ValueError("gather_threads must be >= 0 (0 = all cores)")
+        request.executing = True
+        ctx = resources if resources is not None else _resources_for(max(0, request.destination.device))
+        src, dst = request.source, request.destination
+        rep = ctx.execute_h2d(request.template.bound, src.address, src.capacity_bytes - src.offset_bytes,
+                              dst.address, dst.capacity_bytes - dst.offset_bytes,
+                              n_buffers=n_buffers, chunk_bytes=int(chunk_size or 0),
+                              host_stages=request.selected["host_stages"],
+                              gather_threads=gather_threads, source_pinned=_pinning(pinning),
+                              caller_stream=int(caller_stream or 0))
+        request.consumed = True
+        request.report = _report(rep, request)
+        return dict(request.report)
+    finally:
+        request.executing = False
+        request._lock.release()
+
+
+class GroupRequest:
+    """Members executed as one schedule with one completion (reference
+    GroupRequest, libreloc/include/reloc/Dispatch.h:177-214)."""
+
+    def __init__(self, items):
+        self.items = items
+        self.consumed = False
+        self.executing = False
+        self.report = {}
+
+
+def prepare_dispatch_group(entries):
+    """entries: (template or bound plan, source view, destination view,
+    direction) tuples (reference prepare_dispatch_group)."""
+    items = []
+    for plan, source, destination, direction in entries:
+        t = plan if isinstance(plan, DispatchTemplate) else prepare_dispatch_template(plan, direction)
+        items.append(prepare_dispatch_from_template(t, source, destination))
+    if not items:
+        raise TransferError("invalid_options", "an empty group")
+    if len(items) > 256:
+        raise TransferError("invalid_options", "a group holds at most 256 items")
+    return GroupRequest(items)
+
+
+def execute_dispatch_group(group, *, caller_stream=None, gather_threads=1, gather_pool=None,
+                           pinning="auto", min_pinned_bytes=None, max_scratch_bytes=1 << 62,
+                           resources=None, owners=None, device_layout=False, n_buffers=2,
+                           chunked_members=True):
+    """All members through one ring and one barrier; returns the group
+    report with per-item reports (reference execute_dispatch_group,
+    libreloc/src/Dispatch.cpp:1833-1981)."""
+    if group.executing or group.consumed:
+        raise TransferError("already_executed", "group is executing or already executed")
+    if gather_threads < 1 or not max_scratch_bytes:
+        raise ValueError("gather_threads and max_scratch_bytes must be positive")
+    _pinning(pinning)
+    group.executing = True
+    try:
+        dev = max(0, group.items[0].destination.device)
+        ctx = resources if resources is not None else _resources_for(dev)
+        bounds = [r.template.bound for r in group.items]
+        srcs = [(r.source.address, r.source.capacity_bytes - r.source.offset_bytes) for r in group.items]
+        dsts = [(r.destination.address, r.destination.capacity_bytes - r.destination.offset_bytes)
+                for r in group.items]
+        reps, total = ctx.execute_group_h2d(bounds, srcs, dsts, n_buffers=n_buffers,
+                                            gather_threads=gather_threads,
+                                            caller_stream=int(caller_stream or 0))
+        items = []
+        for r, rep in zip(group.items, reps):
+            r.consumed = True
+            r.report = _report(rep, r)
+            items.append(dict(r.report))
+        group.consumed = True
+        group.report = {"logical_transfers": len(items), "request_count": 1,
+                        "completion_granularity": "group",
+                        "payload_copy_calls": sum(i["host_chunks"] for i in items),
+                        "kernel_launches": sum(i["kernel_launches"] for i in items),
+                        "output_bytes": total["destination_bytes"], "staging": [], "items": items}
+        return dict(group.report)
+    finally:
+        group.executing = False

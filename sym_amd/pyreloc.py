@@ -136,6 +136,10 @@ class Bound:
         self.info = info
 
     @property
+    def typed(self):
+        return bool(self.info.typed)
+
+    @property
     def extents(self):
         return list(self.info.extents[:self.info.rank])
 
@@ -307,3 +311,11 @@ def host_stage(bound, host_stages, src_ptr, wire_ptr, threads=8):
 def measure_h2d(device=0, nbytes=256 << 20, iters=20, rounds=3):
     """Pinned H2D ceiling in GB/s (bench/rtrack/multigpu_h2d.cu:46-91 restated)."""
     return N.lib().relx_measure_h2d(int(device), int(nbytes), int(iters), int(rounds))
+
+
+# The typed dispatch API (prepare_dispatch / execute_dispatch / groups) lives
+# in sym_amd.dispatch and is re-exported here under pyreloc's names.
+from .dispatch import (BufferView, DispatchRequest, DispatchTemplate,  # noqa: E402,F401
+                       GroupRequest, Resources, execute_dispatch, execute_dispatch_group,
+                       prepare_dispatch, prepare_dispatch_from_template, prepare_dispatch_group,
+                       prepare_dispatch_template, query_capability)

@@ -1,0 +1,119 @@
+"""The reference-shaped dispatch API on the MI355X: the typed corpus and a
+grouped C4-like step through prepare_dispatch / execute_dispatch (and the
+template and group forms), bit-exact against the corpus expectations and
+the oracle, with the reference's report fields and single-use rules."""
+import hashlib
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import relx_oracle as O
+from sym_amd import pyreloc as P
+from sym_amd import workloads as W
+from tests import golden_io as G
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+
+def say(*a):
+    print("[gpu-case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+def host_view(a):
+    return P.BufferView(a.ctypes.data, a.nbytes, 0, list(a.shape),
+                        [s // a.dtype.itemsize for s in a.strides], a.dtype.itemsize, "host")
+
+
+def device_view(t):
+    return P.BufferView(t.data_ptr(), t.numel() * t.element_size(), 0, list(t.shape),
+                        list(t.stride()), t.element_size(), "cuda", t.device.index)
+
+
+TORCH = {"f16": torch.float16, "f32": torch.float32, "i8": torch.int8, "bf16": torch.bfloat16,
+         "u8": torch.uint8, "i32": torch.int32}
+
+
+@pytest.fixture(scope="module")
+def resources():
+    assert torch.cuda.is_available(), "a GPU test needs the MI355X"
+    r = P.Resources(0)
+    yield r
+    r.close()
+
+
+TYPED = G.typed_fixtures()
+
+
+@pytest.mark.parametrize("meta,blob", TYPED, ids=[m["name"] for m, _ in TYPED])
+def test_corpus_through_dispatch(resources, meta, blob):
+    plan = P.load_typed_plan(blob)
+    for binding in meta["bindings"]:
+        src = np.ascontiguousarray(G.bits_array(binding["source"]).reshape(binding["source"]["shape"]))
+        exp = G.bits_array(binding["expected"]).reshape(binding["expected"]["shape"])
+        b = P.bind_typed(plan, binding["symbols"], G.fixture_params(meta))
+        rows = [r["implementation"] for r in P.query_capability(b, "h2d", "cuda")["eligible"]]
+        for impl in [""] + rows:
+            say(meta["name"], binding["symbols"], "row", impl or "auto")
+            out = torch.empty(list(exp.shape), dtype=torch.uint8 if exp.dtype.itemsize == 1
+                              else {2: torch.int16, 4: torch.int32, 8: torch.int64}[exp.dtype.itemsize],
+                              device="cuda")
+            req = P.prepare_dispatch(b, host_view(src), device_view(out), "h2d", implementation=impl)
+            rep = P.execute_dispatch(req, resources=resources)
+            torch.cuda.synchronize()
+            got = out.cpu().numpy().view(exp.dtype)
+            assert np.array_equal(got, exp), (meta["name"], impl)
+            assert hashlib.sha256(got.tobytes()).hexdigest() == binding["expected"]["sha256"]
+            fp = binding["footprints"]["h2d"]
+            for key in ("source_bytes", "destination_bytes", "parameter_bytes"):
+                assert rep[key] == fp[key], (meta["name"], key)
+            assert rep["executed"] is True and rep["payload_bytes_transferred"] == rep["wire_bytes"]
+            if impl:
+                assert rep["implementation"] == impl and rep["placement_reason"] == "forced"
+            with pytest.raises(P.TransferError) as e:
+                P.execute_dispatch(req, resources=resources)
+            assert e.value.code == "already_executed"
+
+
+def test_template_reuse_over_many_views(resources, rng):
+    plan = P.Plan(W.c2_plan(n=2).blob)
+    b = P.Bound(plan, {}, {})
+    t = P.prepare_dispatch_template(b, "h2d", "cuda")
+    for seed in range(3):
+        x = np.random.default_rng(seed).standard_normal((2, 3, 224, 224), dtype=np.float32)
+        out = torch.empty((2, 224, 224, 4), dtype=torch.float16, device="cuda")
+        say("template reuse", seed)
+        rep = P.execute_dispatch(P.prepare_dispatch_from_template(t, host_view(x), device_view(out)),
+                                 resources=resources)
+        torch.cuda.synchronize()
+        want = np.zeros((2, 224, 224, 4), np.float16)
+        want[..., :3] = np.transpose(x, (0, 2, 3, 1)).astype(np.float16)
+        assert np.array_equal(out.cpu().numpy().view(np.uint16), want.view(np.uint16))
+        assert rep["implementation"] == "hip_relayout@1"  # pageable source: the cast is staged
+
+
+def test_group_dispatch_c4_like(resources, rng):
+    rows, cols = 512, 256
+    plan = P.Plan(W.c4_plan().blob)
+    entries, outs, wants, keep = [], [], [], []
+    for j in range(6):
+        q = W.int8_weight(rows, cols, rng)
+        s = W.scales(rows, rng)
+        keep.append(q)  # views borrow the memory: the arrays must outlive the call
+        b = P.Bound(plan, {"s0": rows, "s1": cols}, W.param("scale", s))
+        out = torch.empty((rows, cols), dtype=torch.float16, device="cuda")
+        entries.append((b, host_view(q), device_view(out), "h2d"))
+        outs.append(out)
+        deq = np.ascontiguousarray(O.dequantize_s8_f32(q, s[:, None], np.int32(0)), np.float32)
+        wants.append(O.narrow_f32_f16_bits(deq.view(np.uint32)).astype(np.uint16).tobytes())
+    say("group of 6", rows, cols)
+    g = P.prepare_dispatch_group(entries)
+    rep = P.execute_dispatch_group(g, resources=resources, owners=(tuple(keep), tuple(outs)))
+    torch.cuda.synchronize()
+    assert rep["logical_transfers"] == 6 and rep["completion_granularity"] == "group"
+    for out, want in zip(outs, wants):
+        assert out.cpu().numpy().tobytes() == want
+    with pytest.raises(P.TransferError):
+        P.execute_dispatch_group(g, resources=resources)
