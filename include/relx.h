@@ -205,6 +205,21 @@ int relx_execute_group_h2d(relx_ctx *ctx, int n, const relx_bound *const *bounds
                            const size_t *dst_bytes, const relx_options *opt,
                            relx_report *reports, relx_report *total, relx_err *err);
 
+/* Device-resident source -> host destination: the D2H direction of
+ * dispatch::executeDispatch / executeTransfer (libreloc/src/Transfer.cpp:469-488,
+ * libreloc/src/Dispatch.cpp:1072-1099,1513-1530; the reference's
+ * cuda_stages_then_cpu rows). The device runs the relayout and every stage
+ * into the context's device result buffer, one chunk of destination rows at
+ * a time, and each chunk is copied to the host while the next chunk's kernel
+ * runs. For this call `opt->source_pinned` describes the HOST buffer (the
+ * destination): 1 pinned (direct DMA), 0 pageable (pinned ring, worker
+ * threads copy each slot out), -1 probe; `host_stages` must be 0 or -1. The
+ * source is ordered after `opt->caller_stream`. Blocks until the
+ * destination holds the result. */
+int relx_execute_d2h(relx_ctx *ctx, const relx_bound *bound, const void *src, size_t src_bytes,
+                     void *dst, size_t dst_bytes, const relx_options *opt, relx_report *report,
+                     relx_err *err);
+
 /* Device-resident relayout: `wire` is already in device memory (dense source
  * layout at boundary `wire_boundary`); run the relayout + stages
  * [wire_boundary, stages) into `dst` on `stream` (0 = the context's compute

@@ -97,6 +97,8 @@ SIGNATURES = {
                                     ctypes.POINTER(relx_options), ctypes.POINTER(relx_report),
                                     ctypes.POINTER(relx_report), _E]),
     "relx_relayout_device": (_I, [_VP, _VP, _I, _VP, _VP, _U64, _E]),
+    "relx_execute_d2h": (_I, [_VP, _VP, _VP, _SZ, _VP, _SZ, ctypes.POINTER(relx_options),
+                              ctypes.POINTER(relx_report), _E]),
     "relx_host_stage": (_I, [_VP, _I, _VP, _VP, _I, _E]),
     "relx_verify_launches": (_I, [_VP, _I, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64), _E]),
     "relx_ctx_synchronize": (_I, [_VP, _E]),

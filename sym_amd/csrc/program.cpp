@@ -729,17 +729,35 @@ KArgs launch_args(const DeviceProgram &dp, const Box &b) {
 std::vector<KArgs> box_launches(const DeviceProgram &dp, int64_t v0, int64_t v1, bool first,
                                 bool last) {
   const KArgs &a = dp.base;
+  if (dp.chunk_axis < 0)
+    return axis_launches(dp, -1, 0, 0);
+  const int ax = dp.chunk_axis;
+  const int64_t plo = first ? 0 : v0 + a.lo[ax];
+  const int64_t phi = last ? a.pext[ax] : v1 + a.lo[ax];
+  return axis_launches(dp, ax, plo, phi);
+}
+
+int64_t axis_align(const DeviceProgram &dp, int i) { return split_align(dp, i); }
+
+std::vector<KArgs> axis_launches(const DeviceProgram &dp, int axis, int64_t plo, int64_t phi) {
+  return prefix_launches(dp, nullptr, axis, plo, phi);
+}
+
+std::vector<KArgs> prefix_launches(const DeviceProgram &dp, const int64_t *fixed, int axis,
+                                   int64_t plo, int64_t phi) {
+  const KArgs &a = dp.base;
   Box b{};
   for (int i = 0; i < a.rank; ++i) {
     b.lo[i] = 0;
     b.ext[i] = a.pext[i];
   }
-  if (dp.chunk_axis >= 0) {
-    const int ax = dp.chunk_axis;
-    const int64_t plo = first ? 0 : v0 + a.lo[ax];
-    const int64_t phi = last ? a.pext[ax] : v1 + a.lo[ax];
-    b.lo[ax] = plo;
-    b.ext[ax] = phi - plo;
+  if (axis >= 0) {
+    for (int i = 0; fixed && i < axis; ++i) {
+      b.lo[i] = fixed[i];
+      b.ext[i] = 1;
+    }
+    b.lo[axis] = plo;
+    b.ext[axis] = phi - plo;
   }
   std::vector<Box> boxes;
   split_box(dp, b, boxes);
@@ -949,12 +967,17 @@ bool verify_enabled() {
 int64_t launch_program(const DeviceProgram &dp, int64_t v0, int64_t v1, bool first, bool last,
                        const void *src, void *dst, const float *pf, const int32_t *pi,
                        int32_t *status, hipStream_t s) {
+  return launch_all(dp, box_launches(dp, v0, v1, first, last), src, dst, pf, pi, status, s);
+}
+
+int64_t launch_all(const DeviceProgram &dp, std::vector<KArgs> launches, const void *src,
+                   void *dst, const float *pf, const int32_t *pi, int32_t *status, hipStream_t s) {
   // the fast kernels move 16-byte vectors: buffers that are not 16-byte
   // aligned take the element-wise kernel
   const bool aligned = reinterpret_cast<uintptr_t>(src) % 16 == 0 &&
                        reinterpret_cast<uintptr_t>(dst) % 16 == 0;
   int64_t n = 0;
-  for (KArgs &a : box_launches(dp, v0, v1, first, last)) {
+  for (KArgs &a : launches) {
     int family = dp.family;
     if (!aligned && family != kFamGeneric) {
       family = kFamGeneric;

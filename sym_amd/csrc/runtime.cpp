@@ -471,6 +471,169 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
   }
 }
 
+// --------------------------------------------------------------- D2H
+
+D2hPlan d2h_plan(const DeviceProgram &dp, int64_t chunk_bytes) {
+  const KArgs &a = dp.base;
+  const int64_t out_bytes = dp.dst_elems * a.wout;
+  D2hPlan p{-1, 1, 1, 1, out_bytes};
+  bool dense = true;
+  int64_t run = 1;
+  for (int k = a.rank - 1; k >= 0; --k) {
+    dense = dense && a.ds[k] == run;
+    run *= a.pext[k];
+  }
+  if (!dense || run != dp.dst_elems || a.rank < 1)
+    return p;
+  const int64_t want = chunk_bytes > 0 ? chunk_bytes : kDefaultChunkBytes;
+  // the outermost axis one coordinate of which fits a chunk; the axes before
+  // it must accept single-coordinate boxes
+  int64_t outer = 1;
+  for (int j = 0; j < a.rank; ++j) {
+    const int64_t al = axis_align(dp, j);
+    const int64_t row = out_bytes / outer / a.pext[j];
+    if (al <= 0)
+      return p;
+    if (row * al <= want || j == a.rank - 1) {
+      if (a.pext[j] <= al && outer == 1)
+        return p; // one chunk
+      p.axis = j;
+      p.outer = outer;
+      p.units = a.pext[j];
+      p.row = row;
+      int64_t per = std::max<int64_t>(1, want / std::max<int64_t>(1, row));
+      per = std::max<int64_t>(al, per / al * al);
+      p.per = std::min(per, p.units);
+      return p;
+    }
+    if (al != 1)
+      return p; // a fixed coordinate would break the axis' alignment
+    outer *= a.pext[j];
+  }
+  return p;
+}
+
+// Device -> host: the device runs the relayout and every stage, one
+// destination-row chunk at a time, into the context's device result buffer;
+// each chunk then crosses PCIe while the next chunk's kernel runs. A pinned
+// destination takes the DMA directly; a pageable one goes through the pinned
+// ring and the worker threads copy each slot out as soon as its copy lands.
+void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes, void *dst,
+                 size_t dst_bytes, const relx_options &opt, relx_report *report) {
+  DeviceGuard guard(ctx.device);
+  const DeviceProgram &dp = h.program(0);
+  const Bound &b = *h.bound;
+  if (!src || !dst)
+    throw Error("invalid_view", "null source or destination");
+  if (static_cast<int64_t>(src_bytes) < dp.wire_bytes)
+    throw Error("insufficient_capacity", "source holds " + std::to_string(src_bytes) +
+                                             " bytes, the plan reads " +
+                                             std::to_string(dp.wire_bytes));
+  const int64_t out_bytes = dp.dst_elems * dp.base.wout;
+  if (static_cast<int64_t>(dst_bytes) < out_bytes)
+    throw Error("insufficient_capacity", "destination holds " + std::to_string(dst_bytes) +
+                                             " bytes, the plan writes " +
+                                             std::to_string(out_bytes));
+  ensure_wire(ctx, static_cast<size_t>(out_bytes)); // the device result
+  const bool pinned = opt.source_pinned > 0 || (opt.source_pinned < 0 && probe_pinned(dst));
+
+  const D2hPlan plan = d2h_plan(dp, opt.chunk_bytes);
+  const int axis = plan.axis;
+  const int64_t units = plan.units, row = plan.row, per = plan.per;
+  const KArgs &a = dp.base;
+  const int nslots = opt.n_buffers > 0 ? opt.n_buffers : 3;
+  if (!pinned)
+    ensure_ring(ctx, nslots, static_cast<size_t>(per * row));
+  const unsigned threads = opt.gather_threads > 0 ? static_cast<unsigned>(opt.gather_threads) : 8u;
+  if (!ctx.workers || ctx.worker_threads != threads) {
+    ctx.workers = std::make_unique<Workers>(threads);
+    ctx.worker_threads = threads;
+  }
+  hipStream_t caller = reinterpret_cast<hipStream_t>(opt.caller_stream);
+  if (caller) { // the source is produced on the caller's stream
+    HIPCHECK(hipEventRecord(ctx.start_ev, caller));
+    HIPCHECK(hipStreamWaitEvent(ctx.compute, ctx.start_ev, 0));
+    HIPCHECK(hipStreamWaitEvent(ctx.copy, ctx.start_ev, 0));
+  }
+  if (dp.family == kFamGeneric)
+    HIPCHECK(hipMemsetAsync(ctx.status, 0, sizeof(int32_t), ctx.compute));
+  const BoundHandle::DevParams par = h.device_params(ctx.device, 0);
+  uint8_t *result = ctx.wire;
+  uint8_t *out = static_cast<uint8_t *>(dst);
+  struct Pending {
+    int slot;
+    int64_t off, bytes;
+  };
+  std::vector<Pending> pending; // copies issued, not yet copied out of their slot
+  size_t next = 0;
+  auto consume = [&](const Pending &p) {
+    HIPCHECK(hipEventSynchronize(ctx.slot_ev[static_cast<size_t>(p.slot)]));
+    const uint8_t *from = static_cast<const uint8_t *>(ctx.slots[static_cast<size_t>(p.slot)]);
+    ctx.workers->parallel_for(p.bytes, int64_t{1} << 20, [&](int64_t x, int64_t y) {
+      std::memcpy(out + p.off + x, from + x, static_cast<size_t>(y - x));
+    });
+  };
+  int64_t chunks = 0, launches = 0;
+  int ev = 0;
+  int64_t fixed[kMaxRank] = {};
+  for (int64_t o = 0; o < plan.outer; ++o) {
+   int64_t rem = o; // coordinates of the axes before `axis`
+   for (int j = axis - 1; j >= 0; --j) {
+     fixed[j] = rem % a.pext[j];
+     rem /= a.pext[j];
+   }
+   for (int64_t u0 = 0; u0 < units; u0 += per) {
+    const int64_t u1 = std::min(units, u0 + per);
+    launches += launch_all(dp, prefix_launches(dp, fixed, axis, u0, u1), src, result, par.pf,
+                           par.pi, ctx.status, ctx.compute);
+    hipEvent_t ke = ctx.chunk_ev[static_cast<size_t>(ev)];
+    ev = (ev + 1) % kChunkEvents;
+    HIPCHECK(hipEventRecord(ke, ctx.compute));
+    HIPCHECK(hipStreamWaitEvent(ctx.copy, ke, 0));
+    const int64_t off = (o * units + u0) * row, bytes = (u1 - u0) * row;
+    if (pinned) {
+      HIPCHECK(hipMemcpyAsync(out + off, result + off, static_cast<size_t>(bytes),
+                              hipMemcpyDeviceToHost, ctx.copy));
+    } else {
+      const int slot = static_cast<int>(chunks % nslots);
+      if (pending.size() - next >= static_cast<size_t>(nslots)) // the slot's last chunk
+        consume(pending[next++]);
+      HIPCHECK(hipMemcpyAsync(ctx.slots[static_cast<size_t>(slot)], result + off,
+                              static_cast<size_t>(bytes), hipMemcpyDeviceToHost, ctx.copy));
+      HIPCHECK(hipEventRecord(ctx.slot_ev[static_cast<size_t>(slot)], ctx.copy));
+      pending.push_back({slot, off, bytes});
+    }
+    ++chunks;
+   }
+  }
+  while (next < pending.size())
+    consume(pending[next++]);
+  HIPCHECK(hipEventRecord(ctx.done_ev, ctx.copy));
+  if (caller)
+    HIPCHECK(hipStreamWaitEvent(caller, ctx.done_ev, 0));
+  HIPCHECK(hipEventSynchronize(ctx.done_ev));
+  if (dp.family == kFamGeneric) {
+    int32_t flag = 0;
+    HIPCHECK(hipMemcpy(&flag, ctx.status, sizeof(flag), hipMemcpyDeviceToHost));
+    if (flag)
+      throw Error("channel_out_of_range", "a stage selected a channel outside its parameters");
+  }
+  if (report) {
+    relx_report &r = *report;
+    std::memset(&r, 0, sizeof(r));
+    std::snprintf(r.implementation, sizeof(r.implementation), "hip_relayout_d2h");
+    r.source_bytes = b.typed ? b.source_bytes : dp.wire_bytes;
+    r.wire_bytes = out_bytes;
+    r.destination_bytes = out_bytes;
+    r.parameter_bytes = b.parameter_bytes;
+    r.payload_bytes_transferred = out_bytes;
+    r.chunks = chunks;
+    r.kernel_launches = launches;
+    r.wire_boundary = static_cast<int>(h.prep.stages.size());
+    r.direct_dma = pinned ? 1 : 0;
+  }
+}
+
 // ----------------------------------------------------------- contexts
 
 std::unique_ptr<Context> make_context(int device, int64_t max_retained) {
@@ -563,6 +726,22 @@ int64_t verify_launches(BoundHandle &h, uint32_t k, int64_t chunk_bytes) {
       verify_launch(dp, a);
       ++n;
     }
+  if (k == 0) { // the device-to-host schedule
+    const D2hPlan d = d2h_plan(dp, chunk_bytes);
+    int64_t fixed[kMaxRank] = {};
+    for (int64_t o = 0; o < d.outer; ++o) {
+      int64_t rem = o;
+      for (int j = d.axis - 1; j >= 0; --j) {
+        fixed[j] = rem % dp.base.pext[j];
+        rem /= dp.base.pext[j];
+      }
+      for (int64_t u0 = 0; u0 < d.units; u0 += d.per)
+        for (const KArgs &a : prefix_launches(dp, fixed, d.axis, u0, std::min(d.units, u0 + d.per))) {
+          verify_launch(dp, a);
+          ++n;
+        }
+    }
+  }
   return n;
 }
 

@@ -15,6 +15,7 @@
 #include <thread>
 #include <vector>
 
+#include "../../include/relx.h"
 #include "plan.h"
 #include "program.h"
 
@@ -57,6 +58,17 @@ uint64_t host_apply(const HostStage &s, uint64_t x, int64_t c);
 std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, uint32_t k);
 std::vector<KArgs> box_launches(const DeviceProgram &dp, int64_t v0, int64_t v1, bool first,
                                 bool last);
+// Launches covering padded coordinates [plo, phi) of one destination axis
+// (the whole box when axis < 0).
+std::vector<KArgs> axis_launches(const DeviceProgram &dp, int axis, int64_t plo, int64_t phi);
+// Launches for one coordinate of each axis before `axis` (fixed[0..axis))
+// and padded coordinates [plo, phi) of `axis`.
+std::vector<KArgs> prefix_launches(const DeviceProgram &dp, const int64_t *fixed, int axis,
+                                   int64_t plo, int64_t phi);
+// Coordinates a box along axis i must keep together (0: never split).
+int64_t axis_align(const DeviceProgram &dp, int i);
+int64_t launch_all(const DeviceProgram &dp, std::vector<KArgs> launches, const void *src,
+                   void *dst, const float *pf, const int32_t *pi, int32_t *status, hipStream_t s);
 // Launch the program over valid chunk-axis coordinates [v0, v1) (the whole
 // box when it has no chunk axis); returns the number of kernel launches.
 int64_t launch_program(const DeviceProgram &dp, int64_t v0, int64_t v1, bool first, bool last,
@@ -120,6 +132,21 @@ struct BoundHandle {
   DevParams device_params(int device, uint32_t k);
   ~BoundHandle();
 };
+
+// Device-to-host chunk schedule: for each of the `outer` coordinate tuples of
+// the destination axes before `axis`, ranges of `per` coordinates of `axis`
+// (-1: one chunk), `row` bytes per coordinate; every chunk is one contiguous
+// range of the dense destination.
+struct D2hPlan {
+  int axis;
+  int64_t outer, units, per, row;
+};
+D2hPlan d2h_plan(const DeviceProgram &dp, int64_t chunk_bytes);
+
+struct Context;
+// Device-resident source -> host destination (see runtime.cpp).
+void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes, void *dst,
+                 size_t dst_bytes, const relx_options &opt, relx_report *report);
 
 // Leading per-tensor narrowing stages applied on the host for a pageable
 // source (halving PCIe bytes where a cast narrows).

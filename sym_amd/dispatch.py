@@ -10,11 +10,14 @@ boundary a host may reach with per-tensor stages:
     hip_relayout        the source bytes cross PCIe; every stage on the GPU
     hip_relayout@k      the host applies stages [0, k) while staging
 
+The device-to-host direction has one row, `hip_relayout`: the device runs
+the relayout and every stage and the result crosses PCIe (the reference's
+cuda_stages_then_cpu rows with every stage on the device).
+
 Names, argument meaning and error codes follow the reference so that
 `reloc_torch.dispatch` can call these functions in place of `_pyreloc`'s.
-Requests whose policy asks for a CPU executor ("original_cpu"), a forced
-row this build lacks, or the D2H direction raise
-TransferError("implementation_unavailable" / "direction_mismatch").
+Requests whose policy asks for a CPU executor ("original_cpu") or a forced
+row this build lacks raise TransferError("implementation_unavailable").
 """
 import threading
 
@@ -91,12 +94,15 @@ def query_capability(bound, direction, device):
         raise ValueError("direction must be 'h2d' or 'd2h', got '%s'" % direction)
     if not bound.typed:
         raise TransferError("typed_unsupported", "layout plans dispatch through execute_transfer")
-    if direction == "d2h":
-        return {"eligible": [], "excluded": [{"implementation": "hip_relayout",
-                                              "reason": "direction_unsupported"}]}
     if device == "host":
         return {"eligible": [], "excluded": [{"implementation": "hip_relayout",
                                               "reason": "host_destination"}]}
+    if direction == "d2h":
+        out = bound.destination_bytes
+        return {"eligible": [{"implementation": "hip_relayout", "wire_boundary": bound.stage_count,
+                              "wire_result_layout": True, "wire_bytes": out,
+                              "device_temp_bytes": out, "method": "device_relayout"}],
+                "excluded": []}
     rows = [_row(bound, k) for k in range(bound.info.host_stages_max + 1)]
     excluded = [{"implementation": _label(k), "reason": "per_channel_stage_on_host"}
                 for k in range(bound.info.host_stages_max + 1, bound.stage_count + 1)]
@@ -134,8 +140,6 @@ class DispatchRequest:
 def _select(bound, direction, capability, policy, implementation):
     if policy not in POLICIES:
         raise ValueError("policy must be 'auto' or 'original_cpu', got '%s'" % policy)
-    if direction != "h2d":
-        raise TransferError("direction_mismatch", "this build runs host-to-device dispatch only")
     if policy == "original_cpu":
         raise TransferError("implementation_unavailable",
                             "no CPU executor row: every plan runs on the device")
@@ -146,7 +150,10 @@ def _select(bound, direction, capability, policy, implementation):
                                 "row '%s' is not eligible (eligible: %s)" % (implementation,
                                                                            ", ".join(labels)))
         return {"implementation": implementation, "policy": policy, "placement_reason": "forced",
-                "host_stages": labels.index(implementation)}
+                "host_stages": labels.index(implementation) if direction == "h2d" else 0}
+    if direction == "d2h":
+        return {"implementation": "hip_relayout", "policy": policy,
+                "placement_reason": "device_relayout", "host_stages": 0}
     auto = bound.info.host_stages_auto
     return {"implementation": _label(auto), "policy": policy,
             "placement_reason": "device_relayout", "host_stages": -1}
@@ -165,10 +172,10 @@ def prepare_dispatch_template(bound, direction, device="cuda", *, policy="auto",
 
 def _check_views(bound, source, destination, direction):
     info = bound.info
-    if direction == "h2d" and (source.kind != "host" or destination.kind != "cuda"):
-        raise TransferError("direction_mismatch",
-                            "h2d moves a host source into a cuda destination, got %s -> %s"
-                            % (source.kind, destination.kind))
+    want = ("host", "cuda") if direction == "h2d" else ("cuda", "host")
+    if (source.kind, destination.kind) != want:
+        raise TransferError("direction_mismatch", "%s moves %s -> %s, got %s -> %s"
+                            % (direction, want[0], want[1], source.kind, destination.kind))
     for name, view, extents, width in (
             ("source", source, list(info.source_extents[:info.source_rank]), info.source_width),
             ("destination", destination, list(info.result_extents[:info.result_rank]),
@@ -256,14 +263,17 @@ def execute_dispatch(request, *, caller_stream=None, n_buffers=2, n_streams=2, g
         if gather_threads < 0:
             raise ValueError("gather_threads must be >= 0 (0 = all cores)")
         request.executing = True
-        ctx = resources if resources is not None else _resources_for(max(0, request.destination.device))
         src, dst = request.source, request.destination
-        rep = ctx.execute_h2d(request.template.bound, src.address, src.capacity_bytes - src.offset_bytes,
-                              dst.address, dst.capacity_bytes - dst.offset_bytes,
-                              n_buffers=n_buffers, chunk_bytes=int(chunk_size or 0),
-                              host_stages=request.selected["host_stages"],
-                              gather_threads=gather_threads, source_pinned=_pinning(pinning),
-                              caller_stream=int(caller_stream or 0))
+        d2h = request.template.direction == "d2h"
+        device = src.device if d2h else dst.device
+        ctx = resources if resources is not None else _resources_for(max(0, device))
+        run = ctx.execute_d2h if d2h else ctx.execute_h2d
+        rep = run(request.template.bound, src.address, src.capacity_bytes - src.offset_bytes,
+                  dst.address, dst.capacity_bytes - dst.offset_bytes,
+                  n_buffers=n_buffers, chunk_bytes=int(chunk_size or 0),
+                  host_stages=request.selected["host_stages"],
+                  gather_threads=gather_threads, source_pinned=_pinning(pinning),
+                  caller_stream=int(caller_stream or 0))
         request.consumed = True
         request.report = _report(rep, request)
         return dict(request.report)
@@ -288,6 +298,8 @@ def prepare_dispatch_group(entries):
     direction) tuples (reference prepare_dispatch_group)."""
     items = []
     for plan, source, destination, direction in entries:
+        if direction != "h2d":
+            raise TransferError("direction_mismatch", "groups move host-to-device members")
         t = plan if isinstance(plan, DispatchTemplate) else prepare_dispatch_template(plan, direction)
         items.append(prepare_dispatch_from_template(t, source, destination))
     if not items:

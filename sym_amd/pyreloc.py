@@ -250,6 +250,18 @@ class Context:
             _raise(err)
         return [r.as_dict() for r in reps], total.as_dict()
 
+    def execute_d2h(self, bound, src_ptr, src_nbytes, dst_ptr, dst_nbytes, **options):
+        """Run one bound plan device -> host (every stage on the device);
+        `source_pinned` describes the host destination here."""
+        rep = N.relx_report()
+        err = N.relx_err()
+        options.setdefault("host_stages", 0)
+        opt = _options(**options)
+        if N.lib().relx_execute_d2h(self._h, bound._h, src_ptr, src_nbytes, dst_ptr, dst_nbytes,
+                                    ctypes.byref(opt), ctypes.byref(rep), ctypes.byref(err)):
+            _raise(err)
+        return rep.as_dict()
+
     def relayout_device(self, bound, wire_ptr, dst_ptr, wire_boundary=0, stream=0):
         """Launch the device relayout on a device-resident wire (async)."""
         err = N.relx_err()

@@ -45,7 +45,9 @@ def test_capability_rows_per_boundary():
     assert [r["implementation"] for r in cap["eligible"]] == ["hip_relayout", "hip_relayout@1"]
     n = 2 * 3 * 224 * 224  # the source layout's elements, f32 then f16
     assert [r["wire_bytes"] for r in cap["eligible"]] == [4 * n, 2 * n]
-    assert P.query_capability(b, "d2h", "cuda")["eligible"] == []
+    d2h = P.query_capability(b, "d2h", "cuda")["eligible"]
+    assert [r["implementation"] for r in d2h] == ["hip_relayout"]
+    assert d2h[0]["wire_bytes"] == b.destination_bytes and d2h[0]["wire_result_layout"]
     assert P.query_capability(b, "h2d", "host")["eligible"] == []
     c3 = P.Bound(P.Plan(W.c3_plan().blob), {"s0": 64, "s1": 128},
                  W.param("scale", np.ones(128, np.float32)))
@@ -80,9 +82,8 @@ def test_selection_and_forced_rows():
     with pytest.raises(P.TransferError) as e:
         P.prepare_dispatch_template(b, "h2d", "cuda", policy="original_cpu")
     assert e.value.code == "implementation_unavailable"
-    with pytest.raises(P.TransferError) as e:
-        P.prepare_dispatch_template(b, "d2h", "cuda")
-    assert e.value.code == "direction_mismatch"
+    t = P.prepare_dispatch_template(b, "d2h", "cuda")
+    assert t.selection["implementation"] == "hip_relayout" and t.selection["host_stages"] == 0
     with pytest.raises(ValueError):
         P.prepare_dispatch_template(b, "h2d", "cuda", policy="fastest")
     with pytest.raises(ValueError):
@@ -109,6 +110,13 @@ def test_view_validation_codes():
         "insufficient_capacity"
     host_dst = host_view(np.zeros((2, 224, 224, 4), np.float16))
     assert code(host_view(src), host_dst) == "direction_mismatch"
+    # device-to-host: a cuda source into a host destination
+    dev_src = fake_device_view([2, 3, 224, 224], 4)
+    req = P.prepare_dispatch(b, dev_src, host_dst, "d2h")
+    assert req.template.direction == "d2h"
+    with pytest.raises(P.TransferError) as e:
+        P.prepare_dispatch(b, host_view(src), host_dst, "d2h")
+    assert e.value.code == "direction_mismatch"
 
 
 def test_group_preparation():

@@ -117,3 +117,73 @@ def test_group_dispatch_c4_like(resources, rng):
         assert out.cpu().numpy().tobytes() == want
     with pytest.raises(P.TransferError):
         P.execute_dispatch_group(g, resources=resources)
+
+
+# ------------------------------------------------------------- D2H
+
+def test_corpus_device_to_host(resources):
+    for meta, blob in TYPED:
+        plan = P.load_typed_plan(blob)
+        for binding in meta["bindings"]:
+            src = np.ascontiguousarray(G.bits_array(binding["source"]).reshape(binding["source"]["shape"]))
+            exp = G.bits_array(binding["expected"]).reshape(binding["expected"]["shape"])
+            b = P.bind_typed(plan, binding["symbols"], G.fixture_params(meta))
+            src_t = torch.from_numpy(src.view(np.uint8).copy()).cuda()
+            dsrc = P.BufferView(src_t.data_ptr(), src.nbytes, 0, list(src.shape),
+                                [s // src.itemsize for s in src.strides], src.itemsize, "cuda", 0)
+            out = np.full(exp.shape, 0xCD, dtype=np.uint8).view(exp.dtype) if exp.itemsize == 1 \
+                else np.zeros(exp.shape, exp.dtype)
+            say(meta["name"], binding["symbols"], "d2h")
+            req = P.prepare_dispatch(b, dsrc, host_view(out), "d2h")
+            rep = P.execute_dispatch(req, resources=resources)
+            assert np.array_equal(out, exp), meta["name"]
+            fp = binding["footprints"]["d2h"]
+            for key in ("source_bytes", "destination_bytes", "parameter_bytes"):
+                assert rep[key] == fp[key], (meta["name"], key)
+            assert rep["implementation"] == "hip_relayout_d2h" and rep["executed"]
+
+
+def _c5_expected(x, s):
+    x32 = O.widen_f16_f32_bits(x.view(np.uint16)).view(np.float32)      # [B,S,32,128]
+    q = O.quantize_f32_s8(x32, (np.float32(1.0) / s.astype(np.float32))[None, None, :, None])
+    return np.ascontiguousarray(np.transpose(q, (0, 2, 1, 3)))             # [B,32,S,128]
+
+
+@pytest.mark.parametrize("pinned", [False, True])
+@pytest.mark.parametrize("chunk", [0, 64 << 10])
+def test_c5_kv_evict_device_to_host(resources, pinned, chunk):
+    """C5's quantizing permute in the other direction (KV eviction): a device
+    f16 [B,S,32,128] tensor to a host int8 [B,32,S,128] buffer, chunked
+    (ring reuse with two slots at 64 KiB) into pageable or pinned memory."""
+    B, S = 2, 1024
+    x, s = W.c5_input(B, S, seed=77)
+    b = P.Bound(P.Plan(W.c5_plan().blob), {"B": B, "S": S}, W.param("scale", s))
+    xs = torch.from_numpy(x.view(np.uint16).view(np.int16).copy()).cuda()
+    if pinned:
+        out_t = torch.empty(B * 32 * S * 128, dtype=torch.int8).pin_memory()
+        out = out_t.numpy()
+    else:
+        out = np.empty(B * 32 * S * 128, np.int8)
+    say("c5 d2h", B, S, "pinned" if pinned else "pageable", "chunk", chunk)
+    rep = resources.execute_d2h(b, xs.data_ptr(), x.nbytes, out.ctypes.data, out.nbytes,
+                                chunk_bytes=chunk, n_buffers=2, source_pinned=1 if pinned else 0)
+    assert rep["direct_dma"] == (1 if pinned else 0)
+    if chunk:
+        assert rep["chunks"] > 4
+    assert np.array_equal(out.reshape(B, 32, S, 128), _c5_expected(x, s))
+
+
+def test_c3_device_to_host_matches_h2d(resources, rng):
+    """The same bound plan in both directions gives the same bytes."""
+    rows, cols = 256, 512
+    q, s = W.int8_weight(rows, cols, rng), W.scales(cols, rng)
+    b = P.Bound(P.Plan(W.c3_plan().blob), {"s0": rows, "s1": cols}, W.param("scale", s))
+    dev = torch.empty(rows * cols * 2, dtype=torch.uint8, device="cuda")
+    say("c3 h2d then d2h")
+    resources.execute_h2d(b, q.ctypes.data, q.nbytes, dev.data_ptr(), dev.numel())
+    torch.cuda.synchronize()
+    via_h2d = dev.cpu().numpy()
+    qd = torch.from_numpy(q.view(np.uint8).copy()).cuda()
+    out = np.empty(rows * cols * 2, np.uint8)
+    resources.execute_d2h(b, qd.data_ptr(), q.nbytes, out.ctypes.data, out.nbytes, chunk_bytes=16 << 10)
+    assert np.array_equal(out, via_h2d)
