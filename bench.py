@@ -317,6 +317,35 @@ def one_config(torch, ctx, P, name, args, h2d_ceiling):
                            "implementation": prep["implementation"], "chunks": prep["chunks"]}}
 
 
+def d2h_config(torch, ctx, name, args, d2h_ceiling):
+    """The device-to-host direction (KV eviction): the config's source is
+    resident on the device, the result lands in host memory (pageable or
+    pinned); wire bytes are the result's."""
+    case = make_case(name)
+    src = torch.from_numpy(case.src.view(np.uint8).reshape(-1)).cuda()
+    out = {}
+    for pinned in (False, True):
+        dst = torch.empty(case.out_bytes, dtype=torch.uint8)
+        if pinned:
+            dst = dst.pin_memory()
+        for _ in range(3):
+            ctx.execute_d2h(case.bound, src.data_ptr(), src.numel(), dst.data_ptr(), case.out_bytes,
+                            source_pinned=1 if pinned else 0)
+        ts = []
+        for _ in range(max(10, args.e2e_samples // 2)):
+            t = time.perf_counter()
+            rep = ctx.execute_d2h(case.bound, src.data_ptr(), src.numel(), dst.data_ptr(),
+                                  case.out_bytes, source_pinned=1 if pinned else 0)
+            ts.append(time.perf_counter() - t)
+        p50 = float(np.percentile(ts, 50))
+        out["pinned" if pinned else "pageable"] = {
+            "p50_ms": round(p50 * 1e3, 3), "effective_GBps": round(case.out_bytes / p50 / 1e9, 2),
+            "pcie_frac": round(case.out_bytes / p50 / 1e9 / d2h_ceiling, 4), "chunks": rep["chunks"]}
+    del src
+    return {"config": name + "_d2h", "workload": case.workload + " (device -> host)",
+            "kernel": case.kernel, "pinned_d2h_ceiling_GBps": round(d2h_ceiling, 2), **out}
+
+
 def c4_report(torch, ctx, P, args, h2d_ceiling):
     """C4: two experts (6 matrices) per step as one grouped transfer."""
     from sym_amd import workloads as W
@@ -416,6 +445,10 @@ def main():
                 from sym_amd import workloads as W
                 for b, s in W.C5_SHAPES:
                     print(json.dumps(one_config(torch, ctx, P, "c5_%dx%d" % (b, s), args, h2d_ceiling)),
+                          flush=True)
+                d2h_ceiling = P.measure_d2h(0, 256 << 20, 20, 3)
+                for b, s in ((8, 1024), (8, 4096), (64, 1024)):
+                    print(json.dumps(d2h_config(torch, ctx, "c5_%dx%d" % (b, s), args, d2h_ceiling)),
                           flush=True)
             else:
                 print(json.dumps(one_config(torch, ctx, P, name, args, h2d_ceiling)), flush=True)

@@ -258,6 +258,10 @@ int relx_host_free(void *p);
  * a warmup, best of `rounds` (restates bench/rtrack/multigpu_h2d.cu:46-91). */
 double relx_measure_h2d(int device, size_t bytes, int iters, int rounds);
 
+/* The same measurement device -> host into pinned memory: the ceiling the
+ * D2H direction of relx_execute_d2h is reported against. */
+double relx_measure_d2h(int device, size_t bytes, int iters, int rounds);
+
 #ifdef __cplusplus
 }
 #endif

@@ -105,6 +105,7 @@ SIGNATURES = {
     "relx_host_alloc": (_I, [_SZ, ctypes.POINTER(_VP), _E]),
     "relx_host_free": (_I, [_VP]),
     "relx_measure_h2d": (ctypes.c_double, [_I, _SZ, _I, _I]),
+    "relx_measure_d2h": (ctypes.c_double, [_I, _SZ, _I, _I]),
 }
 
 _lib = None

@@ -18,6 +18,7 @@ void destroy_context(Context &ctx);
 void relayout_device(Context &ctx, BoundHandle &h, uint32_t k, const void *wire, void *dst,
                      hipStream_t stream);
 double measure_h2d(int device, size_t bytes, int iters, int rounds);
+double measure_copy(int device, size_t bytes, int iters, int rounds, bool d2h);
 } // namespace relx
 
 struct relx_plan {
@@ -418,6 +419,14 @@ int relx_host_free(void *p) { return hipHostFree(p) == hipSuccess ? RELX_OK : RE
 double relx_measure_h2d(int device, size_t bytes, int iters, int rounds) {
   try {
     return relx::measure_h2d(device, bytes, iters, rounds);
+  } catch (...) {
+    return -1.0;
+  }
+}
+
+double relx_measure_d2h(int device, size_t bytes, int iters, int rounds) {
+  try {
+    return relx::measure_copy(device, bytes, iters, rounds, true);
   } catch (...) {
     return -1.0;
   }

@@ -754,7 +754,13 @@ void relayout_device(Context &ctx, BoundHandle &h, uint32_t k, const void *wire,
                  stream ? stream : ctx.compute);
 }
 
+double measure_copy(int device, size_t bytes, int iters, int rounds, bool d2h);
+
 double measure_h2d(int device, size_t bytes, int iters, int rounds) {
+  return measure_copy(device, bytes, iters, rounds, false);
+}
+
+double measure_copy(int device, size_t bytes, int iters, int rounds, bool d2h) {
   DeviceGuard guard(device);
   void *h = nullptr, *d = nullptr;
   hipStream_t s;
@@ -765,14 +771,18 @@ double measure_h2d(int device, size_t bytes, int iters, int rounds) {
   HIPCHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
   HIPCHECK(hipEventCreate(&e0));
   HIPCHECK(hipEventCreate(&e1));
+  auto copy = [&] {
+    return d2h ? hipMemcpyAsync(h, d, bytes, hipMemcpyDeviceToHost, s)
+               : hipMemcpyAsync(d, h, bytes, hipMemcpyHostToDevice, s);
+  };
   for (int i = 0; i < 3; ++i)
-    HIPCHECK(hipMemcpyAsync(d, h, bytes, hipMemcpyHostToDevice, s));
+    HIPCHECK(copy());
   HIPCHECK(hipStreamSynchronize(s));
   double best = 0.0;
   for (int r = 0; r < rounds; ++r) {
     HIPCHECK(hipEventRecord(e0, s));
     for (int i = 0; i < iters; ++i)
-      HIPCHECK(hipMemcpyAsync(d, h, bytes, hipMemcpyHostToDevice, s));
+      HIPCHECK(copy());
     HIPCHECK(hipEventRecord(e1, s));
     HIPCHECK(hipEventSynchronize(e1));
     float ms = 0.0f;

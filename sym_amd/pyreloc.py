@@ -325,6 +325,11 @@ def measure_h2d(device=0, nbytes=256 << 20, iters=20, rounds=3):
     return N.lib().relx_measure_h2d(int(device), int(nbytes), int(iters), int(rounds))
 
 
+def measure_d2h(device=0, nbytes=256 << 20, iters=20, rounds=3):
+    """Pinned D2H ceiling in GB/s (the same measurement, device to host)."""
+    return N.lib().relx_measure_d2h(int(device), int(nbytes), int(iters), int(rounds))
+
+
 # The typed dispatch API (prepare_dispatch / execute_dispatch / groups) lives
 # in sym_amd.dispatch and is re-exported here under pyreloc's names.
 from .dispatch import (BufferView, DispatchRequest, DispatchTemplate,  # noqa: E402,F401
