@@ -655,6 +655,82 @@ __global__ __launch_bounds__(kBlock) void k_interleave(KArgs a) {
   }
 }
 
+// ------------------------------------------------------------- permute
+
+// Destination axes [batch..., c, m, e] from a source holding (m, c, e)
+// contiguously. A block takes T consecutive m (one contiguous T*C*E source
+// run), applies the stages on the way into LDS, which it fills in
+// destination order [c][t][e], then writes C contiguous runs of T*E
+// elements. Reads are whole source rows, writes whole destination runs.
+template <int WIN, int WOUT, int CH>
+__global__ __launch_bounds__(kBlock) void k_permute(KArgs a) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  constexpr int VI = 16 / WIN, BO = VI * WOUT;
+  constexpr int U = 4; // source vectors in flight per thread
+  const uint32_t t = blockIdx.x;
+  if (t >= a.work)
+    return;
+  const uint32_t batch = fdiv(t, a.p_tiles);
+  const uint32_t m0 = (t - batch * a.p_tiles.d) * a.p_t;
+  int64_t sbase = a.sbase, dbase = a.dbase;
+  decompose<kBatchLevels>(a.lv, batch, sbase, dbase); // permutes carry no pads
+  const uint32_t CE = a.p_ce.d, E = a.p_e.d;
+  const uint8_t *src = a.src + (sbase + static_cast<int64_t>(m0) * CE) * WIN;
+  const uint32_t nvec = a.p_t * CE / VI;
+  for (uint32_t v0 = threadIdx.x; v0 < nvec; v0 += kBlock * U) {
+    vec4 in[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t v = v0 + u * kBlock;
+      if (v < nvec)
+        in[u] = ld16<true>(reinterpret_cast<const vec4 *>(src) + v);
+    }
+    // one body per vector with a compile-time index, so `in` stays in
+    // registers whatever the chain's size
+    auto emit = [&](auto uc) {
+      constexpr int u = decltype(uc)::value;
+      const uint32_t v = v0 + u * kBlock;
+      if (v >= nvec)
+        return;
+      const uint32_t off = v * VI; // element offset in the block's source run
+      const uint32_t tt = fdiv(off, a.p_ce);
+      const uint32_t rem = off - tt * CE;
+      const uint32_t c = fdiv(rem, a.p_e);
+      const uint32_t e = rem - c * E;
+      uint32_t x[VI];
+      unpack<WIN, VI>(&in[u], x);
+      chain_vec<CH, VI>(a, x, dbase + c * a.p_dsc + static_cast<int64_t>(m0 + tt) * E + e);
+      vec4 o[(BO + 15) / 16];
+      o[0] = vec4{0u, 0u, 0u, 0u};
+      pack<WOUT, VI>(x, o);
+      uint8_t *dstl = lds + ((c * a.p_t + tt) * E + e) * WOUT;
+      if constexpr (BO >= 16) {
+#pragma unroll
+        for (int j = 0; j < BO / 16; ++j)
+          reinterpret_cast<vec4 *>(dstl)[j] = o[j];
+      } else if constexpr (BO == 8) {
+        *reinterpret_cast<vec2 *>(dstl) = vec2{o[0].x, o[0].y};
+      } else {
+        *reinterpret_cast<uint32_t *>(dstl) = o[0].x;
+      }
+    };
+    static_assert(U == 4, "four vectors in flight");
+    emit(std::integral_constant<int, 0>{});
+    emit(std::integral_constant<int, 1>{});
+    emit(std::integral_constant<int, 2>{});
+    emit(std::integral_constant<int, 3>{});
+  }
+  __syncthreads();
+  const uint32_t nout = a.p_lds / 16, run = a.p_run.d;
+  uint8_t *dst = a.dst + (dbase + static_cast<int64_t>(m0) * E) * WOUT;
+  for (uint32_t w = threadIdx.x; w < nout; w += kBlock) {
+    const uint32_t c = fdiv(w, a.p_run);
+    const uint32_t j = w - c * run;
+    const vec4 val = reinterpret_cast<const vec4 *>(lds)[w];
+    st16<true>(reinterpret_cast<vec4 *>(dst + c * a.p_dsc * WOUT) + j, val);
+  }
+}
+
 // ------------------------------------------------------------ launch
 
 // One work item per thread up to 2^22 blocks (2^30 work-items per launch,
@@ -705,6 +781,13 @@ hipError_t interleave_cp(const KArgs &a, hipStream_t s) {
   } else {
     return hipErrorInvalidValue;
   }
+}
+
+template <int WIN, int WOUT, int CH>
+hipError_t permute_launch(const KArgs &a, hipStream_t s) {
+  hipLaunchKernelGGL((k_permute<WIN, WOUT, CH>), dim3(static_cast<unsigned>(a.work)),
+                     dim3(kBlock), a.p_lds, s, a);
+  return hipGetLastError();
 }
 
 template <int WIN, int WOUT, int CH>
@@ -802,5 +885,7 @@ hipError_t transpose_fast(const KArgs &a, hipStream_t s, bool &handled);
 hipError_t transpose_generic(const KArgs &a, hipStream_t s);
 hipError_t interleave_fast(const KArgs &a, hipStream_t s, bool &handled);
 hipError_t interleave_generic(const KArgs &a, hipStream_t s);
+hipError_t permute_fast(const KArgs &a, hipStream_t s, bool &handled);
+hipError_t permute_generic(const KArgs &a, hipStream_t s);
 
 } // namespace relx

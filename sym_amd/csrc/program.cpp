@@ -400,7 +400,36 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
     }
     return true;
   };
-  if (widths_ok && dense && !needs_expr) {
+  if (widths_ok && dense && !needs_expr && !any_pad && r >= 3 && r - 3 <= kBatchLevels) {
+    // permute: destination [batch..., c, m, e] from a source holding
+    // (m, c, e) contiguously -- two axes swapped above a contiguous inner
+    // block (an activation's [B,S,H,D] -> [B,H,S,D])
+    const int c = r - 3, m = r - 2, e = r - 1;
+    const int64_t E = a.vext[e], C = a.vext[c], M = a.vext[m];
+    const int VI = 16 / win;
+    bool ok = a.ss[e] == 1 && a.ds[e] == 1 && a.ss[c] == E && a.ss[m] == C * E &&
+              a.ds[m] == E && a.ds[c] == M * E && E % VI == 0 && (E * wout) % 16 == 0 &&
+              C > 1 && M > 1;
+    for (int i = 0; i < c; ++i)
+      ok = ok && a.ss[i] % VI == 0;
+    // T rows of m per block: about 16 KiB of source, an LDS tile of at most
+    // 32 KiB, T dividing M
+    int64_t T = 0;
+    if (ok) {
+      T = 1;
+      while (T * 2 <= M && M % (T * 2) == 0 && T * 2 * C * E * win <= 16384 &&
+             T * 2 * C * E * wout <= 32768)
+        T *= 2;
+      ok = T * C * E * wout <= 32768;
+    }
+    if (ok && channels_ok(VI)) {
+      family = kFamPermute;
+      a.vec = VI;
+      a.p_t = static_cast<uint32_t>(T);
+      a.p_lds = static_cast<uint32_t>(T * C * E * wout);
+    }
+  }
+  if (family == kFamGeneric && widths_ok && dense && !needs_expr) {
     // stream: innermost axis contiguous on both sides, unpadded
     if (a.ss[r - 1] == 1 && a.ds[r - 1] == 1 && !inner_pad && a.vext[r - 1] % V == 0) {
       bool ok = true;
@@ -485,7 +514,7 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
       code = kChainQuant;
     a.chain_code = code;
   }
-  static const char *names[] = {"generic", "stream", "transpose", "interleave"};
+  static const char *names[] = {"generic", "stream", "transpose", "interleave", "permute"};
   dp->kernel = names[family];
 
   // ------------------------------------------------------- chunk axis
@@ -514,6 +543,13 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
         // boxes never split the channel axis
         if (family == kFamInterleave && ax == r - 1)
           dp->chunk_axis = -1;
+        // a permute block takes T rows of m and all of c and e
+        if (family == kFamPermute) {
+          if (ax == r - 2)
+            dp->chunk_align = a.p_t;
+          else if (ax >= r - 3)
+            dp->chunk_axis = -1;
+        }
       }
     }
   }
@@ -541,6 +577,10 @@ int64_t box_work(const DeviceProgram &dp, const Box &b) {
       e /= a.vec;
     else if (dp.family == kFamInterleave && i == r - 1)
       e = 1;
+    else if (dp.family == kFamPermute && i == r - 2)
+      e /= a.p_t;
+    else if (dp.family == kFamPermute && i > r - 4)
+      e = 1;
     n *= e;
   }
   return n;
@@ -557,6 +597,10 @@ int64_t split_align(const DeviceProgram &dp, int i) {
     return dp.base.vec;
   if (dp.family == kFamInterleave && i == r - 1)
     return 0;
+  if (dp.family == kFamPermute && i == r - 2)
+    return dp.base.p_t;
+  if (dp.family == kFamPermute && i > r - 4)
+    return 0;
   return 1;
 }
 
@@ -568,6 +612,8 @@ bool level_axis(const DeviceProgram &dp, int i) {
     return i != dp.qa && i != dp.ca;
   if (dp.family == kFamInterleave)
     return i < r - 2;
+  if (dp.family == kFamPermute)
+    return i < r - 3;
   return true;
 }
 
@@ -704,6 +750,20 @@ KArgs launch_args(const DeviceProgram &dp, const Box &b) {
     a.t_ssc = a.ss[dp.ca];
     a.t_dsq = a.ds[dp.qa];
     break;
+  case kFamPermute: {
+    int idx[kMaxRank], n = 0;
+    for (int i = 0; i < r - 3; ++i)
+      idx[n++] = i;
+    for (int j = 0; j < n; ++j)
+      a.lv[kBatchLevels - n + j] = axis_level(a, b, idx[j], 1);
+    const int64_t E = a.vext[r - 1], C = a.vext[r - 3], M = a.vext[r - 2], T = a.p_t;
+    a.p_tiles = make_div(b.ext[r - 2] / T);
+    a.p_ce = make_div(C * E);
+    a.p_e = make_div(E);
+    a.p_run = make_div(T * E * a.wout / 16);
+    a.p_dsc = M * E;
+    break;
+  }
   case kFamInterleave:
     batch(r - 2, r - 1);
     a.i_ng = make_div(b.ext[r - 2] / a.vec);
@@ -926,6 +986,34 @@ void verify_launch(const DeviceProgram &dp, const KArgs &a) {
         const int32_t vc = c - a.i_loc;
         if (!pad && static_cast<uint32_t>(vc) < static_cast<uint32_t>(a.i_vc))
           ck.src_run(sbase + vc * a.i_ssc + p0, G, true);
+      }
+    }
+    break;
+  }
+  case kFamPermute: {
+    if (a.work64 > (int64_t{1} << 22) || a.work != a.work64)
+      bad_launch(dp, "more blocks than one launch takes");
+    const int64_t CE = a.p_ce.d, E = a.p_e.d, T = a.p_t, C = CE / E;
+    const int VI = 16 / win;
+    if (a.p_lds != T * CE * wout || a.p_lds > 32768 || int64_t{a.p_run.d} * 16 != T * E * wout ||
+        a.vec != VI || CE % VI != 0 || (E * wout) % 16 != 0)
+      bad_launch(dp, "block geometry disagrees with the kernel");
+    for (uint32_t t = 0; t < a.work; ++t) {
+      const uint32_t batch = fdiv(t, a.p_tiles);
+      const int64_t m0 = int64_t{t - batch * a.p_tiles.d} * T;
+      int64_t sbase = a.sbase, dbase = a.dbase;
+      if (decompose_rt(kBatchLevels, a.lv, batch, sbase, dbase))
+        bad_launch(dp, "a permute block reaches a pad");
+      ck.src_run(sbase + m0 * CE, T * CE, false);
+      if (((sbase + m0 * CE) * win) % 16 != 0)
+        bad_launch(dp, "unaligned source rows");
+      for (int64_t c = 0; c < C; ++c) {
+        ck.dst_run(dbase + c * a.p_dsc + m0 * E, T * E, false);
+        if (((dbase + c * a.p_dsc + m0 * E) * wout) % 16 != 0)
+          bad_launch(dp, "unaligned destination runs");
+        for (int64_t tt = 0; tt < T; ++tt)
+          for (int64_t e = 0; e < E; e += VI)
+            ck.channels(dbase + c * a.p_dsc + (m0 + tt) * E + e, VI);
       }
     }
     break;

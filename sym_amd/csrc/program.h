@@ -92,6 +92,7 @@ enum Family : int32_t {
   kFamStream = 1,     // innermost axis contiguous on both sides
   kFamTranspose = 2,  // batched 2-D transpose, LDS tiled
   kFamInterleave = 3, // planar -> interleaved with a small padded inner axis
+  kFamPermute = 4,    // swap of two axes above a contiguous inner block, through LDS
 };
 
 // Pixels per interleave work item: the packed output of an item fills one
@@ -162,6 +163,13 @@ struct KArgs {
   FastDiv i_ng;
   int64_t i_ssc;        // plane stride (source stride of c)
   int32_t i_loc, i_vc;  // leading pad and valid extent of c
+  // permute: destination axes [batch..., c, m, e]; the source holds (m, c, e)
+  // contiguously (rows of C*E per m). A block takes T consecutive m.
+  FastDiv p_tiles;      // m-tiles in the box
+  FastDiv p_ce, p_e;    // C*E and E (source row and inner extents)
+  FastDiv p_run;        // 16-byte output vectors per (c, tile) run: T*E*wout/16
+  uint32_t p_t, p_lds;  // T, LDS bytes per block (T*C*E*wout)
+  int64_t p_dsc;        // destination stride of c (M*E)
   Chain chain;
   // ---- generic kernel and host bookkeeping (coalesced destination axes)
   int32_t rank;

@@ -476,7 +476,7 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
 D2hPlan d2h_plan(const DeviceProgram &dp, int64_t chunk_bytes) {
   const KArgs &a = dp.base;
   const int64_t out_bytes = dp.dst_elems * a.wout;
-  D2hPlan p{-1, 1, 1, 1, out_bytes};
+  D2hPlan p{-1, 1, 1, 1, out_bytes, out_bytes};
   bool dense = true;
   int64_t run = 1;
   for (int k = a.rank - 1; k >= 0; --k) {
@@ -486,6 +486,7 @@ D2hPlan d2h_plan(const DeviceProgram &dp, int64_t chunk_bytes) {
   if (!dense || run != dp.dst_elems || a.rank < 1)
     return p;
   const int64_t want = chunk_bytes > 0 ? chunk_bytes : kDefaultChunkBytes;
+  p.copy_bytes = std::min(out_bytes, want);
   // the outermost axis one coordinate of which fits a chunk; the axes before
   // it must accept single-coordinate boxes
   int64_t outer = 1;
@@ -539,11 +540,13 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
 
   const D2hPlan plan = d2h_plan(dp, opt.chunk_bytes);
   const int axis = plan.axis;
-  const int64_t units = plan.units, row = plan.row, per = plan.per;
+  // without a chunk axis the kernel runs once and only the copies are chunked
+  const int64_t units = axis < 0 ? (out_bytes + plan.copy_bytes - 1) / plan.copy_bytes : plan.units;
+  const int64_t row = axis < 0 ? plan.copy_bytes : plan.row, per = axis < 0 ? 1 : plan.per;
   const KArgs &a = dp.base;
   const int nslots = opt.n_buffers > 0 ? opt.n_buffers : 3;
   if (!pinned)
-    ensure_ring(ctx, nslots, static_cast<size_t>(per * row));
+    ensure_ring(ctx, nslots, static_cast<size_t>(std::min(per * row, out_bytes)));
   const unsigned threads = opt.gather_threads > 0 ? static_cast<unsigned>(opt.gather_threads) : 8u;
   if (!ctx.workers || ctx.worker_threads != threads) {
     ctx.workers = std::make_unique<Workers>(threads);
@@ -584,13 +587,16 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
    }
    for (int64_t u0 = 0; u0 < units; u0 += per) {
     const int64_t u1 = std::min(units, u0 + per);
-    launches += launch_all(dp, prefix_launches(dp, fixed, axis, u0, u1), src, result, par.pf,
-                           par.pi, ctx.status, ctx.compute);
-    hipEvent_t ke = ctx.chunk_ev[static_cast<size_t>(ev)];
-    ev = (ev + 1) % kChunkEvents;
-    HIPCHECK(hipEventRecord(ke, ctx.compute));
-    HIPCHECK(hipStreamWaitEvent(ctx.copy, ke, 0));
-    const int64_t off = (o * units + u0) * row, bytes = (u1 - u0) * row;
+    if (axis >= 0 || u0 == 0) {
+      launches += launch_all(dp, prefix_launches(dp, fixed, axis, u0, u1), src, result, par.pf,
+                             par.pi, ctx.status, ctx.compute);
+      hipEvent_t ke = ctx.chunk_ev[static_cast<size_t>(ev)];
+      ev = (ev + 1) % kChunkEvents;
+      HIPCHECK(hipEventRecord(ke, ctx.compute));
+      HIPCHECK(hipStreamWaitEvent(ctx.copy, ke, 0));
+    }
+    const int64_t off = (o * units + u0) * row;
+    const int64_t bytes = std::min((u1 - u0) * row, out_bytes - off);
     if (pinned) {
       HIPCHECK(hipMemcpyAsync(out + off, result + off, static_cast<size_t>(bytes),
                               hipMemcpyDeviceToHost, ctx.copy));
@@ -726,7 +732,7 @@ int64_t verify_launches(BoundHandle &h, uint32_t k, int64_t chunk_bytes) {
       verify_launch(dp, a);
       ++n;
     }
-  if (k == 0) { // the device-to-host schedule
+  if (k == 0) { // the device-to-host schedule (axis < 0: one whole launch)
     const D2hPlan d = d2h_plan(dp, chunk_bytes);
     int64_t fixed[kMaxRank] = {};
     for (int64_t o = 0; o < d.outer; ++o) {

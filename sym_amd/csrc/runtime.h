@@ -140,6 +140,8 @@ struct BoundHandle {
 struct D2hPlan {
   int axis;
   int64_t outer, units, per, row;
+  // axis < 0: one kernel launch, then copies of `copy_bytes` each
+  int64_t copy_bytes;
 };
 D2hPlan d2h_plan(const DeviceProgram &dp, int64_t chunk_bytes);
 

@@ -169,7 +169,7 @@ def test_c5_kv_evict_device_to_host(resources, pinned, chunk):
                                 chunk_bytes=chunk, n_buffers=2, source_pinned=1 if pinned else 0)
     assert rep["direct_dma"] == (1 if pinned else 0)
     if chunk:
-        assert rep["chunks"] > 4
+        assert rep["chunks"] > 4  # byte-chunked copies after one permute launch
     assert np.array_equal(out.reshape(B, 32, S, 128), _c5_expected(x, s))
 
 
