@@ -205,6 +205,37 @@ int relx_execute_group_h2d(relx_ctx *ctx, int n, const relx_bound *const *bounds
                            const size_t *dst_bytes, const relx_options *opt,
                            relx_report *reports, relx_report *total, relx_err *err);
 
+/* ------------------------------------------------------- asynchronous */
+
+typedef struct relx_completion relx_completion;
+
+/* Enqueue a group like relx_execute_group_h2d and return without waiting:
+ * `*out` is the group's completion (Resources::submit,
+ * libreloc/src/DispatchResources.cpp:688-747; pyreloc.submit_dispatch_group,
+ * libreloc/python/PyDispatch.cpp:696-707). Staging of pageable sources runs
+ * during this call (the pinned ring is host-driven); pinned sources move by
+ * DMA entirely after it returns. Sources and destinations must stay alive
+ * until the completion has been waited for or freed. */
+int relx_submit_group_h2d(relx_ctx *ctx, int n, const relx_bound *const *bounds,
+                          const void *const *srcs, const size_t *src_bytes, void *const *dsts,
+                          const size_t *dst_bytes, const relx_options *opt, relx_report *reports,
+                          relx_report *total, relx_completion **out, relx_err *err);
+
+/* Completion::query: *done = 1 once every kernel of the call finished. */
+int relx_completion_query(relx_completion *c, int *done, relx_err *err);
+
+/* Completion::wait: block until done; reports a channel outside the
+ * parameters (`channel_out_of_range`) like the blocking call would. */
+int relx_completion_wait(relx_completion *c, relx_err *err);
+
+/* Completion::waitStream: order `stream` after the call without blocking
+ * the host (H2D: the destination is ready for kernels on `stream`). */
+int relx_completion_wait_stream(relx_completion *c, uint64_t stream, relx_err *err);
+
+/* Free a completion; an unfinished call is waited for first (abandoning a
+ * handle drains, as the reference's ~Completion does). */
+void relx_completion_free(relx_completion *c);
+
 /* Device-resident source -> host destination: the D2H direction of
  * dispatch::executeDispatch / executeTransfer (libreloc/src/Transfer.cpp:469-488,
  * libreloc/src/Dispatch.cpp:1072-1099,1513-1530; the reference's

@@ -97,6 +97,14 @@ SIGNATURES = {
                                     ctypes.POINTER(relx_options), ctypes.POINTER(relx_report),
                                     ctypes.POINTER(relx_report), _E]),
     "relx_relayout_device": (_I, [_VP, _VP, _I, _VP, _VP, _U64, _E]),
+    "relx_submit_group_h2d": (_I, [_VP, _I, ctypes.POINTER(_VP), ctypes.POINTER(_VP),
+                                   ctypes.POINTER(_SZ), ctypes.POINTER(_VP), ctypes.POINTER(_SZ),
+                                   ctypes.POINTER(relx_options), ctypes.POINTER(relx_report),
+                                   ctypes.POINTER(relx_report), ctypes.POINTER(_VP), _E]),
+    "relx_completion_query": (_I, [_VP, ctypes.POINTER(_I), _E]),
+    "relx_completion_wait": (_I, [_VP, _E]),
+    "relx_completion_wait_stream": (_I, [_VP, _U64, _E]),
+    "relx_completion_free": (None, [_VP]),
     "relx_execute_d2h": (_I, [_VP, _VP, _VP, _SZ, _VP, _SZ, ctypes.POINTER(relx_options),
                               ctypes.POINTER(relx_report), _E]),
     "relx_host_stage": (_I, [_VP, _I, _VP, _VP, _I, _E]),

@@ -11,7 +11,9 @@
 namespace relx {
 void execute_members(Context &ctx, int n, BoundHandle *const *bounds, const void *const *srcs,
                      const size_t *src_bytes, void *const *dsts, const size_t *dst_bytes,
-                     const relx_options &opt, relx_report *reports, relx_report *total);
+                     const relx_options &opt, relx_report *reports, relx_report *total,
+                     Completion *comp);
+void completion_wait(Completion &c);
 std::unique_ptr<Context> make_context(int device, int64_t max_retained);
 bool drain(Context &ctx);
 void destroy_context(Context &ctx);
@@ -28,7 +30,11 @@ struct relx_bound {
   relx::BoundHandle h;
 };
 struct relx_ctx {
-  std::unique_ptr<relx::Context> ctx;
+  std::shared_ptr<relx::Context> ctx;
+};
+
+struct relx_completion {
+  relx::Completion c;
 };
 
 namespace {
@@ -250,7 +256,7 @@ int relx_ctx_stats_get(const relx_ctx *ctx, relx_ctx_stats *out) {
 static int run_group(relx_ctx *ctx, int n, const relx_bound *const *bounds,
                      const void *const *srcs, const size_t *src_bytes, void *const *dsts,
                      const size_t *dst_bytes, const relx_options *opt, relx_report *reports,
-                     relx_report *total, relx_err *err) {
+                     relx_report *total, relx_err *err, relx_completion *comp = nullptr) {
   if (!ctx) {
     set_err(err, "invalid_argument", "null context");
     return RELX_ERROR;
@@ -276,7 +282,8 @@ static int run_group(relx_ctx *ctx, int n, const relx_bound *const *bounds,
         throw relx::Error("invalid_argument", "null bound plan");
       hs.push_back(const_cast<relx::BoundHandle *>(&bounds[i]->h));
     }
-    relx::execute_members(c, n, hs.data(), srcs, src_bytes, dsts, dst_bytes, o, reports, total);
+    relx::execute_members(c, n, hs.data(), srcs, src_bytes, dsts, dst_bytes, o, reports, total,
+                          comp ? &comp->c : nullptr);
   });
   if (rc != RELX_OK) {
     ++c.failures;
@@ -302,6 +309,80 @@ int relx_execute_group_h2d(relx_ctx *ctx, int n, const relx_bound *const *bounds
                            const size_t *dst_bytes, const relx_options *opt,
                            relx_report *reports, relx_report *total, relx_err *err) {
   return run_group(ctx, n, bounds, srcs, src_bytes, dsts, dst_bytes, opt, reports, total, err);
+}
+
+int relx_submit_group_h2d(relx_ctx *ctx, int n, const relx_bound *const *bounds,
+                          const void *const *srcs, const size_t *src_bytes, void *const *dsts,
+                          const size_t *dst_bytes, const relx_options *opt, relx_report *reports,
+                          relx_report *total, relx_completion **out, relx_err *err) {
+  if (!ctx || !out) {
+    set_err(err, "invalid_argument", "null context or output");
+    return RELX_ERROR;
+  }
+  auto *comp = new relx_completion{};
+  comp->c.ctx = ctx->ctx;
+  {
+    relx::DeviceScope scope(ctx->ctx->device);
+    if (hipEventCreateWithFlags(&comp->c.ev, hipEventDisableTiming) != hipSuccess) {
+      delete comp;
+      set_err(err, "backend_failure", "hipEventCreateWithFlags failed");
+      return RELX_ERROR;
+    }
+  }
+  const int rc =
+      run_group(ctx, n, bounds, srcs, src_bytes, dsts, dst_bytes, opt, reports, total, err, comp);
+  if (rc != RELX_OK) {
+    relx_completion_free(comp);
+    return rc;
+  }
+  *out = comp;
+  return RELX_OK;
+}
+
+int relx_completion_query(relx_completion *c, int *done, relx_err *err) {
+  return guarded(err, [&] {
+    if (!c || !done)
+      throw relx::Error("invalid_argument", "null argument");
+    relx::DeviceScope scope(c->c.ctx->device);
+    const hipError_t e = hipEventQuery(c->c.ev);
+    if (e != hipSuccess && e != hipErrorNotReady)
+      throw relx::Error("backend_failure", std::string("hipEventQuery: ") + hipGetErrorString(e));
+    *done = e == hipSuccess ? 1 : 0;
+    if (*done)
+      relx::completion_wait(c->c); // reports a channel error once complete
+  });
+}
+
+int relx_completion_wait(relx_completion *c, relx_err *err) {
+  return guarded(err, [&] {
+    if (!c)
+      throw relx::Error("invalid_argument", "null completion");
+    relx::completion_wait(c->c);
+  });
+}
+
+int relx_completion_wait_stream(relx_completion *c, uint64_t stream, relx_err *err) {
+  return guarded(err, [&] {
+    if (!c)
+      throw relx::Error("invalid_argument", "null completion");
+    relx::DeviceScope scope(c->c.ctx->device);
+    const hipError_t e = hipStreamWaitEvent(reinterpret_cast<hipStream_t>(stream), c->c.ev, 0);
+    if (e != hipSuccess)
+      throw relx::Error("backend_failure", std::string("hipStreamWaitEvent: ") + hipGetErrorString(e));
+  });
+}
+
+void relx_completion_free(relx_completion *c) {
+  if (!c)
+    return;
+  {
+    relx::DeviceScope scope(c->c.ctx->device);
+    if (c->c.ev) {
+      (void)hipEventSynchronize(c->c.ev); // abandoning a handle drains its work
+      (void)hipEventDestroy(c->c.ev);
+    }
+  }
+  delete c;
 }
 
 int relx_execute_d2h(relx_ctx *ctx, const relx_bound *bound, const void *src, size_t src_bytes,

@@ -298,7 +298,7 @@ struct Member {
 } // namespace
 
 void execute(Context &ctx, std::vector<Member> &members, const relx_options &opt,
-             relx_report *total);
+             relx_report *total, Completion *comp);
 
 } // namespace relx
 
@@ -307,7 +307,8 @@ namespace relx {
 
 void execute_members(Context &ctx, int n, BoundHandle *const *bounds, const void *const *srcs,
                      const size_t *src_bytes, void *const *dsts, const size_t *dst_bytes,
-                     const relx_options &opt, relx_report *reports, relx_report *total) {
+                     const relx_options &opt, relx_report *reports, relx_report *total,
+                     Completion *comp) {
   DeviceGuard guard(ctx.device);
   std::vector<Member> ms;
   size_t wire_total = 0;
@@ -344,11 +345,11 @@ void execute_members(Context &ctx, int n, BoundHandle *const *bounds, const void
     wire_total += (static_cast<size_t>(m.dp->wire_bytes) + 255) / 256 * 256;
     ms.push_back(m);
   }
-  execute(ctx, ms, opt, total);
+  execute(ctx, ms, opt, total, comp);
 }
 
 void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
-             relx_report *total) {
+             relx_report *total, Completion *comp) {
   size_t wire_total = 0;
   for (const Member &m : ms)
     wire_total = std::max(wire_total, m.wire_off + static_cast<size_t>(m.dp->wire_bytes));
@@ -382,8 +383,9 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
   bool any_generic = false;
   for (const Member &m : ms)
     any_generic = any_generic || m.dp->family == kFamGeneric;
+  int32_t *status = ctx.status + (ctx.status_next++ % kStatusSlots);
   if (any_generic)
-    HIPCHECK(hipMemsetAsync(ctx.status, 0, sizeof(int32_t), ctx.compute));
+    HIPCHECK(hipMemsetAsync(status, 0, sizeof(int32_t), ctx.compute));
 
   int slot = 0;
   int ev = 0;
@@ -425,7 +427,7 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
       HIPCHECK(hipEventRecord(ce, ctx.copy));
       HIPCHECK(hipStreamWaitEvent(ctx.compute, ce, 0));
       launches += launch_program(dp, v0, v1, v0 == 0, v1 == p.units, wire, m.dst, par.pf, par.pi,
-                                 ctx.status, ctx.compute);
+                                 status, ctx.compute);
       ++chunks;
     }
     if (m.report) {
@@ -460,12 +462,30 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
     std::snprintf(sum.implementation, sizeof(sum.implementation), "hip_relayout_group");
     *total = sum;
   }
+  if (comp) {
+    HIPCHECK(hipEventRecord(comp->ev, ctx.compute));
+    comp->status = status;
+    comp->generic = any_generic;
+    return;
+  }
   if (opt.no_wait)
     return;
   HIPCHECK(hipEventSynchronize(ctx.done_ev));
   if (any_generic) {
     int32_t flag = 0;
-    HIPCHECK(hipMemcpy(&flag, ctx.status, sizeof(flag), hipMemcpyDeviceToHost));
+    HIPCHECK(hipMemcpy(&flag, status, sizeof(flag), hipMemcpyDeviceToHost));
+    if (flag)
+      throw Error("channel_out_of_range", "a stage selected a channel outside its parameters");
+  }
+}
+
+void completion_wait(Completion &c) {
+  DeviceGuard guard(c.ctx->device);
+  HIPCHECK(hipEventSynchronize(c.ev));
+  if (c.generic && !c.checked) {
+    int32_t flag = 0;
+    HIPCHECK(hipMemcpy(&flag, c.status, sizeof(flag), hipMemcpyDeviceToHost));
+    c.checked = true;
     if (flag)
       throw Error("channel_out_of_range", "a stage selected a channel outside its parameters");
   }
@@ -558,8 +578,9 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
     HIPCHECK(hipStreamWaitEvent(ctx.compute, ctx.start_ev, 0));
     HIPCHECK(hipStreamWaitEvent(ctx.copy, ctx.start_ev, 0));
   }
+  int32_t *status = ctx.status + (ctx.status_next++ % kStatusSlots);
   if (dp.family == kFamGeneric)
-    HIPCHECK(hipMemsetAsync(ctx.status, 0, sizeof(int32_t), ctx.compute));
+    HIPCHECK(hipMemsetAsync(status, 0, sizeof(int32_t), ctx.compute));
   const BoundHandle::DevParams par = h.device_params(ctx.device, 0);
   uint8_t *result = ctx.wire;
   uint8_t *out = static_cast<uint8_t *>(dst);
@@ -589,7 +610,7 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
     const int64_t u1 = std::min(units, u0 + per);
     if (axis >= 0 || u0 == 0) {
       launches += launch_all(dp, prefix_launches(dp, fixed, axis, u0, u1), src, result, par.pf,
-                             par.pi, ctx.status, ctx.compute);
+                             par.pi, status, ctx.compute);
       hipEvent_t ke = ctx.chunk_ev[static_cast<size_t>(ev)];
       ev = (ev + 1) % kChunkEvents;
       HIPCHECK(hipEventRecord(ke, ctx.compute));
@@ -620,7 +641,7 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
   HIPCHECK(hipEventSynchronize(ctx.done_ev));
   if (dp.family == kFamGeneric) {
     int32_t flag = 0;
-    HIPCHECK(hipMemcpy(&flag, ctx.status, sizeof(flag), hipMemcpyDeviceToHost));
+    HIPCHECK(hipMemcpy(&flag, status, sizeof(flag), hipMemcpyDeviceToHost));
     if (flag)
       throw Error("channel_out_of_range", "a stage selected a channel outside its parameters");
   }
@@ -661,6 +682,13 @@ std::unique_ptr<Context> make_context(int device, int64_t max_retained) {
   return ctx;
 }
 
+Context::~Context() {
+  if (status) {
+    DeviceScope scope(device);
+    (void)hipFree(status);
+  }
+}
+
 // Drain both streams. False when completion cannot be proven.
 bool drain(Context &ctx) {
   DeviceGuard guard(ctx.device);
@@ -683,8 +711,8 @@ void destroy_context(Context &ctx) {
     (void)hipEventDestroy(ctx.done_ev);
   if (ctx.wire)
     (void)hipFree(ctx.wire);
-  if (ctx.status)
-    (void)hipFree(ctx.status);
+  ctx.wire = nullptr;
+  ctx.wire_cap = 0;
   if (ctx.copy)
     (void)hipStreamDestroy(ctx.copy);
   if (ctx.compute)

@@ -21,6 +21,24 @@
 
 namespace relx {
 
+// Makes `dev` the current device for a scope, restoring the previous one.
+struct DeviceScope {
+  int prev = -1;
+  explicit DeviceScope(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess)
+      prev = -1;
+    if (prev != dev)
+      (void)hipSetDevice(dev);
+  }
+  ~DeviceScope() {
+    int cur;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev)
+      (void)hipSetDevice(prev);
+  }
+  DeviceScope(const DeviceScope &) = delete;
+  DeviceScope &operator=(const DeviceScope &) = delete;
+};
+
 // One value stage as host scalars (reference StageArithmetic,
 // libreloc/include/reloc/TypedExecute.h:52-68).
 struct HostStage {
@@ -168,7 +186,8 @@ struct Context {
   hipEvent_t start_ev = nullptr, done_ev = nullptr;
   uint8_t *wire = nullptr;
   size_t wire_cap = 0;
-  int32_t *status = nullptr;
+  int32_t *status = nullptr; // kStatusSlots flags, one per call in flight
+  int status_next = 0;
   std::unique_ptr<Workers> workers;
   unsigned worker_threads = 0;
   int64_t max_retained = 0;
@@ -176,6 +195,20 @@ struct Context {
   int64_t calls = 0, failures = 0;
   bool quarantined = false;
   bool closed = false;
+  ~Context(); // frees the status flags (the rest goes in destroy_context)
+};
+
+constexpr int kStatusSlots = 64;
+
+// An asynchronous call's completion: an event recorded after its last kernel
+// and the status flag its element-wise kernels report into. Holds the context
+// so the flag outlives a close.
+struct Completion {
+  std::shared_ptr<Context> ctx;
+  hipEvent_t ev = nullptr;
+  int32_t *status = nullptr;
+  bool generic = false;
+  bool checked = false;
 };
 
 } // namespace relx

@@ -346,3 +346,85 @@ def execute_dispatch_group(group, *, caller_stream=None, gather_threads=1, gathe
         return dict(group.report)
     finally:
         group.executing = False
+
+
+class DispatchCompletion:
+    """Completion of a submitted group (reference pyreloc.DispatchCompletion,
+    libreloc/python/PyDispatch.cpp:659-695): wait(), query() and
+    wait_stream(stream). The group report is filled in once it completed."""
+
+    def __init__(self, group, native, items):
+        self.group = group
+        self._native = native
+        self._items = items
+
+    def _finish(self):
+        if self.group.consumed:
+            return
+        items = []
+        for r, rep in zip(self._items, self._native.reports):
+            r.consumed = True
+            r.report = _report(rep, r)
+            items.append(dict(r.report))
+        self.group.consumed = True
+        self.group.report = {"logical_transfers": len(items), "request_count": 1,
+                             "completion_granularity": "group",
+                             "payload_copy_calls": sum(i["host_chunks"] for i in items),
+                             "kernel_launches": sum(i["kernel_launches"] for i in items),
+                             "output_bytes": self._native.total["destination_bytes"],
+                             "staging": [], "items": items}
+
+    def wait(self):
+        try:
+            self._native.wait()
+        finally:
+            self.group.executing = False
+        self._finish()
+        return dict(self.group.report)
+
+    def query(self):
+        done = self._native.query()
+        if done:
+            self.group.executing = False
+            self._finish()
+        return done
+
+    def wait_stream(self, stream):
+        self._native.wait_stream(stream)
+
+    def close(self):
+        self._native.close()
+        self.group.executing = False
+
+    def __reduce_ex__(self, protocol):
+        raise TypeError("dispatch completions cannot be serialized")
+
+
+def submit_dispatch_group(group, *, caller_stream=None, gather_threads=8, gather_pool=None,
+                          pinning="auto", min_pinned_bytes=None, max_scratch_bytes=64 << 20,
+                          resources=None, owners=None, device_layout=False, n_buffers=2,
+                          chunked_members=False):
+    """Enqueue a group and return its completion; host staging of pageable
+    sources happens before this returns (reference submit_dispatch_group)."""
+    if group.executing or group.consumed:
+        raise TransferError("already_executed", "group is executing or already executed")
+    if owners is None or not isinstance(owners, tuple) or len(owners) not in (2, 3):
+        raise ValueError("owners must be (source owners, destination owners[, extra owners])")
+    if gather_threads < 1 or not max_scratch_bytes:
+        raise ValueError("gather_threads and max_scratch_bytes must be positive")
+    _pinning(pinning)
+    dev = max(0, group.items[0].destination.device)
+    ctx = resources if resources is not None else _resources_for(dev)
+    bounds = [r.template.bound for r in group.items]
+    srcs = [(r.source.address, r.source.capacity_bytes - r.source.offset_bytes) for r in group.items]
+    dsts = [(r.destination.address, r.destination.capacity_bytes - r.destination.offset_bytes)
+            for r in group.items]
+    group.executing = True
+    try:
+        native = ctx.submit_group_h2d(bounds, srcs, dsts, owners=owners, n_buffers=n_buffers,
+                                      gather_threads=gather_threads,
+                                      caller_stream=int(caller_stream or 0))
+    except Exception:
+        group.executing = False
+        raise
+    return DispatchCompletion(group, native, group.items)

@@ -262,6 +262,25 @@ class Context:
             _raise(err)
         return rep.as_dict()
 
+    def submit_group_h2d(self, bounds, srcs, dsts, owners=None, **options):
+        """Enqueue a group without waiting; returns a Completion. `owners`
+        are kept alive until the completion is waited for or closed."""
+        n = len(bounds)
+        bh = (ctypes.c_void_p * n)(*[b._h.value for b in bounds])
+        sp = (ctypes.c_void_p * n)(*[s[0] for s in srcs])
+        sb = (ctypes.c_size_t * n)(*[s[1] for s in srcs])
+        dp = (ctypes.c_void_p * n)(*[d[0] for d in dsts])
+        db = (ctypes.c_size_t * n)(*[d[1] for d in dsts])
+        reps = (N.relx_report * n)()
+        total = N.relx_report()
+        err = N.relx_err()
+        h = ctypes.c_void_p()
+        opt = _options(**options)
+        if N.lib().relx_submit_group_h2d(self._h, n, bh, sp, sb, dp, db, ctypes.byref(opt), reps,
+                                         ctypes.byref(total), ctypes.byref(h), ctypes.byref(err)):
+            _raise(err)
+        return Completion(h, [r.as_dict() for r in reps], total.as_dict(), (bounds, owners))
+
     def relayout_device(self, bound, wire_ptr, dst_ptr, wire_boundary=0, stream=0):
         """Launch the device relayout on a device-resident wire (async)."""
         err = N.relx_err()
@@ -301,6 +320,46 @@ class Context:
             pass
 
 
+class Completion:
+    """An enqueued call (reference dispatch::Completion): wait(), query(),
+    wait_stream(stream); closing or dropping it waits for the work first.
+    Holds the plans and buffers it was given until then."""
+
+    def __init__(self, handle, reports, total, keep):
+        self._h = handle
+        self.reports = reports
+        self.total = total
+        self._keep = keep
+
+    def _call(self, name, *args):
+        if not self._h:
+            raise TransferError("resources_closed", "completion is closed")
+        err = N.relx_err()
+        if getattr(N.lib(), name)(self._h, *args, ctypes.byref(err)):
+            _raise(err)
+
+    def wait(self):
+        self._call("relx_completion_wait")
+
+    def query(self):
+        done = ctypes.c_int(0)
+        self._call("relx_completion_query", ctypes.byref(done))
+        return bool(done.value)
+
+    def wait_stream(self, stream):
+        self._call("relx_completion_wait_stream", int(stream))
+
+    def close(self):
+        h = getattr(self, "_h", None)
+        if h:
+            N.lib().relx_completion_free(h)
+            self._h = None
+            self._keep = None
+
+    def __del__(self):
+        self.close()
+
+
 def verify_launches(bound, wire_boundary=0, chunk_bytes=0):
     """Check on the host every kernel launch the executor would make for
     `bound` (wire at `wire_boundary`, chunks of `chunk_bytes`); returns the
@@ -332,7 +391,8 @@ def measure_d2h(device=0, nbytes=256 << 20, iters=20, rounds=3):
 
 # The typed dispatch API (prepare_dispatch / execute_dispatch / groups) lives
 # in sym_amd.dispatch and is re-exported here under pyreloc's names.
-from .dispatch import (BufferView, DispatchRequest, DispatchTemplate,  # noqa: E402,F401
-                       GroupRequest, Resources, execute_dispatch, execute_dispatch_group,
-                       prepare_dispatch, prepare_dispatch_from_template, prepare_dispatch_group,
-                       prepare_dispatch_template, query_capability)
+from .dispatch import (BufferView, DispatchCompletion, DispatchRequest,  # noqa: E402,F401
+                       DispatchTemplate, GroupRequest, Resources, execute_dispatch,
+                       execute_dispatch_group, prepare_dispatch, prepare_dispatch_from_template,
+                       prepare_dispatch_group, prepare_dispatch_template, query_capability,
+                       submit_dispatch_group)

@@ -187,3 +187,64 @@ def test_c3_device_to_host_matches_h2d(resources, rng):
     out = np.empty(rows * cols * 2, np.uint8)
     resources.execute_d2h(b, qd.data_ptr(), q.nbytes, out.ctypes.data, out.nbytes, chunk_bytes=16 << 10)
     assert np.array_equal(out, via_h2d)
+
+
+# ------------------------------------------------------------ asynchronous
+
+def _expert_group(rng, rows, cols, n, pinned):
+    plan = P.Plan(W.c4_plan().blob)
+    entries, outs, wants, keep = [], [], [], []
+    for _ in range(n):
+        q, s = W.int8_weight(rows, cols, rng), W.scales(rows, rng)
+        if pinned:
+            qt = torch.from_numpy(q).pin_memory()
+            q = qt.numpy()
+            keep.append(qt)
+        keep.append(q)
+        b = P.Bound(plan, {"s0": rows, "s1": cols}, W.param("scale", s))
+        out = torch.empty((rows, cols), dtype=torch.float16, device="cuda")
+        entries.append((b, host_view(q), device_view(out), "h2d"))
+        outs.append(out)
+        deq = np.ascontiguousarray(O.dequantize_s8_f32(q, s[:, None], np.int32(0)), np.float32)
+        wants.append(O.narrow_f32_f16_bits(deq.view(np.uint32)).astype(np.uint16))
+    return entries, outs, wants, keep
+
+
+@pytest.mark.parametrize("pinned", [False, True])
+def test_submitted_groups_overlap_and_order_a_stream(resources, rng, pinned):
+    """Two groups in flight at once; the second is consumed on a torch stream
+    through wait_stream (no host wait) and the first through wait()."""
+    ea, oa, wa, ka = _expert_group(rng, 1024, 512, 3, pinned)
+    eb, ob, wb, kb = _expert_group(rng, 512, 1024, 3, pinned)
+    say("submit two groups", "pinned" if pinned else "pageable")
+    ca = P.submit_dispatch_group(P.prepare_dispatch_group(ea), resources=resources,
+                                 owners=(tuple(ka), tuple(oa)))
+    cb = P.submit_dispatch_group(P.prepare_dispatch_group(eb), resources=resources,
+                                 owners=(tuple(kb), tuple(ob)))
+    consumer = torch.cuda.Stream()
+    cb.wait_stream(consumer.cuda_stream)
+    with torch.cuda.stream(consumer):
+        sums = [o.view(torch.int16).to(torch.int64).sum() for o in ob]
+    rep = ca.wait()
+    assert rep["logical_transfers"] == 3 and ca.query()
+    for out, want in zip(oa, wa):
+        assert np.array_equal(out.cpu().numpy().view(np.uint16), want)
+    consumer.synchronize()
+    for sm, want in zip(sums, wb):
+        assert int(sm.item()) == int(want.view(np.int16).astype(np.int64).sum())
+    cb.wait()
+    for out, want in zip(ob, wb):
+        assert np.array_equal(out.cpu().numpy().view(np.uint16), want)
+    with pytest.raises(P.TransferError):
+        P.submit_dispatch_group(ca.group, resources=resources, owners=((), ()))
+    ca.close()
+    cb.close()
+
+
+def test_abandoned_completion_drains(resources, rng):
+    e, o, w, k = _expert_group(rng, 256, 256, 2, True)
+    c = P.submit_dispatch_group(P.prepare_dispatch_group(e), resources=resources,
+                                owners=(tuple(k), tuple(o)))
+    c.close()  # waits for the work before releasing the handle
+    for out, want in zip(o, w):
+        assert np.array_equal(out.cpu().numpy().view(np.uint16), want)
