@@ -49,15 +49,19 @@ const char *relx_version(void);
  * a plan. Replaces reloc::peekWireVersion (libreloc/src/Decode.cpp:868-874). */
 int relx_wire_version(const uint8_t *blob, size_t n);
 
-/* Decode a wire v0 (layout) or v1 (typed) plan; the header picks the decoder.
- * Replaces reloc::decodePlan / reloc::decodeTypedPlan
- * (libreloc/src/Decode.cpp:876-948) and pyreloc.load_plan/load_typed_plan
- * (libreloc/python/PyReloc.cpp:596,921). Errors: code "decode_error" with the
- * byte offset of the violated item. */
+/* Decode a wire v0 (layout), v1 (typed) or v2 (indexed) plan; the header
+ * picks the decoder. Replaces reloc::decodePlan / reloc::decodeTypedPlan /
+ * reloc::decodeIndexedPlan (libreloc/src/Decode.cpp:876-948,993-1012) and
+ * pyreloc.load_plan / load_typed_plan / load_indexed_plan
+ * (libreloc/python/PyReloc.cpp:596,864,921). Errors: code "decode_error"
+ * with the byte offset of the violated item. */
 int relx_plan_load(const uint8_t *blob, size_t n, relx_plan **out, relx_err *err);
 
-/* 1 for a typed (v1) plan, 0 for a layout (v0) plan. */
+/* 1 for a typed (v1) plan, 0 otherwise. */
 int relx_plan_is_typed(const relx_plan *plan);
+
+/* The decoded plan's wire version (0, 1 or 2). */
+int relx_plan_version(const relx_plan *plan);
 
 /* Number of plan symbols and the i-th symbol name (owned by the plan). */
 int relx_plan_symbol_count(const relx_plan *plan);
@@ -88,6 +92,20 @@ typedef struct relx_param {
 int relx_bind(const relx_plan *plan, const char *const *sym_names, const int64_t *sym_values,
               int nsym, const relx_param *params, int nparam, relx_bound **out,
               relx_err *err);
+
+/* Bind an indexed (v2) plan: symbols plus the index operand, given as its
+ * element type (kind 2 integer; bits 32 or 64), extents and little-endian
+ * bytes, which are copied and range-checked during the call. The bound plan
+ * describes the selected rows: an identity relocation of
+ * [count, row elements] plus the plan's cast. Replaces reloc::bindIndexed
+ * (libreloc/src/Bind.cpp:701-819) and pyreloc.bind_indexed /
+ * bind_indexed_from_pointer (libreloc/python/PyReloc.cpp:876-919). Errors:
+ * "bind_error" with the reference's messages, including
+ * "index_out_of_range: index_select row is outside the source". */
+int relx_bind_indexed(const relx_plan *plan, const char *const *sym_names,
+                      const int64_t *sym_values, int nsym, int index_kind, int index_bits,
+                      const int64_t *index_extents, int index_rank, const void *index_data,
+                      size_t index_bytes, relx_bound **out, relx_err *err);
 
 void relx_bound_free(relx_bound *bound);
 
@@ -121,6 +139,14 @@ typedef struct relx_bound_info {
   int host_stages_max;  /* leading per-tensor stages a host may apply */
   int host_stages_auto; /* of those, the narrowing ones applied for a pageable source */
   int64_t wire_bytes_at[RELX_MAX_STAGES + 1]; /* H2D wire (source layout) at boundary k */
+  /* indexed (v2) plans (reference IndexedBoundPlan, libreloc/include/reloc/Bind.h):
+   * the physical source is table_rows rows of row_elements elements;
+   * source_bytes above counts the selected rows only */
+  int indexed;
+  int64_t table_rows;
+  int64_t row_elements;
+  int64_t table_bytes;
+  int64_t index_count;
 } relx_bound_info;
 
 int relx_bound_query(const relx_bound *bound, relx_bound_info *out);
@@ -190,6 +216,10 @@ typedef struct relx_report {
  * for the H2D direction, executeTransfer (libreloc/src/Transfer.cpp:493-544)
  * for layout plans, and pyreloc.execute_dispatch / execute_transfer
  * (libreloc/python/PyDispatch.cpp:159-235, PyTransfer.cpp:180-219).
+ * An indexed (v2) bound plan takes the whole host table as `src`: worker
+ * threads gather the selected rows (through the leading per-tensor stages
+ * the staging applies) into the pinned ring, as the reference's CPU path
+ * does (libreloc/src/Dispatch.cpp:1238-1247), and the device runs the rest.
  * Errors: "insufficient_capacity", "invalid_options", "backend_failure",
  * "channel_out_of_range", "invalid_view". */
 int relx_execute_h2d(relx_ctx *ctx, const relx_bound *bound, const void *src, size_t src_bytes,
@@ -260,6 +290,19 @@ int relx_execute_d2h(relx_ctx *ctx, const relx_bound *bound, const void *src, si
  * (libreloc/include/reloc/CudaKernels.h:28-122). */
 int relx_relayout_device(relx_ctx *ctx, const relx_bound *bound, int wire_boundary,
                          const void *wire, void *dst, uint64_t stream, relx_err *err);
+
+/* Indexed plans with a device-resident table: gather the bound's selected
+ * rows of `table` (table_rows x row_elements source elements, dense) into
+ * `dst` (dense selected rows of the result type), the plan's cast fused into
+ * the gather, on `stream` (0 = the context's compute stream). Asynchronous:
+ * returns after the launch. The reference executes indexed plans only from
+ * host memory, gathering on the CPU (libreloc/src/Dispatch.cpp:1269-1283,
+ * 1397-1404); this is the device form of its index_select. Errors:
+ * "plan_mismatch" (not an indexed plan), "insufficient_capacity",
+ * "invalid_view" (null or misaligned buffers). */
+int relx_index_select_device(relx_ctx *ctx, const relx_bound *bound, const void *table,
+                             size_t table_bytes, void *dst, size_t dst_bytes, uint64_t stream,
+                             relx_err *err);
 
 /* Apply a bound plan's leading `host_stages` stages to a dense source on the
  * host (the staging-side transform of relx_execute_h2d), writing the wire

@@ -45,6 +45,13 @@ def lib():
         L.ref_layout_execute.restype = ctypes.c_int
         L.ref_layout_execute.argtypes = [vp, vp, vp]
         L.ref_layout_free.argtypes = [vp]
+        L.ref_indexed_decode.restype = ctypes.c_int
+        L.ref_indexed_decode.argtypes = [cp, sz, ctypes.POINTER(ctypes.c_int64), cp, sz]
+        L.ref_indexed_prepare.restype = vp
+        L.ref_indexed_prepare.argtypes = [cp, sz, ctypes.POINTER(cp), ctypes.POINTER(ctypes.c_int64),
+                                          ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                          ctypes.POINTER(ctypes.c_int64), ctypes.c_int, vp, sz,
+                                          ctypes.c_uint, cp, sz]
         _lib = L
     return _lib
 
@@ -114,3 +121,32 @@ class LayoutRef:
         if getattr(self, "h", None):
             lib().ref_layout_free(self.h)
             self.h = None
+
+
+def indexed_decode(blob):
+    """decodeIndexedPlan: None when valid, else (offset, message)."""
+    off = ctypes.c_int64(-1)
+    err = ctypes.create_string_buffer(512)
+    if lib().ref_indexed_decode(blob, len(blob), ctypes.byref(off), err, 512):
+        return off.value, err.value.decode()
+    return None
+
+
+class IndexedRef(TypedRef):
+    """decodeIndexedPlan + bindIndexed + the indexed program of
+    prepareIndexSelect; execute() runs executeHost's indexed rows over the
+    whole table."""
+
+    def __init__(self, blob, symbols, index_dtype, index_extents, index_bytes, threads=1):
+        L = lib()
+        sn, sv, ns = _syms(symbols)
+        kind, bits = KINDS[index_dtype]
+        ext = (ctypes.c_int64 * max(1, len(index_extents)))(*[int(e) for e in index_extents])
+        self._keep = [ctypes.create_string_buffer(bytes(index_bytes), max(1, len(index_bytes)))]
+        err = ctypes.create_string_buffer(512)
+        self.h = L.ref_indexed_prepare(blob, len(blob), sn, sv, ns, kind, bits, ext,
+                                       len(index_extents), ctypes.addressof(self._keep[0]),
+                                       len(index_bytes), threads, err, 512)
+        if not self.h:
+            raise RuntimeError(err.value.decode())
+        self.result_bytes = L.ref_typed_result_bytes(self.h)

@@ -9,6 +9,10 @@
 //   typed::prepareProgram          libreloc/src/TypedExecute.cpp:292-403
 //   typed::executeHost             libreloc/src/TypedExecute.cpp:926-931
 //   executeH2DThreaded             libreloc/src/Execute.cpp:145-216
+//   decodeIndexedPlan / bindIndexed libreloc/src/Decode.cpp:993-1012,
+//                                  libreloc/src/Bind.cpp:701-819; the program
+//                                  fields prepareIndexSelect sets
+//                                  (libreloc/src/Dispatch.cpp:1269-1283)
 #include "reloc/Bind.h"
 #include "reloc/Decode.h"
 #include "reloc/Execute.h"
@@ -140,5 +144,54 @@ int ref_layout_execute(void *h, const void *src, void *dst) {
 }
 
 void ref_layout_free(void *h) { delete static_cast<RefLayout *>(h); }
+
+// Decode a wire v2 blob: 0 when valid, else 1 with the message and offset.
+int ref_indexed_decode(const uint8_t *blob, size_t n, int64_t *offset, char *err, size_t cap) {
+  auto decoded = reloc::decodeIndexedPlan(blob, n);
+  if (auto *e = std::get_if<reloc::DecodeError>(&decoded)) {
+    setErr(err, cap, e->message);
+    if (offset)
+      *offset = static_cast<int64_t>(e->offset);
+    return 1;
+  }
+  return 0;
+}
+
+// Decode + bindIndexed + prepareProgram, then the indexed program fields
+// (rows, row elements, row indices) as prepareIndexSelect sets them; errors
+// are "decode: ...", "bind: ..." or "<code>: ...".
+void *ref_indexed_prepare(const uint8_t *blob, size_t n, const char **symNames,
+                          const int64_t *symVals, int nsym, int idxKind, int idxBits,
+                          const int64_t *idxExtents, int idxRank, const void *idxData,
+                          size_t idxBytes, unsigned threads, char *err, size_t cap) {
+  auto decoded = reloc::decodeIndexedPlan(blob, n);
+  if (auto *e = std::get_if<reloc::DecodeError>(&decoded)) {
+    setErr(err, cap, "decode: " + e->message);
+    return nullptr;
+  }
+  reloc::SymbolMap symbols;
+  for (int i = 0; i < nsym; ++i)
+    symbols[symNames[i]] = symVals[i];
+  std::vector<int64_t> extents(idxExtents, idxExtents + idxRank);
+  auto bound = reloc::bindIndexed(std::get<reloc::IndexedRelocationPlan>(decoded), symbols,
+                                  typeOf(idxKind, idxBits), extents, idxData, idxBytes);
+  if (auto *e = std::get_if<reloc::BindError>(&bound)) {
+    setErr(err, cap, "bind: " + e->message);
+    return nullptr;
+  }
+  auto &b = std::get<reloc::IndexedBoundPlan>(bound);
+  auto program = reloc::typed::prepareProgram(b.selected);
+  if (auto *e = std::get_if<reloc::typed::ExecutionError>(&program)) {
+    setErr(err, cap, e->code + ": " + e->message);
+    return nullptr;
+  }
+  auto *h = new RefTyped{std::move(std::get<reloc::typed::Program>(program)), nullptr};
+  h->program.indexedSourceRows = b.sourceExtents.front();
+  h->program.indexedRowElements = b.rowElements;
+  h->program.rowIndices = b.indices;
+  if (threads > 1)
+    h->pool = std::make_unique<reloc::GatherPool>(threads);
+  return h;
+}
 
 } // extern "C"

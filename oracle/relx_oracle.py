@@ -4,6 +4,7 @@ This module is the checker the parity tests compare the HIP path against. It
 restates, in numpy, the reference runtime's algorithm for the hot path:
 
 * wire decode v0/v1      -- libreloc/src/Decode.cpp:115-948
+* wire decode v2         -- libreloc/src/Decode.cpp:950-1012 (indexed plans)
 * expression evaluation  -- libreloc/src/Bind.cpp:84-161
 * bind (layout)          -- libreloc/src/Bind.cpp:176-384
 * bindTyped              -- libreloc/src/Bind.cpp:494-699
@@ -16,6 +17,9 @@ restates, in numpy, the reference runtime's algorithm for the hot path:
                             semantics of walk()/element(), 202-290)
 * layout gather          -- libreloc/src/Execute.cpp:94-134
 * planChunks             -- libreloc/src/ChunkSchedule.cpp:9-90
+* bindIndexed + the indexed host rows
+                         -- libreloc/src/Bind.cpp:701-819,
+                            libreloc/src/TypedExecute.cpp:741-790
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
 import it, and only as the checker; the product (sym_amd) never does.
@@ -1573,3 +1577,141 @@ DTYPE_TYPES = {
     "bfloat16": ElementType(KIND_BFLOAT, 16), "int8": ElementType(KIND_INT, 8),
     "int32": ElementType(KIND_INT, 32), "int64": ElementType(KIND_INT, 64),
 }
+
+
+# ---------------------------------------------------------------------------
+# Indexed plans (wire v2): index_select along axis 0, then at most one cast
+# ---------------------------------------------------------------------------
+
+@dataclass
+class IndexedPlan:
+    symbols: List[str]
+    source: TensorDesc
+    indices: TensorDesc
+    result: TensorDesc
+    axis: int
+    policy: int
+
+
+def validate_indexed_plan(p: IndexedPlan) -> Optional[str]:
+    """validateIndexedPlan, Decode.cpp:950-991."""
+    def const(e):
+        return e[0][1] if len(e) == 1 and e[0][0] == OP_PUSH_CONST else None
+
+    for d in (p.source, p.indices, p.result):
+        if not d.extents or d.strides or const(d.offset) != 0:
+            return "indexed plan requires dense zero-offset positive-rank descriptors"
+        for e in d.extents:
+            c = const(e)
+            if c is not None and c <= 0:
+                return "indexed plan extents must be positive"
+    it = p.indices.element_type
+    if p.axis != 0 or len(p.indices.extents) != 1 or it.kind != KIND_INT or \
+            it.bitwidth not in (32, 64):
+        return "indexed plan requires axis 0 and rank-one i32/i64 indices"
+    if len(p.source.extents) != len(p.result.extents):
+        return "indexed plan source/result rank mismatch"
+    for i, a in enumerate(p.result.extents):
+        b = p.indices.extents[0] if i == 0 else p.source.extents[i]
+        ca, cb = const(a), const(b)
+        if ca is not None and cb is not None and ca != cb:
+            return "indexed plan result extent mismatch"
+    a, b = p.source.element_type, p.result.element_type
+    supported = _isf(a, 32) or _isf(a, 16) or _isi8(a)
+    if (a.same(b) and supported and p.policy == P_EXACT) or \
+            (_isf(a, 32) and _isf(b, 16) and p.policy == P_IEEE_RNE) or \
+            (_isf(a, 16) and _isf(b, 32) and p.policy == P_EXACT):
+        return None
+    return "indexed plan has an unsupported type/policy pair"
+
+
+def decode_indexed_plan(data: bytes) -> IndexedPlan:
+    """decodeIndexedPlan, Decode.cpp:993-1012."""
+    r = _Reader(data)
+    symbols = _parse_header(r, 2)
+    n = len(symbols)
+    source = _parse_desc(r, n)
+    indices = _parse_desc(r, n)
+    result = _parse_desc(r, n)
+    axis = r.u32()
+    policy = r.u8()
+    if r.remaining():
+        r.fail(r.off, "trailing bytes after indexed plan")
+    p = IndexedPlan(symbols, source, indices, result, axis, policy)
+    why = validate_indexed_plan(p)
+    if why:
+        r.fail(r.off, why)
+    return p
+
+
+@dataclass
+class IndexedBoundPlan:
+    source_extents: List[int]  # the table
+    result_extents: List[int]
+    indices: List[int]
+    row_elements: int
+    source_type: ElementType
+    result_type: ElementType
+    policy: int
+    source_bytes: int          # selected rows, source type
+    destination_bytes: int
+    parameter_bytes: int       # index bytes
+
+
+def bind_indexed(plan: IndexedPlan, sym_map: Dict[str, int], index_dtype: ElementType,
+                 index_extents: Sequence[int], index_bytes: bytes) -> IndexedBoundPlan:
+    """bindIndexed, Bind.cpp:708-819 (error messages as there)."""
+    why = validate_indexed_plan(plan)
+    if why:
+        raise BindError(why)
+    syms = _resolve(plan.symbols, sym_map)
+    table = _dense_desc(plan.source, syms, "source")
+    ind = _dense_desc(plan.indices, syms, "indices")
+    result = _dense_desc(plan.result, syms, "result")
+    if list(index_extents) != ind or not index_dtype.same(plan.indices.element_type):
+        raise BindError("index operand dtype/extents do not match the plan")
+    selected = [ind[0]] + table[1:]
+    if selected != result:
+        raise BindError("indexed result shape does not match source and indices")
+    iw = index_dtype.width
+    ib = _mul_ok(ind[0], iw)
+    if ib is None or ib != len(index_bytes):
+        raise BindError("index operand byte size mismatch or overflow")
+    row = 1
+    for e in table[1:]:
+        row = _mul_ok(row, e)
+        if row is None:
+            raise BindError("indexed row size overflow")
+    sw, rw = plan.source.element_type.width, plan.result.element_type.width
+    sizes = []
+    for a, b in ((table[0], row), (ind[0], row)):
+        n = _mul_ok(a, b)
+        sizes.append(n)
+    ok = sizes[0] is not None and _mul_ok(sizes[0], sw) is not None and sizes[1] is not None \
+        and _mul_ok(sizes[1], sw) is not None and _mul_ok(sizes[1], rw) is not None
+    if not ok:
+        raise BindError("indexed tensor size overflow")
+    vals = [_sign_extend(int.from_bytes(index_bytes[i * iw:(i + 1) * iw], "little"),
+                         index_dtype.bitwidth) for i in range(ind[0])]
+    if any(v < 0 or v >= table[0] for v in vals):
+        raise BindError("index_out_of_range: index_select row is outside the source")
+    return IndexedBoundPlan(table, result, vals, row, plan.source.element_type,
+                            plan.result.element_type, plan.policy, sizes[1] * sw, sizes[1] * rw, ib)
+
+
+def execute_indexed(b: IndexedBoundPlan, table: np.ndarray) -> np.ndarray:
+    """The indexed branch of executeHost (TypedExecute.cpp:741-790): each
+    selected row copied, or cast element by element with the stage
+    arithmetic of applyStage. Returns the dense selected rows as bytes."""
+    sw, rw = b.source_type.width, b.result_type.width
+    raw = np.ascontiguousarray(table).view(np.uint8).reshape(-1)
+    rows = raw[:b.source_extents[0] * b.row_elements * sw].reshape(b.source_extents[0], -1)
+    sel = rows[np.asarray(b.indices, dtype=np.int64)]
+    if b.source_type.same(b.result_type):
+        return sel.reshape(-1).copy()
+    bits = sel.reshape(-1).view(_NP_BITS[sw])
+    if _isf(b.source_type, 32):
+        out = narrow_f32_f16_bits(bits).astype(np.uint16)
+    else:
+        out = widen_f16_f32_bits(bits).astype(np.uint32)
+    return out.view(np.uint8)

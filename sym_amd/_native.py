@@ -43,7 +43,10 @@ class relx_bound_info(ctypes.Structure):
                 ("result_rank", ctypes.c_int), ("result_extents", _I64R),
                 ("kernel", ctypes.c_char * 32), ("host_stages_max", ctypes.c_int),
                 ("host_stages_auto", ctypes.c_int),
-                ("wire_bytes_at", ctypes.c_int64 * (RELX_MAX_STAGES + 1))]
+                ("wire_bytes_at", ctypes.c_int64 * (RELX_MAX_STAGES + 1)),
+                ("indexed", ctypes.c_int), ("table_rows", ctypes.c_int64),
+                ("row_elements", ctypes.c_int64), ("table_bytes", ctypes.c_int64),
+                ("index_count", ctypes.c_int64)]
 
 
 class relx_ctx_stats(ctypes.Structure):
@@ -80,11 +83,15 @@ SIGNATURES = {
     "relx_wire_version": (_I, [ctypes.c_char_p, _SZ]),
     "relx_plan_load": (_I, [ctypes.c_char_p, _SZ, ctypes.POINTER(_VP), _E]),
     "relx_plan_is_typed": (_I, [_VP]),
+    "relx_plan_version": (_I, [_VP]),
     "relx_plan_symbol_count": (_I, [_VP]),
     "relx_plan_symbol": (ctypes.c_char_p, [_VP, _I]),
     "relx_plan_free": (None, [_VP]),
     "relx_bind": (_I, [_VP, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_I64), _I,
                        ctypes.POINTER(relx_param), _I, ctypes.POINTER(_VP), _E]),
+    "relx_bind_indexed": (_I, [_VP, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_I64), _I,
+                               _I, _I, ctypes.POINTER(_I64), _I, _VP, _SZ, ctypes.POINTER(_VP),
+                               _E]),
     "relx_bound_free": (None, [_VP]),
     "relx_bound_query": (_I, [_VP, ctypes.POINTER(relx_bound_info)]),
     "relx_ctx_create": (_I, [_I, _I64, ctypes.POINTER(_VP), _E]),
@@ -107,6 +114,7 @@ SIGNATURES = {
     "relx_completion_free": (None, [_VP]),
     "relx_execute_d2h": (_I, [_VP, _VP, _VP, _SZ, _VP, _SZ, ctypes.POINTER(relx_options),
                               ctypes.POINTER(relx_report), _E]),
+    "relx_index_select_device": (_I, [_VP, _VP, _VP, _SZ, _VP, _SZ, _U64, _E]),
     "relx_host_stage": (_I, [_VP, _I, _VP, _VP, _I, _E]),
     "relx_verify_launches": (_I, [_VP, _I, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64), _E]),
     "relx_ctx_synchronize": (_I, [_VP, _E]),

@@ -95,6 +95,10 @@ int relx_plan_load(const uint8_t *blob, size_t n, relx_plan **out, relx_err *err
 
 int relx_plan_is_typed(const relx_plan *plan) { return plan && plan->plan->version == 1; }
 
+int relx_plan_version(const relx_plan *plan) {
+  return plan ? static_cast<int>(plan->plan->version) : -1;
+}
+
 int relx_plan_symbol_count(const relx_plan *plan) {
   return plan ? static_cast<int>(plan->plan->symbols.size()) : 0;
 }
@@ -147,6 +151,35 @@ int relx_bind(const relx_plan *plan, const char *const *sym_names, const int64_t
   });
 }
 
+int relx_bind_indexed(const relx_plan *plan, const char *const *sym_names,
+                      const int64_t *sym_values, int nsym, int index_kind, int index_bits,
+                      const int64_t *index_extents, int index_rank, const void *index_data,
+                      size_t index_bytes, relx_bound **out, relx_err *err) {
+  return guarded(err, [&] {
+    if (!plan || !out)
+      throw relx::Error("invalid_argument", "null plan or output");
+    if (index_rank < 0 || (index_rank > 0 && !index_extents))
+      throw relx::Error("bind_error", "index operand extents are missing");
+    std::map<std::string, int64_t> syms;
+    for (int i = 0; i < nsym; ++i)
+      syms[sym_names[i]] = sym_values[i];
+    relx::DType t;
+    t.kind = static_cast<uint8_t>(index_kind);
+    t.bits = static_cast<uint32_t>(index_bits);
+    const std::vector<int64_t> ext(index_extents, index_extents + index_rank);
+    auto b = new relx_bound;
+    try {
+      b->h.bound = relx::bind_indexed(*plan->plan, syms, t, ext, index_data, index_bytes);
+      relx::prepare_stages(*b->h.bound, b->h.prep);
+      (void)b->h.program(0);
+    } catch (...) {
+      delete b;
+      throw;
+    }
+    *out = b;
+  });
+}
+
 void relx_bound_free(relx_bound *bound) { delete bound; }
 
 int relx_bound_query(const relx_bound *bound, relx_bound_info *out) {
@@ -190,6 +223,11 @@ int relx_bound_query(const relx_bound *bound, relx_bound_info *out) {
     ++out->host_stages_max;
   }
   out->host_stages_auto = static_cast<int>(relx::auto_host_stages(bound->h));
+  out->indexed = b.indexed ? 1 : 0;
+  out->table_rows = b.table_rows;
+  out->row_elements = b.row_elements;
+  out->table_bytes = b.table_bytes;
+  out->index_count = static_cast<int64_t>(b.indices.size());
   {
     int64_t elems = 1;
     for (int64_t e : b.source_extents)
@@ -436,6 +474,17 @@ int relx_relayout_device(relx_ctx *ctx, const relx_bound *bound, int wire_bounda
   });
 }
 
+int relx_index_select_device(relx_ctx *ctx, const relx_bound *bound, const void *table,
+                             size_t table_bytes, void *dst, size_t dst_bytes, uint64_t stream,
+                             relx_err *err) {
+  return guarded(err, [&] {
+    if (!ctx || !bound)
+      throw relx::Error("invalid_argument", "null argument");
+    relx::index_select_device(*ctx->ctx, const_cast<relx::BoundHandle &>(bound->h), table,
+                              table_bytes, dst, dst_bytes, reinterpret_cast<hipStream_t>(stream));
+  });
+}
+
 int relx_verify_launches(const relx_bound *bound, int wire_boundary, int64_t chunk_bytes,
                          int64_t *launches, relx_err *err) {
   return guarded(err, [&] {
@@ -471,6 +520,15 @@ int relx_host_stage(const relx_bound *bound, int host_stages, const void *src, v
     else
       n = const_cast<relx::BoundHandle &>(h).program(0).wire_elems;
     relx::Workers w(static_cast<unsigned>(threads > 0 ? threads : 1));
+    if (h.bound->indexed) {
+      const int64_t wout =
+          host_stages ? h.prep.stages[static_cast<size_t>(host_stages - 1)].out_width : sw;
+      w.parallel_for(n, int64_t{1} << 16, [&](int64_t a, int64_t b) {
+        relx::host_gather(*h.bound, h.prep, static_cast<uint32_t>(host_stages), src,
+                          static_cast<uint8_t *>(wire) + a * wout, a, b);
+      });
+      return;
+    }
     w.parallel_for(n, int64_t{1} << 16, [&](int64_t a, int64_t b) {
       relx::host_transform(h.prep, static_cast<uint32_t>(host_stages), sw, src, wire, a, b);
     });

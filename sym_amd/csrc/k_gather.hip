@@ -1,0 +1,166 @@
+// k_gather.hip - row gather kernels for indexed plans (index_select along
+// axis 0 of a device-resident table, with the plan's optional cast fused).
+//
+// Each lane moves one vector item (up to 16 bytes of a row) at a time, two
+// items 64 apart per trip, like the stream kernel: a wave covers 64
+// consecutive items of the output, which are consecutive items of one or a
+// few source rows, so loads and stores stay contiguous per row. The row index
+// of an item comes from one division by the row length in items; lanes of the
+// same row read the same index word. Output is written once and streamed past
+// the caches; table loads stay cached, since an index may repeat.
+#include "kernels.h"
+
+#ifndef RELX_GATHER_NT_LOAD
+#define RELX_GATHER_NT_LOAD false
+#endif
+#ifndef RELX_GATHER_NT_STORE
+#define RELX_GATHER_NT_STORE true
+#endif
+
+namespace relx {
+namespace {
+
+template <int NB, bool NT> __device__ __forceinline__ vec4 gload(const uint8_t *p) {
+  if constexpr (NB >= 4) {
+    return ld_n<NB, NT>(p);
+  } else {
+    vec4 r = {0u, 0u, 0u, 0u};
+    if constexpr (NB == 2)
+      r.x = *reinterpret_cast<const uint16_t *>(p);
+    else
+      r.x = *p;
+    return r;
+  }
+}
+
+template <int NB, bool NT> __device__ __forceinline__ void gstore(uint8_t *p, const vec4 &v) {
+  if constexpr (NB >= 4) {
+    st_n<NB, NT>(p, v);
+  } else if constexpr (NB == 2) {
+    *reinterpret_cast<uint16_t *>(p) = static_cast<uint16_t>(v.x);
+  } else {
+    *p = static_cast<uint8_t>(v.x);
+  }
+}
+
+constexpr int gather_out_bytes(int op, int nbi) {
+  return op == kGatherCopy ? nbi : op == kGatherF32F16 ? nbi / 2 : nbi * 2;
+}
+
+// One item's value conversion: NBI source bytes -> the item's output bytes.
+template <int OP, int NBI> __device__ __forceinline__ vec4 convert(const vec4 &in) {
+  if constexpr (OP == kGatherCopy) {
+    return in;
+  } else if constexpr (OP == kGatherF32F16) {
+    constexpr int V = NBI / 4;
+    uint32_t w[2] = {0u, 0u};
+#pragma unroll
+    for (int e = 0; e < V; ++e)
+      w[e >> 1] |= op_f32_f16(in[e]) << ((e & 1) * 16);
+    return vec4{w[0], w[1], 0u, 0u};
+  } else {
+    constexpr int V = NBI / 2;
+    vec4 out = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int e = 0; e < V; ++e)
+      out[e] = op_f16_f32((in[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
+    return out;
+  }
+}
+
+template <int OP, int NBI, int IW>
+__global__ __launch_bounds__(kBlock) void k_gather(GatherArgs a) {
+  constexpr int NBO = gather_out_bytes(OP, NBI);
+  constexpr int U = 2;
+  constexpr bool NTL = RELX_GATHER_NT_LOAD, NTS = RELX_GATHER_NT_STORE;
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = (blockIdx.x * kBlock + threadIdx.x) >> 6;
+  const uint32_t stride = gridDim.x * (kBlock / 64) * (64 * U);
+  for (uint32_t base = wave * (64 * U) + lane; base < a.work; base += stride) {
+    vec4 in[U];
+    bool live[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t i = base + 64u * u;
+      live[u] = u == 0 || i < a.work;
+      if (live[u]) {
+        const uint32_t r = fdiv(i, a.per_row);
+        const uint32_t c = i - r * a.row_items;
+        int64_t row;
+        if constexpr (IW == 4)
+          row = reinterpret_cast<const int32_t *>(a.idx)[r];
+        else
+          row = reinterpret_cast<const int64_t *>(a.idx)[r];
+        const uint64_t item = static_cast<uint64_t>(row) * a.row_items + c;
+        in[u] = gload<NBI, NTL>(a.table + item * NBI);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (!live[u])
+        break;
+      const uint32_t i = base + 64u * u;
+      gstore<NBO, NTS>(a.dst + static_cast<uint64_t>(i) * NBO, convert<OP, NBI>(in[u]));
+    }
+  }
+}
+
+template <int OP, int NBI>
+hipError_t gather_iw(const GatherArgs &a, int iw, hipStream_t s) {
+  const dim3 grid(grid_for((static_cast<int64_t>(a.work) + 1) / 2)), block(kBlock);
+  if (iw == 4)
+    hipLaunchKernelGGL((k_gather<OP, NBI, 4>), grid, block, 0, s, a);
+  else if (iw == 8)
+    hipLaunchKernelGGL((k_gather<OP, NBI, 8>), grid, block, 0, s, a);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+} // namespace
+
+// Launch one gather: `op` a GatherOp, `nbi` source bytes per item (copy 1, 2,
+// 4, 8 or 16; f32 -> f16 4, 8 or 16; f16 -> f32 2, 4 or 8), `iw` index bytes.
+hipError_t gather_launch(const GatherArgs &a, int op, int nbi, int iw, hipStream_t s) {
+  if (a.work == 0)
+    return hipSuccess;
+  switch (op) {
+  case kGatherCopy:
+    switch (nbi) {
+    case 1:
+      return gather_iw<kGatherCopy, 1>(a, iw, s);
+    case 2:
+      return gather_iw<kGatherCopy, 2>(a, iw, s);
+    case 4:
+      return gather_iw<kGatherCopy, 4>(a, iw, s);
+    case 8:
+      return gather_iw<kGatherCopy, 8>(a, iw, s);
+    case 16:
+      return gather_iw<kGatherCopy, 16>(a, iw, s);
+    }
+    break;
+  case kGatherF32F16:
+    switch (nbi) {
+    case 4:
+      return gather_iw<kGatherF32F16, 4>(a, iw, s);
+    case 8:
+      return gather_iw<kGatherF32F16, 8>(a, iw, s);
+    case 16:
+      return gather_iw<kGatherF32F16, 16>(a, iw, s);
+    }
+    break;
+  case kGatherF16F32:
+    switch (nbi) {
+    case 2:
+      return gather_iw<kGatherF16F32, 2>(a, iw, s);
+    case 4:
+      return gather_iw<kGatherF16F32, 4>(a, iw, s);
+    case 8:
+      return gather_iw<kGatherF16F32, 8>(a, iw, s);
+    }
+    break;
+  }
+  return hipErrorInvalidValue;
+}
+
+} // namespace relx

@@ -258,7 +258,7 @@ std::vector<std::string> read_header(Cursor &c, const uint8_t *data, uint32_t &v
   c.u32();
   const size_t at = c.pos();
   version = c.u32();
-  if (version > 1)
+  if (version > 2)
     c.reject(at, "unsupported wire format version");
   std::vector<std::string> syms;
   const uint32_t ns = c.count("symbol table count");
@@ -673,6 +673,21 @@ std::unique_ptr<Plan> decode(const uint8_t *data, size_t n) {
       c.reject(c.pos(), "trailing bytes after inverse section");
     return p;
   }
+  if (p->version == 2) {
+    // docs/reloc-plan-format.md:287-345: source, indices and result
+    // descriptors, u32 axis, u8 numeric policy; nothing after.
+    p->source = read_desc(c, nsym);
+    p->indices = read_desc(c, nsym);
+    p->result = read_desc(c, nsym);
+    p->axis = c.u32();
+    p->policy = c.u8();
+    if (c.left())
+      c.reject(c.pos(), "trailing bytes after indexed plan");
+    const std::string why = validate_indexed(*p);
+    if (!why.empty())
+      c.reject(c.pos(), why);
+    return p;
+  }
   p->source = read_desc(c, nsym);
   p->result = read_desc(c, nsym);
   const size_t layout_at = c.pos();
@@ -700,6 +715,37 @@ std::unique_ptr<Plan> decode(const uint8_t *data, size_t n) {
     c.reject(c.pos(), "trailing bytes after fills section");
   validate_typed(c, *p, layout_at, stages_at, stage_at, fills_at, fill_at);
   return p;
+}
+
+std::string validate_indexed(const Plan &p) {
+  auto is_const = [](const Expr &e) { return e.size() == 1 && e[0].op == kPushConst; };
+  for (const TensorDesc *d : {&p.source, &p.indices, &p.result}) {
+    if (d->extents.empty() || !d->strides.empty() || !is_const(d->offset) ||
+        d->offset[0].value != 0)
+      return "indexed plan requires dense zero-offset positive-rank descriptors";
+    for (const Expr &e : d->extents)
+      if (is_const(e) && e[0].value <= 0)
+        return "indexed plan extents must be positive";
+  }
+  if (p.axis != 0 || p.indices.extents.size() != 1 || p.indices.type.kind != kInteger ||
+      (p.indices.type.bits != 32 && p.indices.type.bits != 64))
+    return "indexed plan requires axis 0 and rank-one i32/i64 indices";
+  if (p.source.extents.size() != p.result.extents.size())
+    return "indexed plan source/result rank mismatch";
+  // Constant extents must already agree: result[0] with the index count,
+  // result[i] with source[i] for i > 0.
+  for (size_t i = 0; i < p.result.extents.size(); ++i) {
+    const Expr &a = p.result.extents[i];
+    const Expr &b = i == 0 ? p.indices.extents[0] : p.source.extents[i];
+    if (is_const(a) && is_const(b) && a[0].value != b[0].value)
+      return "indexed plan result extent mismatch";
+  }
+  const DType a = p.source.type, b = p.result.type;
+  const bool supported = a.f32() || a.f16() || a.i8();
+  if ((a == b && supported && p.policy == kExact) ||
+      (a.f32() && b.f16() && p.policy == kIeeeRne) || (a.f16() && b.f32() && p.policy == kExact))
+    return std::string();
+  return "indexed plan has an unsupported type/policy pair";
 }
 
 // ------------------------------------------------------------- evaluation
@@ -960,6 +1006,8 @@ void check_values(const BoundParam &p, bool is_scale, uint8_t policy) {
 
 std::unique_ptr<Bound> bind(const Plan &plan, const std::map<std::string, int64_t> &symbols,
                             const std::map<std::string, ParamValue> &params) {
+  if (plan.version == 2)
+    fail("bind_error", "indexed (wire v2) plans bind with their index operand");
   auto out = std::make_unique<Bound>();
   out->symbols = resolve(plan.symbols, symbols);
   if (plan.version == 0) {
@@ -1111,6 +1159,94 @@ std::unique_ptr<Bound> bind(const Plan &plan, const std::map<std::string, int64_
       if (res != n)
         fail("bind_error", "result descriptor element count disagrees with the layout");
     }
+  }
+  return out;
+}
+
+std::unique_ptr<Bound> bind_indexed(const Plan &plan,
+                                    const std::map<std::string, int64_t> &symbols,
+                                    DType index_type, const std::vector<int64_t> &index_extents,
+                                    const void *index_data, size_t index_bytes) {
+  if (plan.version != 2)
+    fail("bind_error", "bind_indexed needs an indexed (wire v2) plan");
+  {
+    const std::string why = validate_indexed(plan);
+    if (!why.empty())
+      fail("bind_error", why);
+  }
+  auto out = std::make_unique<Bound>();
+  out->symbols = resolve(plan.symbols, symbols);
+  const auto &syms = out->symbols;
+  out->table_extents = dense_extents(plan.source, syms, "source");
+  const std::vector<int64_t> ind = dense_extents(plan.indices, syms, "indices");
+  out->result_extents = dense_extents(plan.result, syms, "result");
+  if (index_extents != ind || index_type != plan.indices.type)
+    fail("bind_error", "index operand dtype/extents do not match the plan");
+  std::vector<int64_t> selected = out->table_extents;
+  selected[0] = ind[0];
+  if (selected != out->result_extents)
+    fail("bind_error", "indexed result shape does not match source and indices");
+  const int64_t count = ind[0];
+  const uint32_t iw = index_type.width();
+  int64_t ibytes;
+  if (!mul_ok(count, static_cast<int64_t>(iw), ibytes) ||
+      static_cast<uint64_t>(ibytes) != index_bytes)
+    fail("bind_error", "index operand byte size mismatch or overflow");
+  int64_t row = 1;
+  for (size_t i = 1; i < out->table_extents.size(); ++i)
+    if (!mul_ok(row, out->table_extents[i], row))
+      fail("bind_error", "indexed row size overflow");
+  out->source_type = plan.source.type;
+  out->result_type = plan.result.type;
+  const int64_t sw = out->source_type.width(), rw = out->result_type.width();
+  const int64_t rows = out->table_extents[0];
+  int64_t table_elems, elems;
+  if (!mul_ok(rows, row, table_elems) || !mul_ok(table_elems, sw, out->table_bytes) ||
+      !mul_ok(count, row, elems) || !mul_ok(elems, sw, out->source_bytes) ||
+      !mul_ok(elems, rw, out->destination_bytes))
+    fail("bind_error", "indexed tensor size overflow");
+  // Snapshot the index values (little-endian, sign-extended) and check them.
+  const uint8_t *raw = static_cast<const uint8_t *>(index_data);
+  if (count && !raw)
+    fail("bind_error", "index operand bytes are missing");
+  out->indices.resize(static_cast<size_t>(count));
+  bool in_range = true;
+  for (int64_t i = 0; i < count; ++i) {
+    uint64_t bits = 0;
+    std::memcpy(&bits, raw + i * iw, iw);
+    const int64_t v = sign_extend(bits, index_type.bits);
+    out->indices[static_cast<size_t>(i)] = v;
+    in_range &= v >= 0 && v < rows;
+  }
+  if (!in_range)
+    fail("bind_error", "index_out_of_range: index_select row is outside the source");
+  out->indexed = true;
+  out->typed = true;
+  out->index_type = index_type;
+  out->table_rows = rows;
+  out->row_elements = row;
+  out->parameter_bytes = ibytes;
+  out->source_extents = selected;
+  // The selected rows relocate by identity: one coalesced axis of every
+  // selected element, dense on both sides.
+  BoundLayout &L = out->layout;
+  L.extents = {elems};
+  L.src_strides = {1};
+  L.dst_strides = {1};
+  L.perm = {0};
+  L.element_size = static_cast<uint32_t>(rw);
+  L.total_bytes = out->destination_bytes;
+  L.inner_run = elems;
+  out->bytes_at.push_back(out->source_bytes);
+  if (out->source_type != out->result_type) {
+    BoundStage st;
+    st.transform = kCast;
+    st.policy = plan.policy;
+    st.in = out->source_type;
+    st.out = out->result_type;
+    st.shape = selected;
+    out->stages.push_back(std::move(st));
+    out->bytes_at.push_back(out->destination_bytes);
   }
   return out;
 }

@@ -2,7 +2,9 @@
 //
 // Semantics follow the reference runtime so results are interchangeable:
 //   wire format v0/v1   docs/reloc-plan-format.md; libreloc/src/Decode.cpp
+//   wire format v2      docs/reloc-plan-format.md:287-345; Decode.cpp:950-1012
 //   evaluation/binding  libreloc/src/Bind.cpp:84-699
+//   indexed binding     libreloc/src/Bind.cpp:701-819
 // The representation is this library's own: plans are decoded into flat
 // structs with expression streams kept as postfix token vectors, and every
 // failure is a relx::Error carrying a stable code.
@@ -119,19 +121,27 @@ struct PlanFill {
 };
 
 struct Plan {
-  uint32_t version = 0; // 0 layout, 1 typed
+  uint32_t version = 0; // 0 layout, 1 typed, 2 indexed
   std::vector<std::string> symbols;
   LayoutPlan layout;
-  // typed (v1) only
+  // typed (v1) and indexed (v2)
   TensorDesc source, result;
   std::vector<PlanStage> stages;
   std::vector<PlanFill> fills;
+  // indexed (v2) only: rows `indices` of `source` along `axis` (always 0),
+  // cast to the result type under `policy`
+  TensorDesc indices;
+  uint32_t axis = 0;
+  uint8_t policy = kExact;
 };
 
 // Wire version of an "RPLN" blob, -1 otherwise.
 int peek_wire_version(const uint8_t *data, size_t n);
-// Decode v0 or v1 (by header). Throws Error{"decode_error", msg, offset}.
+// Decode v0, v1 or v2 (by header). Throws Error{"decode_error", msg, offset}.
 std::unique_ptr<Plan> decode(const uint8_t *data, size_t n);
+// The indexed-plan invariants (reference validateIndexedPlan,
+// libreloc/src/Decode.cpp:950-991); empty when the plan is valid.
+std::string validate_indexed(const Plan &p);
 
 // Scalar stage arithmetic on bit patterns (docs/reloc-typed-semantics.md).
 uint16_t f32_to_f16_bits(uint32_t f);
@@ -205,10 +215,25 @@ struct Bound {
   std::vector<PlanFill> fills;
   std::vector<int64_t> bytes_at; // dense footprint per stage boundary
   int64_t source_bytes = 0, destination_bytes = 0, parameter_bytes = 0;
+  // indexed (v2): the typed fields above describe the selected rows (an
+  // identity layout over [count, row_elements] plus at most one cast); the
+  // physical source is `table_rows` rows of `row_elements` elements.
+  bool indexed = false;
+  std::vector<int64_t> table_extents;
+  std::vector<int64_t> indices; // one per selected row, each in [0, table_rows)
+  int64_t table_rows = 0, row_elements = 0, table_bytes = 0;
+  DType index_type;
 };
 
 // bind (v0) / bindTyped (v1). Throws Error{"bind_error", ...}.
 std::unique_ptr<Bound> bind(const Plan &plan, const std::map<std::string, int64_t> &symbols,
                             const std::map<std::string, ParamValue> &params);
+
+// bindIndexed (v2): symbols plus the index operand (element type, extents,
+// little-endian bytes), whose values are copied and range-checked.
+std::unique_ptr<Bound> bind_indexed(const Plan &plan,
+                                    const std::map<std::string, int64_t> &symbols,
+                                    DType index_type, const std::vector<int64_t> &index_extents,
+                                    const void *index_data, size_t index_bytes);
 
 } // namespace relx

@@ -18,8 +18,6 @@
 
 namespace relx {
 
-namespace {
-
 FastDiv make_div(int64_t d64) {
   FastDiv f{};
   const uint32_t d = static_cast<uint32_t>(d64 < 1 ? 1 : d64);
@@ -34,6 +32,8 @@ FastDiv make_div(int64_t d64) {
   f.m = static_cast<uint32_t>(num / d + 1);
   return f;
 }
+
+namespace {
 
 uint8_t op_of(const BoundStage &s) {
   if (s.transform == kCast) {

@@ -193,4 +193,24 @@ struct KArgs {
   int64_t re[kMaxRank];
 };
 
+// Row gather of an indexed plan (index_select along axis 0, at most one cast):
+// a launch covers `work` vector items of consecutive selected rows, each row
+// `row_items` items; item i belongs to selected row r = i / row_items and
+// reads item i - r * row_items of table row idx[r]. The host splits launches
+// so that `work` < 2^31 and offsets `dst` and `idx` to the launch's first row.
+enum GatherOp : int32_t {
+  kGatherCopy = 0,   // same element type (bit copy)
+  kGatherF32F16 = 1, // cast f32 -> f16, ieee_rne
+  kGatherF16F32 = 2, // cast f16 -> f32, exact
+};
+
+struct GatherArgs {
+  const uint8_t *table;
+  uint8_t *dst;
+  const void *idx; // int32 or int64 row indices
+  uint32_t work;
+  uint32_t row_items;
+  FastDiv per_row; // division by row_items
+};
+
 } // namespace relx

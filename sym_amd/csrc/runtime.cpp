@@ -183,6 +183,10 @@ BoundHandle::~BoundHandle() {
     if (cur != kv.first.first)
       (void)hipSetDevice(cur);
   }
+  for (auto &kv : dev_indices) {
+    DeviceScope scope(kv.first);
+    (void)hipFree(kv.second);
+  }
 }
 
 } // namespace relx
@@ -318,7 +322,10 @@ void execute_members(Context &ctx, int n, BoundHandle *const *bounds, const void
     Member m{h, static_cast<const uint8_t *>(srcs[i]), src_bytes[i],
              static_cast<uint8_t *>(dsts[i]), dst_bytes[i], reports ? &reports[i] : nullptr, 0,
              nullptr, false, 0};
-    const bool pinned = opt.source_pinned > 0 || (opt.source_pinned < 0 && probe_pinned(m.src));
+    const bool indexed = h->bound->indexed;
+    // An indexed plan's rows are scattered over the table: always staged.
+    const bool pinned = !indexed && (opt.source_pinned > 0 ||
+                                     (opt.source_pinned < 0 && probe_pinned(m.src)));
     const uint32_t nst = static_cast<uint32_t>(h->prep.stages.size());
     if (hs < 0)
       m.k = pinned ? 0 : auto_host_stages(*h);
@@ -330,8 +337,9 @@ void execute_members(Context &ctx, int n, BoundHandle *const *bounds, const void
     m.dp = &h->program(m.k);
     m.direct = pinned && m.k == 0;
     const Bound &b = *h->bound;
-    const int64_t need_src = b.typed ? b.source_bytes
-                                     : m.dp->wire_elems * static_cast<int64_t>(b.layout.element_size);
+    const int64_t need_src = indexed ? b.table_bytes
+                             : b.typed ? b.source_bytes
+                                       : m.dp->wire_elems * static_cast<int64_t>(b.layout.element_size);
     if (static_cast<int64_t>(m.src_bytes) < need_src)
       throw Error("insufficient_capacity", "source holds " + std::to_string(m.src_bytes) +
                                                " bytes, the plan reads " + std::to_string(need_src));
@@ -413,10 +421,18 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
         const uint8_t *src_base = m.src + e0 * sw;
         const uint32_t k = m.k;
         const Prepared &prep = m.h->prep;
+        const Bound &bd = *m.h->bound;
         // each worker converts a contiguous element range into the slot
-        ctx.workers->parallel_for(ne, int64_t{1} << 16, [&](int64_t a, int64_t b) {
-          host_transform(prep, k, sw, src_base, s, a, b);
-        });
+        if (bd.indexed) {
+          const int64_t wout = dp.base.win; // wire element bytes at boundary k
+          ctx.workers->parallel_for(ne, int64_t{1} << 16, [&](int64_t a, int64_t b) {
+            host_gather(bd, prep, k, m.src, s + a * wout, e0 + a, e0 + b);
+          });
+        } else {
+          ctx.workers->parallel_for(ne, int64_t{1} << 16, [&](int64_t a, int64_t b) {
+            host_transform(prep, k, sw, src_base, s, a, b);
+          });
+        }
         HIPCHECK(hipMemcpyAsync(wire + woff, s, static_cast<size_t>(wbytes),
                                 hipMemcpyHostToDevice, ctx.copy));
         HIPCHECK(hipEventRecord(ctx.slot_ev[static_cast<size_t>(slot)], ctx.copy));
@@ -437,7 +453,7 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
           m.k == 0 ? std::string("hip_relayout") : "hip_relayout@" + std::to_string(m.k);
       std::snprintf(r.implementation, sizeof(r.implementation), "%s", impl.c_str());
       const Bound &b = *m.h->bound;
-      r.source_bytes = b.typed ? b.source_bytes : dp.wire_elems * sw;
+      r.source_bytes = b.indexed ? b.table_bytes : b.typed ? b.source_bytes : dp.wire_elems * sw;
       r.wire_bytes = dp.wire_bytes;
       r.destination_bytes = dp.dst_elems * dp.base.wout;
       r.parameter_bytes = b.parameter_bytes;
@@ -542,6 +558,8 @@ D2hPlan d2h_plan(const DeviceProgram &dp, int64_t chunk_bytes) {
 void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes, void *dst,
                  size_t dst_bytes, const relx_options &opt, relx_report *report) {
   DeviceGuard guard(ctx.device);
+  if (h.bound->indexed) // libreloc/src/Dispatch.cpp:196-201: indexed sources are host rows
+    throw Error("plan_mismatch", "indexed source requires the prepared host row shape");
   const DeviceProgram &dp = h.program(0);
   const Bound &b = *h.bound;
   if (!src || !dst)
@@ -760,6 +778,24 @@ int64_t verify_launches(BoundHandle &h, uint32_t k, int64_t chunk_bytes) {
       verify_launch(dp, a);
       ++n;
     }
+  if (h.bound->indexed) {
+    // The device gather, at the natural alignment and one element off it
+    // (addresses only: nothing is dereferenced).
+    const Bound &b = *h.bound;
+    const uint32_t sw = b.source_type.width(), rw = b.result_type.width();
+    uint8_t *const base = reinterpret_cast<uint8_t *>(uintptr_t{1} << 20);
+    const void *idx = base;
+    for (int shift = 0; shift < 2; ++shift) {
+      const uint8_t *table = base + (uintptr_t{1} << 44) + shift * sw;
+      uint8_t *dst = base + (uintptr_t{1} << 45) + shift * rw;
+      const GatherPlan g = gather_plan(b, table, dst);
+      const std::vector<GatherArgs> ls = gather_launches(b, g, table, dst, idx);
+      verify_gather(b, g, ls, table, static_cast<size_t>(b.table_bytes), dst,
+                    static_cast<size_t>(b.destination_bytes), idx);
+      n += static_cast<int64_t>(ls.size());
+    }
+    return n;
+  }
   if (k == 0) { // the device-to-host schedule (axis < 0: one whole launch)
     const D2hPlan d = d2h_plan(dp, chunk_bytes);
     int64_t fixed[kMaxRank] = {};

@@ -70,6 +70,8 @@ struct DeviceProgram {
   std::vector<int32_t> pi;
 };
 
+// Division by a runtime constant d >= 1 for 32-bit numerators (FastDiv).
+FastDiv make_div(int64_t d);
 void prepare_stages(const Bound &b, Prepared &p);
 bool fill_at(const Bound &b, const Prepared &p, uint32_t to, uint64_t &bits);
 uint64_t host_apply(const HostStage &s, uint64_t x, int64_t c);
@@ -146,10 +148,39 @@ struct BoundHandle {
     int32_t *pi = nullptr;
   };
   std::map<std::pair<int, uint32_t>, DevParams> params; // (device, boundary)
+  std::map<int, void *> dev_indices;                     // indexed plans, per device
   const DeviceProgram &program(uint32_t k);
   DevParams device_params(int device, uint32_t k);
+  // The bound row indices in device memory (int32 when the table has fewer
+  // than 2^31 rows, else int64), uploaded once per device.
+  const void *device_indices(int device);
   ~BoundHandle();
 };
+
+// ------------------------------------------------------------ indexed plans
+
+// Vector shape of a device row gather for one table/destination alignment.
+struct GatherPlan {
+  int op = kGatherCopy;
+  int nbi = 1, nbo = 1; // source / destination bytes per item
+  int iw = 4;           // index bytes
+  int64_t row_items = 1;
+};
+GatherPlan gather_plan(const Bound &b, const void *table, const void *dst);
+// Launches over every selected row; `idx` holds the device indices.
+std::vector<GatherArgs> gather_launches(const Bound &b, const GatherPlan &g, const void *table,
+                                        void *dst, const void *idx);
+// Host-side check that every gather launch stays inside the table (of
+// `table_bytes`), the destination (of `dst_bytes`) and the index array.
+void verify_gather(const Bound &b, const GatherPlan &g, const std::vector<GatherArgs> &launches,
+                   const void *table, size_t table_bytes, const void *dst, size_t dst_bytes,
+                   const void *idx);
+hipError_t gather_launch(const GatherArgs &a, int op, int nbi, int iw, hipStream_t s);
+// Host staging of an indexed plan: selected elements [g0, g1) (dense
+// selected-row order) gathered from the table through stages [0, k) into
+// `dst`, which receives element g0 first.
+void host_gather(const Bound &b, const Prepared &p, uint32_t k, const void *table, void *dst,
+                 int64_t g0, int64_t g1);
 
 // Device-to-host chunk schedule: for each of the `outer` coordinate tuples of
 // the destination axes before `axis`, ranges of `per` coordinates of `axis`
@@ -167,6 +198,11 @@ struct Context;
 // Device-resident source -> host destination (see runtime.cpp).
 void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes, void *dst,
                  size_t dst_bytes, const relx_options &opt, relx_report *report);
+
+// Device-resident table -> device destination: the row gather with the
+// plan's cast fused, asynchronous on `stream`.
+void index_select_device(Context &ctx, BoundHandle &h, const void *table, size_t table_bytes,
+                         void *dst, size_t dst_bytes, hipStream_t stream);
 
 // Leading per-tensor narrowing stages applied on the host for a pageable
 // source (halving PCIe bytes where a cast narrows).

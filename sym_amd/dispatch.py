@@ -14,6 +14,12 @@ The device-to-host direction has one row, `hip_relayout`: the device runs
 the relayout and every stage and the result crosses PCIe (the reference's
 cuda_stages_then_cpu rows with every stage on the device).
 
+Indexed (wire v2) plans go through `prepare_index_select_program(bound,
+source_view)` (reference prepareIndexSelect, libreloc/src/Dispatch.cpp:
+1269-1283): the source view is the whole host table; the host gathers the
+selected rows while staging and the device runs the rest. They have no
+device-to-host row.
+
 Names, argument meaning and error codes follow the reference so that
 `reloc_torch.dispatch` can call these functions in place of `_pyreloc`'s.
 Requests whose policy asks for a CPU executor ("original_cpu") or a forced
@@ -85,9 +91,49 @@ def _row(bound, k):
             "wire_bytes": wire, "device_temp_bytes": wire, "method": "device_relayout"}
 
 
+class IndexSelectProgram:
+    """A bound indexed plan checked against its host table view (reference
+    prepareIndexSelect's Program, libreloc/src/Dispatch.cpp:1269-1283)."""
+
+    def __init__(self, bound, source):
+        self.bound = bound
+        self.source = source
+
+
+def _check_table_view(bound, view):
+    """The source-view checks of checkView for an indexed program
+    (libreloc/src/Dispatch.cpp:161-201)."""
+    if view.kind == "cuda":
+        raise TransferError("direction_mismatch", "host-to-device source must be host memory")
+    if view.span_bytes() > view.capacity_bytes:
+        raise TransferError("insufficient_capacity", "source view reaches %d bytes of %d"
+                            % (view.span_bytes(), view.capacity_bytes))
+    if view.element_size != bound.info.source_width:
+        raise TransferError("plan_mismatch", "source element size differs from the typed "
+                            "program's source type")
+    if not view.is_dense():
+        raise TransferError("unsupported_layout", "source view must be dense row-major")
+    if view.extents != bound.source_extents:
+        raise TransferError("plan_mismatch", "indexed source requires the prepared host row shape")
+
+
+def prepare_index_select_program(bound, source):
+    """Check a bound indexed plan against its host table view (reference
+    prepare_index_select_program, libreloc/python/PyDispatch.cpp:518-528)."""
+    if not isinstance(bound, P.IndexedBound):
+        raise TypeError("prepare_index_select_program needs a bound indexed plan")
+    _check_table_view(bound, source)
+    return IndexSelectProgram(bound, source)
+
+
+def _unwrap(plan):
+    return plan.bound if isinstance(plan, IndexSelectProgram) else plan
+
+
 def query_capability(bound, direction, device):
     """Eligible and excluded rows (reference query_capability,
     libreloc/src/Dispatch.cpp:1382-1532)."""
+    bound = _unwrap(bound)
     if device not in ("host", "cuda"):
         raise ValueError("device must be 'host' or 'cuda', got '%s'" % device)
     if direction not in ("h2d", "d2h"):
@@ -97,6 +143,10 @@ def query_capability(bound, direction, device):
     if device == "host":
         return {"eligible": [], "excluded": [{"implementation": "hip_relayout",
                                               "reason": "host_destination"}]}
+    if direction == "d2h" and bound.indexed:
+        # indexed sources are host rows (libreloc/src/Dispatch.cpp:1397-1404)
+        return {"eligible": [], "excluded": [{"implementation": "hip_relayout",
+                                              "reason": "host_index_select"}]}
     if direction == "d2h":
         out = bound.destination_bytes
         return {"eligible": [{"implementation": "hip_relayout", "wire_boundary": bound.stage_count,
@@ -144,6 +194,9 @@ def _select(bound, direction, capability, policy, implementation):
         raise TransferError("implementation_unavailable",
                             "no CPU executor row: every plan runs on the device")
     labels = [r["implementation"] for r in capability["eligible"]]
+    if not labels:
+        raise TransferError("implementation_unavailable", "no eligible row (%s)" % ", ".join(
+            "%s: %s" % (r["implementation"], r["reason"]) for r in capability["excluded"]))
     if implementation:
         if implementation not in labels:
             raise TransferError("implementation_unavailable",
@@ -165,6 +218,7 @@ def prepare_dispatch_template(bound, direction, device="cuda", *, policy="auto",
     and launches nothing (reference prepare_dispatch_template)."""
     if int(threads) < 1:
         raise ValueError("threads must be >= 1")
+    bound = _unwrap(bound)
     capability = query_capability(bound, direction, device)
     selection = _select(bound, direction, capability, policy, implementation)
     return DispatchTemplate(bound, direction, capability, selection, int(threads))
@@ -176,8 +230,11 @@ def _check_views(bound, source, destination, direction):
     if (source.kind, destination.kind) != want:
         raise TransferError("direction_mismatch", "%s moves %s -> %s, got %s -> %s"
                             % (direction, want[0], want[1], source.kind, destination.kind))
+    if bound.indexed:
+        _check_table_view(bound, source)
     for name, view, extents, width in (
-            ("source", source, list(info.source_extents[:info.source_rank]), info.source_width),
+            ("source", source, bound.source_extents if bound.indexed else
+             list(info.source_extents[:info.source_rank]), info.source_width),
             ("destination", destination, list(info.result_extents[:info.result_rank]),
              info.result_width)):
         if view.extents != extents or view.element_size != width:
@@ -238,9 +295,11 @@ def _report(rep, request):
             "wire_bytes": rep["wire_bytes"], "destination_bytes": rep["destination_bytes"],
             "parameter_bytes": rep["parameter_bytes"],
             "payload_bytes_transferred": rep["payload_bytes_transferred"],
-            "device_temp_bytes": rep["wire_bytes"], "artifact_version": 1, "executed": True,
+            "device_temp_bytes": rep["wire_bytes"],
+            "artifact_version": 2 if request.template.bound.indexed else 1, "executed": True,
             "host_pipeline": "pinned_ring" if not rep["direct_dma"] else "direct_dma",
-            "host_kernel": "host_stages" if rep["wire_boundary"] else "copy",
+            "host_kernel": "index_select" if request.template.bound.indexed else
+            "host_stages" if rep["wire_boundary"] else "copy",
             "host_chunks": rep["chunks"], "host_chunk_bytes": 0, "host_buffers": 0,
             "kernel_launches": rep["kernel_launches"], "staging": []}
 

@@ -1,4 +1,5 @@
-"""Recipe -> relocation plan encoder (wire v0 layout, wire v1 typed).
+"""Recipe -> relocation plan encoder (wire v0 layout, wire v1 typed, wire v2
+indexed).
 
 The reference produces plans with its MLIR exporter (`sym-reloc-export`,
 sym/dialect/reloc/Transforms/PlanBuilder.h:27-172 and
@@ -560,8 +561,12 @@ def _fold(bits: int, st: _Stage) -> int:
 # ------------------------------------------------------------- finalise
 
 class _Writer:
-    def __init__(self):
+    """Little-endian wire writer; expressions name symbols by their index in
+    `symbols` (docs/reloc-plan-format.md:74-97)."""
+
+    def __init__(self, symbols=None):
         self.out = bytearray()
+        self.symbols = symbols if symbols is not None else []
 
     def u8(self, v):
         self.out += struct.pack("<B", v)
@@ -579,6 +584,43 @@ class _Writer:
         b = s.encode()
         self.u32(len(b))
         self.out += b
+
+    def expr(self, e: E):
+        ops = []
+
+        def emit(x):
+            if x.kind == "const":
+                ops.append((PUSH_CONST, x.value))
+            elif x.kind == "sym":
+                ops.append((PUSH_SYM, self.symbols.index(x.value)))
+            elif x.kind == "dim":
+                ops.append((PUSH_DIM, x.value))
+            else:
+                emit(x.a)
+                emit(x.b)
+                ops.append(({"add": ADD, "sub": SUB, "mul": MUL, "floordiv": FLOORDIV,
+                             "mod": MOD}[x.kind], None))
+        emit(e)
+        self.u32(len(ops))
+        for op, v in ops:
+            self.u8(op)
+            if op == PUSH_CONST:
+                self.i64(v)
+            elif op in (PUSH_SYM, PUSH_DIM):
+                self.u32(v)
+
+    def dtype(self, dt):
+        kind, bits = DTYPES[dt]
+        self.u8(kind)
+        self.u32(bits)
+
+    def desc(self, shape, dt):
+        self.u32(len(shape))
+        for e in shape:
+            self.expr(e)
+        self.u32(0)  # canonical row-major strides
+        self.expr(E.c(0))
+        self.dtype(dt)
 
 
 def _finalize(source_shape, source_dtype, axes, pads, stages, divisibility, dtype, result_shape,
@@ -625,44 +667,7 @@ def _finalize(source_shape, source_dtype, axes, pads, stages, divisibility, dtyp
             note(e.a)
             note(e.b)
 
-    w = _Writer()
-
-    def put_expr(e: E):
-        ops = []
-
-        def emit(x):
-            if x.kind == "const":
-                ops.append((PUSH_CONST, x.value))
-            elif x.kind == "sym":
-                ops.append((PUSH_SYM, symbols.index(x.value)))
-            elif x.kind == "dim":
-                ops.append((PUSH_DIM, x.value))
-            else:
-                emit(x.a)
-                emit(x.b)
-                ops.append(({"add": ADD, "sub": SUB, "mul": MUL, "floordiv": FLOORDIV,
-                             "mod": MOD}[x.kind], None))
-        emit(e)
-        w.u32(len(ops))
-        for op, v in ops:
-            w.u8(op)
-            if op == PUSH_CONST:
-                w.i64(v)
-            elif op in (PUSH_SYM, PUSH_DIM):
-                w.u32(v)
-
-    def put_type(dt):
-        kind, bits = DTYPES[dt]
-        w.u8(kind)
-        w.u32(bits)
-
-    def put_desc(shape, dt):
-        w.u32(len(shape))
-        for e in shape:
-            put_expr(e)
-        w.u32(0)  # canonical row-major strides
-        put_expr(E.c(0))
-        put_type(dt)
+    w = _Writer(symbols)
 
     # symbol table by first use, in section order
     seq: List[E] = []
@@ -690,31 +695,31 @@ def _finalize(source_shape, source_dtype, axes, pads, stages, divisibility, dtyp
     for s in symbols:
         w.str(s)
     if typed:
-        put_desc(source_shape, source_dtype)
-        put_desc(result_shape, dtype)
+        w.desc(source_shape, source_dtype)
+        w.desc(result_shape, dtype)
     # layout body (v0 sections 3..12)
-    put_desc(source_shape, source_dtype)
-    put_desc(pext, dtype)
+    w.desc(source_shape, source_dtype)
+    w.desc(pext, dtype)
     w.u32(len(perm))
     for p in perm:
         w.u32(p)
     w.u32(len(maxes))
     for k, (a, s) in enumerate(zip(maxes, dstr)):
         w.str("d%d" % k)
-        put_expr(a.extent)
-        put_expr(a.stride)
-        put_expr(s)
+        w.expr(a.extent)
+        w.expr(a.stride)
+        w.expr(s)
     w.u32(len(new_pads))
     for k in sorted(new_pads):
         p = new_pads[k]
         w.u32(k)
-        put_expr(p.lo)
-        put_expr(p.hi)
-        put_type(dtype)
+        w.expr(p.lo)
+        w.expr(p.hi)
+        w.dtype(dtype)
         w.u64(p.bits)
     w.u32(len(divisibility))
     for e, d in divisibility:
-        put_expr(e)
+        w.expr(e)
         w.i64(d)
     w.u32(0)  # alignment
     w.u32(len(maxes))
@@ -728,27 +733,27 @@ def _finalize(source_shape, source_dtype, axes, pads, stages, divisibility, dtyp
     w.u32(len(maxes))
     inv = [perm.index(i) for i in range(len(perm))]
     for i in range(len(maxes)):
-        put_expr(E.d(inv[i]))
+        w.expr(E.d(inv[i]))
     params: List[Tuple[str, str, List[E]]] = []
     if typed:
         w.u32(len(stages))
         for st in stages:
             w.u8(TRANSFORMS[st.transform])
             w.u8(POLICIES[st.policy])
-            put_type(st.input)
+            w.dtype(st.input)
             w.u8(SIGNED if st.transform == "dequantize" else SIGNLESS)
-            put_type(st.output)
+            w.dtype(st.output)
             w.u8(SIGNED if st.transform == "quantize" else SIGNLESS)
             w.u32(len(st.shape))
             for e in st.shape:
-                put_expr(e)
+                w.expr(e)
             for role, p in (("scale", st.scale), ("zero_point", st.zero_point)):
                 if p is None:
                     w.u8(0)
                 elif isinstance(p, InlineParam):
                     w.u8(1)
                     w.u8(p.rank)
-                    put_type(p.dtype)
+                    w.dtype(p.dtype)
                     eb = p.element_bits()
                     w.u32(len(eb))
                     for v in eb:
@@ -758,14 +763,14 @@ def _finalize(source_shape, source_dtype, axes, pads, stages, divisibility, dtyp
                     w.str(p.name)
                     w.u8(len(p.extents))
                     for x in p.extents:
-                        put_expr(expr(x))
-                    put_type(p.dtype)
+                        w.expr(expr(x))
+                    w.dtype(p.dtype)
                     params.append((p.name, p.dtype, [expr(x) for x in p.extents]))
             w.i64(st.axis)
             if st.channel is not None:
                 w.u8(1)
                 w.u32(len(result_shape))
-                put_expr(st.channel)
+                w.expr(st.channel)
             else:
                 w.u8(0)
         w.u32(len(new_pads))
@@ -773,9 +778,68 @@ def _finalize(source_shape, source_dtype, axes, pads, stages, divisibility, dtyp
             p = new_pads[k]
             w.u32(k)
             w.u32(p.stage)
-            put_type(p.original_dtype)
+            w.dtype(p.original_dtype)
             w.u64(p.original_bits)
     elif pads and len({p.bits for p in pads}) > 1:
         raise EncodeError("layout plans carry a single fill value")
     return Plan(bytes(w.out), symbols, typed, list(source_shape), list(result_shape), source_dtype,
                 dtype, list(divisibility), params)
+
+
+# ------------------------------------------------------------ indexed (v2)
+
+# Element-type pairs an indexed plan may carry, with the numeric policy the
+# cast takes (docs/reloc-plan-format.md:287-345; validateIndexedPlan,
+# libreloc/src/Decode.cpp:950-991).
+_INDEXED_PAIRS = {("float32", "float32"): "exact", ("float16", "float16"): "exact",
+                  ("int8", "int8"): "exact", ("float32", "float16"): "ieee_rne",
+                  ("float16", "float32"): "exact"}
+
+
+def encode_index_select(source_shape: Sequence, source_dtype: str, count, index_dtype: str,
+                        result_dtype: Optional[str] = None) -> bytes:
+    """Wire v2 plan of `index_select(source, indices, axis 0)` followed by an
+    optional cast to `result_dtype` (the reference exporter's
+    `reloc.index_select` [+ `reloc.cast`] chain, test/dialect/reloc/
+    indexed_export.mlir). Extents are ints or symbol names; `count` is the
+    index operand's extent. Symbols are numbered by first use: source, then
+    indices, then result."""
+    result_dtype = result_dtype or source_dtype
+    policy = _INDEXED_PAIRS.get((source_dtype, result_dtype))
+    if policy is None:
+        raise EncodeError("indexed plans cast only f32 -> f16 and f16 -> f32 "
+                          "(or keep f32, f16, i8): %s -> %s" % (source_dtype, result_dtype))
+    if index_dtype not in ("int32", "int64"):
+        raise EncodeError("indices must be int32 or int64, got %s" % index_dtype)
+    src = [expr(x) for x in source_shape]
+    if not src:
+        raise EncodeError("index_select needs a source of rank >= 1")
+    for e in src + [expr(count)]:
+        if e.is_const() and e.value <= 0:
+            raise EncodeError("indexed plan extents must be positive")
+    ind = [expr(count)]
+    res = ind + src[1:]
+    symbols: List[str] = []
+
+    def note(e: E):
+        if e.kind == "sym":
+            if e.value not in symbols:
+                symbols.append(e.value)
+        elif e.kind not in ("const", "dim"):
+            note(e.a)
+            note(e.b)
+
+    for e in src + ind + res:
+        note(e)
+    w = _Writer(symbols)
+    w.out += b"RPLN"
+    w.u32(2)
+    w.u32(len(symbols))
+    for name in symbols:
+        w.str(name)
+    w.desc(src, source_dtype)
+    w.desc(ind, index_dtype)
+    w.desc(res, result_dtype)
+    w.u32(0)  # axis
+    w.u8(POLICIES[policy])
+    return bytes(w.out)

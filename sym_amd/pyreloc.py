@@ -3,7 +3,8 @@
 PyTransfer.cpp:312-461) for the H2D plan-execution path.
 
 Names and argument meaning follow the reference: `wire_version`,
-`load_plan`, `load_typed_plan`, `bind`, `bind_typed`, and errors raised as
+`load_plan`, `load_typed_plan`, `load_indexed_plan`, `bind`, `bind_typed`,
+`bind_indexed`, `bind_indexed_from_pointer`, and errors raised as
 `DecodeError`, `BindError` or `TransferError("<code>: <detail>")`. Buffers
 cross as (pointer, nbytes) pairs; ctypes releases the GIL during each call.
 """
@@ -105,6 +106,92 @@ def load_typed_plan(blob):
     return Plan(blob)
 
 
+def load_indexed_plan(blob):
+    """Decode an indexed (v2) plan (reference load_indexed_plan,
+    libreloc/python/PyReloc.cpp:863-875); a v0 or v1 blob is rejected at
+    byte 4."""
+    if wire_version(blob) not in (2, None):
+        raise DecodeError("unsupported wire format version (at byte 4)", 4)
+    return IndexedPlan(blob)
+
+
+_DTYPE_NAMES = {(0, 32): "float32", (0, 16): "float16", (0, 64): "float64", (1, 16): "bfloat16",
+                (2, 8): "int8", (2, 16): "int16", (2, 32): "int32", (2, 64): "int64"}
+_POLICY_NAMES = {0: "ieee_rne", 1: "exact", 2: "symmetric_rne", 3: "affine"}
+
+
+def _indexed_metadata(blob):
+    """Descriptor shapes, dtypes, axis and policy of a decoded v2 blob, as
+    the reference's IndexedPlanHandle.metadata (PyReloc.cpp:177-238):
+    expressions become nested lists (['const', v], ['symbol', name],
+    ['add'|'mul', lhs, rhs], ['floordiv'|'mod', lhs, constant]; a
+    subtraction reads as lhs + (-1 * rhs))."""
+    import struct
+    off = [8]
+
+    def u32():
+        v = struct.unpack_from("<I", blob, off[0])[0]
+        off[0] += 4
+        return v
+
+    def u8():
+        v = blob[off[0]]
+        off[0] += 1
+        return v
+
+    symbols = []
+    for _ in range(u32()):
+        n = u32()
+        symbols.append(blob[off[0]:off[0] + n].decode())
+        off[0] += n
+
+    def expr():
+        stack = []
+        for _ in range(u32()):
+            op = u8()
+            if op == 1:
+                stack.append(["const", struct.unpack_from("<q", blob, off[0])[0]])
+                off[0] += 8
+            elif op == 0:
+                stack.append(["symbol", symbols[u32()]])
+            else:
+                rhs, lhs = stack.pop(), stack.pop()
+                if op == 2:
+                    stack.append(["add", lhs, rhs])
+                elif op == 3:
+                    stack.append(["add", lhs, ["mul", ["const", -1], rhs]])
+                elif op == 4:
+                    stack.append(["mul", lhs, rhs])
+                else:
+                    if rhs[0] != "const":
+                        raise ValueError("indexed metadata requires constant divisors")
+                    stack.append(["floordiv" if op == 5 else "mod", lhs, rhs[1]])
+        return stack[-1]
+
+    def desc():
+        shape = [expr() for _ in range(u32())]
+        for _ in range(u32()):
+            expr()
+        expr()
+        kind = u8()
+        bits = u32()
+        return {"shape": shape, "dtype": _DTYPE_NAMES.get((kind, bits), "unknown")}
+
+    out = {"source": desc(), "indices": desc(), "result": desc()}
+    out["axis"] = u32()
+    out["policy"] = _POLICY_NAMES.get(u8(), "unknown")
+    return out
+
+
+class IndexedPlan(Plan):
+    """A decoded indexed plan (reference IndexedPlanHandle,
+    libreloc/python/PyReloc.cpp:852-854)."""
+
+    @property
+    def metadata(self):
+        return _indexed_metadata(self.blob)
+
+
 class Bound:
     """A bound plan with its prepared device program."""
 
@@ -130,6 +217,9 @@ class Bound:
         h = ctypes.c_void_p()
         if N.lib().relx_bind(plan._h, sn, sv, n, arr, len(params), ctypes.byref(h), ctypes.byref(err)):
             _raise(err)
+        self._adopt(h)
+
+    def _adopt(self, h):
         self._h = h
         info = N.relx_bound_info()
         N.lib().relx_bound_query(h, ctypes.byref(info))
@@ -138,6 +228,10 @@ class Bound:
     @property
     def typed(self):
         return bool(self.info.typed)
+
+    @property
+    def indexed(self):
+        return bool(self.info.indexed)
 
     @property
     def extents(self):
@@ -192,9 +286,83 @@ class Bound:
             self._h = None
 
 
+class IndexedBound(Bound):
+    """A bound indexed plan (reference IndexedBoundPlan,
+    libreloc/python/PyReloc.cpp:855-862): `source_extents` is the table's
+    shape, `result_extents` the selected rows', `indices` the bound,
+    range-checked row indices (a copy). The device program relocates the
+    selected rows (identity) through the plan's cast."""
+
+    def __init__(self, plan, symbols, dtype, extents, data):
+        if dtype not in DTYPE_KINDS:
+            raise ValueError("unsupported index dtype %r" % (dtype,))
+        self.plan = plan
+        kind, bits = DTYPE_KINDS[dtype]
+        names = list(symbols)
+        n = len(names)
+        sn = (ctypes.c_char_p * max(1, n))(*[s.encode() for s in names])
+        sv = (ctypes.c_int64 * max(1, n))(*[int(symbols[s]) for s in names])
+        ext = [int(e) for e in extents]
+        ea = (ctypes.c_int64 * max(1, len(ext)))(*ext)
+        data = bytes(data)
+        buf = ctypes.create_string_buffer(data, max(1, len(data)))
+        err = N.relx_err()
+        h = ctypes.c_void_p()
+        if N.lib().relx_bind_indexed(plan._h, sn, sv, n, kind, bits, ea, len(ext),
+                                     ctypes.cast(buf, ctypes.c_void_p), len(data),
+                                     ctypes.byref(h), ctypes.byref(err)):
+            _raise(err)
+        self._adopt(h)
+        self._index_bytes = data
+        self._index_bits = bits
+
+    @property
+    def source_extents(self):
+        i = self.info
+        return [i.table_rows] + list(i.result_extents[1:i.result_rank])
+
+    @property
+    def result_extents(self):
+        return list(self.info.result_extents[:self.info.result_rank])
+
+    @property
+    def row_elements(self):
+        return self.info.row_elements
+
+    @property
+    def table_bytes(self):
+        return self.info.table_bytes
+
+    @property
+    def indices(self):
+        import array
+        a = array.array("q" if self._index_bits == 64 else "i")
+        a.frombytes(self._index_bytes)
+        return list(a)
+
+
 def bind(plan, symbols):
     """bind (Bind.cpp:176-384) for a layout plan."""
     return Bound(plan, symbols)
+
+
+def bind_indexed(plan, symbols, indices):
+    """bindIndexed (Bind.cpp:701-819): `indices` is the (dtype, extents,
+    little-endian bytes) operand, as the reference's pyreloc.bind_indexed."""
+    if not isinstance(indices, tuple) or len(indices) != 3:
+        raise ValueError("indices must be a (dtype, extents, bytes) tuple")
+    dtype, extents, data = indices
+    return IndexedBound(plan, symbols, dtype, extents, data)
+
+
+def bind_indexed_from_pointer(plan, symbols, dtype, extents, pointer, nbytes):
+    """bind_indexed over a caller-owned little-endian index buffer at
+    `pointer` (reference bind_indexed_from_pointer, PyReloc.cpp:894-919);
+    the buffer is read during this call only."""
+    if not pointer and nbytes:
+        raise ValueError("index pointer must not be null")
+    data = ctypes.string_at(pointer, int(nbytes)) if nbytes else b""
+    return IndexedBound(plan, symbols, dtype, extents, data)
 
 
 def bind_typed(plan, symbols, parameters):
@@ -280,6 +448,14 @@ class Context:
                                          ctypes.byref(total), ctypes.byref(h), ctypes.byref(err)):
             _raise(err)
         return Completion(h, [r.as_dict() for r in reps], total.as_dict(), (bounds, owners))
+
+    def index_select_device(self, bound, table_ptr, table_nbytes, dst_ptr, dst_nbytes, stream=0):
+        """Gather an indexed plan's selected rows from a device-resident
+        table into `dst`, cast fused (async on `stream`)."""
+        err = N.relx_err()
+        if N.lib().relx_index_select_device(self._h, bound._h, table_ptr, table_nbytes, dst_ptr,
+                                            dst_nbytes, int(stream or 0), ctypes.byref(err)):
+            _raise(err)
 
     def relayout_device(self, bound, wire_ptr, dst_ptr, wire_boundary=0, stream=0):
         """Launch the device relayout on a device-resident wire (async)."""
@@ -392,7 +568,8 @@ def measure_d2h(device=0, nbytes=256 << 20, iters=20, rounds=3):
 # The typed dispatch API (prepare_dispatch / execute_dispatch / groups) lives
 # in sym_amd.dispatch and is re-exported here under pyreloc's names.
 from .dispatch import (BufferView, DispatchCompletion, DispatchRequest,  # noqa: E402,F401
-                       DispatchTemplate, GroupRequest, Resources, execute_dispatch,
-                       execute_dispatch_group, prepare_dispatch, prepare_dispatch_from_template,
-                       prepare_dispatch_group, prepare_dispatch_template, query_capability,
+                       DispatchTemplate, GroupRequest, IndexSelectProgram, Resources,
+                       execute_dispatch, execute_dispatch_group, prepare_dispatch,
+                       prepare_dispatch_from_template, prepare_dispatch_group,
+                       prepare_dispatch_template, prepare_index_select_program, query_capability,
                        submit_dispatch_group)

@@ -11,6 +11,8 @@ Sources:
   libreloc/test/TypedDecodeTest.cpp:43-49  v0 identity golden (181 bytes)
   libreloc/test/DecodeTest.cpp:41-120      v0 identity/reference/pad/degraded
   docs/runtime-evidence/cuda.json:40-60    exported example plan digests
+  test/dialect/reloc/indexed_export_check.py:50-57  frozen wire v2 bytes
+                                           (static f32[8,5], i64[3] -> f32[3,5])
 """
 import json
 import pathlib
@@ -49,7 +51,11 @@ def main():
                 walk(v, key)
 
     walk(evidence)
-    OUT.write_text(json.dumps({"typed_v1": typed, "layout_v0": v0, "exported_plan_digests": digests},
+    check = (REF / "test/dialect/reloc/indexed_export_check.py").read_text()
+    m = re.search(r"identity\.hex\(\) == \(((?:\s*'[0-9a-f]*')+)\s*\)", check)
+    indexed = {"static_f32_8x5_i64_3_exact": "".join(re.findall(r"'([0-9a-f]*)'", m.group(1)))}
+    OUT.write_text(json.dumps({"typed_v1": typed, "layout_v0": v0, "exported_plan_digests": digests,
+                               "indexed_v2": indexed},
                               indent=1, sort_keys=True) + "\n")
     print("wrote", OUT, len(typed), "typed,", len(v0), "v0,", len(digests), "digests")
 
