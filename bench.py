@@ -15,7 +15,8 @@ Headline (C2 image-batch relayout): fp32 NCHW
 * `cpu_baseline`: the reference's own compiled CPU executor (oracle/_ref,
   typed::executeHost) on this host, on a bounded sample.
 
-`--report` prints one JSON line per config (C1..C5) instead.
+`--report` prints one JSON line per config (C1..C5, and the indexed-plan
+gathers ix_*) instead.
 """
 import argparse
 import json
@@ -103,6 +104,161 @@ def make_case(name):
                     % (b, s), W.c5_plan().blob, {"B": b, "S": s}, W.param("scale", sc), x,
                     {"B": b, "S": s}, widths=(2, 1))
     raise ValueError(name)
+
+
+# ------------------------------------------------------ indexed plans
+
+# index_select (axis 0) + cast workloads: table shape, source dtype, result
+# dtype, selected rows (random, with repeats).
+IX = {"ix_f32f16": ((1 << 20, 1024), "float32", "float16", 65536),
+      "ix_f16f32": ((1 << 20, 1024), "float16", "float32", 65536),
+      "ix_i8": ((1 << 20, 4096), "int8", "int8", 65536),
+      "ix_row5": ((1 << 23, 5), "float32", "float16", 1 << 22)}
+IX_SETS = 8  # index sets rotated per step
+_W = {"float32": 4, "float16": 2, "int8": 1}
+_NP = {"float32": np.float32, "float16": np.float16, "int8": np.int8}
+SEED = 20260710
+
+
+def ix_bound(P, name, rows=None, seed=SEED):
+    from sym_amd.encoder import encode_index_select
+    shape, sd, rd, count = IX[name]
+    shape = ((rows,) + shape[1:]) if rows else shape
+    idx = np.random.default_rng(seed).integers(0, shape[0], count).astype("<i8")
+    b = P.bind_indexed(P.load_indexed_plan(encode_index_select(list(shape), sd, count, "int64", rd)),
+                       {}, ("int64", [count], idx.tobytes()))
+    return b, shape, sd, rd, idx
+
+
+def ix_kernel(name):
+    """The gather kernel instance a config launches (GatherOp, source bytes
+    per item) for 256-byte aligned buffers, as the library selects it."""
+    shape, sd, rd, _ = IX[name]
+    row = int(np.prod(shape[1:]))
+    if sd == rd:
+        nb = 16
+        while nb > 1 and (row * _W[sd]) % nb:
+            nb //= 2
+        return 0, nb
+    v = 4
+    while v > 1 and row % v:
+        v //= 2
+    return (1 if sd == "float32" else 2), v * _W[sd]
+
+
+def ix_alg_bytes(b, sd, rd, count):
+    """Algorithmic HBM bytes of one gather: selected rows read, 4-byte
+    device indices read, result written."""
+    return count * b.row_elements * (_W[sd] + _W[rd]) + 4 * count
+
+
+def gather_rate(torch, ctx, bounds, table, out_bytes, steps, warmup):
+    """K back-to-back device gathers into rotating outputs, each step with
+    the next of `bounds` (index sets drawn with different seeds, so that the
+    rows one step reads are not still in the 256 MB Infinity Cache from the
+    step before); returns (ms per step over the bracketed region, mean
+    per-launch ms)."""
+    sets = max(2, min(8, int(np.ceil(600e6 / out_bytes))))
+    outs = [torch.empty(out_bytes, dtype=torch.uint8, device="cuda") for _ in range(sets)]
+    stream = torch.cuda.Stream()
+    sp = stream.cuda_stream
+    tb = table.numel() * table.element_size()
+
+    def run(i):
+        ctx.index_select_device(bounds[i % len(bounds)], table.data_ptr(), tb,
+                                outs[i % sets].data_ptr(), out_bytes, stream=sp)
+    for i in range(warmup):
+        run(i)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for i in range(steps):
+        run(i)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms_step = t0.elapsed_time(t1) / steps
+    n = min(steps, 200)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for i in range(n):
+        ev[i][0].record(stream)
+        run(i)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    kms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
+    del outs
+    return ms_step, kms
+
+
+def device_table(torch, shape, sd):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(SEED)
+    if sd == "int8":
+        return torch.randint(-128, 128, shape, dtype=torch.int8, device="cuda", generator=g)
+    return torch.randn(shape, dtype=getattr(torch, sd), device="cuda", generator=g)
+
+
+def ix_config(torch, ctx, P, name, args, h2d_ceiling):
+    """Device gather from an HBM-resident table (relx_index_select_device),
+    then the host-table upload (host gather into the pinned ring + device
+    cast), pageable and pinned, and the reference CPU executor on the same
+    host table."""
+    b, shape, sd, rd, idx = ix_bound(P, name)
+    count = len(idx)
+    table = device_table(torch, shape, sd)
+    out_bytes = b.destination_bytes
+    bounds = [b] + [ix_bound(P, name, seed=SEED + s)[0] for s in range(1, IX_SETS)]
+    ms_step, kms = gather_rate(torch, ctx, bounds, table, out_bytes, max(50, args.steps // 20), 10)
+    alg = ix_alg_bytes(b, sd, rd, count)
+    del table
+    res = {"config": name, "workload": "index_select %s %s -> %d rows -> %s" % (sd, list(shape), count, rd),
+           "kernel": "gather<%d, %d>" % ix_kernel(name),
+           "device": {"ms_per_step": round(ms_step, 5), "kernel_ms_per_launch_events": round(kms, 5),
+                      "output_GBps": round(out_bytes / ms_step / 1e6, 1),
+                      "algorithmic_bytes": alg, "achieved_GBps": round(alg / ms_step / 1e6, 1),
+                      "hbm_frac": round(alg / ms_step / 1e6 / HBM_PEAK_GBS, 4),
+                      "traffic": traffic_for(name)}}
+    # upload from a host table a quarter the size (same selected rows)
+    rows = max(shape[0] // 4, 1)
+    hb, hshape, _, _, hidx = ix_bound(P, name, rows=rows)
+    rng = np.random.default_rng(SEED)
+    host = (rng.standard_normal(hshape, dtype=np.float32).astype(_NP[sd]) if sd != "int8"
+            else rng.integers(-128, 128, hshape, dtype=np.int8))
+    out = torch.empty(out_bytes, dtype=torch.uint8, device="cuda")
+    for pinned in (False, True):
+        src = torch.from_numpy(host.view(np.uint8).reshape(-1)).pin_memory() if pinned else None
+        ptr, nb = (src.data_ptr(), src.numel()) if pinned else (host.ctypes.data, host.nbytes)
+        for _ in range(3):
+            rep = ctx.execute_h2d(hb, ptr, nb, out.data_ptr(), out_bytes)
+        ts = []
+        for _ in range(max(10, args.e2e_samples // 4)):
+            t = time.perf_counter()
+            rep = ctx.execute_h2d(hb, ptr, nb, out.data_ptr(), out_bytes)
+            ts.append(time.perf_counter() - t)
+        p50 = float(np.percentile(ts, 50))
+        res["e2e_pinned" if pinned else "e2e_pageable"] = {
+            "table_bytes": host.nbytes, "p50_ms": round(p50 * 1e3, 3),
+            "effective_GBps": round(out_bytes / p50 / 1e9, 2), "wire_bytes": rep["wire_bytes"],
+            "pcie_frac": round(rep["wire_bytes"] / p50 / 1e9 / h2d_ceiling, 4),
+            "implementation": rep["implementation"], "chunks": rep["chunks"]}
+        del src
+    from oracle import ref
+    if ref.available() and not args.no_cpu:
+        from sym_amd.encoder import encode_index_select
+        blob = encode_index_select(list(hshape), sd, count, "int64", rd)
+        r = ref.IndexedRef(blob, {}, "int64", [count], hidx.tobytes(), threads=8)
+        o = np.empty(out_bytes, np.uint8)
+        r.execute(host, o)
+        n, t0 = 0, time.perf_counter()
+        while True:
+            r.execute(host, o)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= min(args.cpu_seconds, 5.0) and n >= 3:
+                break
+        res["cpu_baseline"] = {"value": round(out_bytes * n / el / 1e9, 3), "unit": "GB/s",
+                               "cores": 8, "kind": "reference",
+                               "sample": "%d x typed::executeHost (indexed rows) over the host table" % n}
+    return res
 
 
 # ----------------------------------------------------------- measurements
@@ -236,6 +392,18 @@ def traffic_probe(torch, ctx, names):
     del a, b
     kernels = {}
     for name in names:
+        if name in IX:
+            from sym_amd import pyreloc as P
+            b, shape, sd, rd, idx = ix_bound(P, name)
+            table = device_table(torch, shape, sd)
+            bounds = [b] + [ix_bound(P, name, seed=SEED + s)[0] for s in range(1, IX_SETS)]
+            gather_rate(torch, ctx, bounds, table, b.destination_bytes, 20, 2)
+            del table
+            op, nbi = ix_kernel(name)
+            kernels[name] = {"family": "gather", "pattern": "k_gather<%d, %d," % (op, nbi),
+                             "output_bytes": b.destination_bytes,
+                             "algorithmic_bytes": ix_alg_bytes(b, sd, rd, len(idx))}
+            continue
         case = make_case(name)
         device_rate(torch, ctx, case.bound, case.wire_bytes, case.out_bytes, 20, 2)
         bi = case.bound
@@ -273,7 +441,7 @@ def summarize_pmc(fetch_dir, write_dir, probe):
         factor = probe["calibration_bytes"] / float(np.median(cal))
         out[counter + "_calibration_factor"] = round(factor, 4)
         for name, info in probe["kernels"].items():
-            pat = "k_%s<%d, %d" % (info["family"], info["win"], info["wout"])
+            pat = info.get("pattern") or "k_%s<%d, %d" % (info["family"], info["win"], info["wout"])
             vals = [v for k, v in rows if pat in k]
             if vals:
                 med.setdefault(name, {})[counter] = float(np.median(vals)) * factor
@@ -284,6 +452,8 @@ def summarize_pmc(fetch_dir, write_dir, probe):
             alg = probe["kernels"][name]["algorithmic_bytes"]
             t = m["FETCH_SIZE"] + m["WRITE_SIZE"]
             out["configs"][name] = {"kernel": m["kernel"], "dispatches": m["dispatches"],
+                                    "fetch_factor": out["FETCH_SIZE_calibration_factor"],
+                                    "write_factor": out["WRITE_SIZE_calibration_factor"],
                                     "fetch_bytes": round(m["FETCH_SIZE"]),
                                     "write_bytes": round(m["WRITE_SIZE"]),
                                     "traffic_bytes": round(t), "algorithmic_bytes": alg,
@@ -410,7 +580,14 @@ def main():
         if probe is None:
             sys.exit("probe.json (the --traffic-probe output line) missing from the PMC directories")
         res = summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], probe)
-        with open(os.path.join(ROOT, "profiles", "traffic.json"), "w") as f:
+        path = os.path.join(ROOT, "profiles", "traffic.json")
+        if os.path.exists(path):  # keep the configs this probe did not cover
+            with open(path) as f:
+                old = json.load(f)
+            merged = dict(old.get("configs", {}))
+            merged.update(res["configs"])
+            res["configs"] = merged
+        with open(path, "w") as f:
             json.dump(res, f, indent=1)
         print(json.dumps(res))
         return
@@ -441,6 +618,8 @@ def main():
                     p50, p95, rep = e2e_rate(torch, ctx, case, 50, pinned=False)
                     print(json.dumps({"config": "c1", "N": n, "e2e_latency_us_p50": round(p50 * 1e6, 1),
                                       "e2e_latency_us_p95": round(p95 * 1e6, 1)}), flush=True)
+            elif name in IX:
+                print(json.dumps(ix_config(torch, ctx, P, name, args, h2d_ceiling)), flush=True)
             elif name == "c5":
                 from sym_amd import workloads as W
                 for b, s in W.C5_SHAPES:

@@ -161,17 +161,59 @@ void verify_gather(const Bound &b, const GatherPlan &g, const std::vector<Gather
 
 void host_gather(const Bound &b, const Prepared &p, uint32_t k, const void *table, void *dst,
                  int64_t g0, int64_t g1) {
+  // No software prefetch: measured on the host, the hardware prefetchers
+  // cover rows of 256 bytes and more, and explicit prefetches of the next
+  // rows only slowed the copy down.
   const uint32_t sw = b.source_type.width();
   const uint32_t wout = k ? p.stages[k - 1].out_width : sw;
   const uint8_t *t = static_cast<const uint8_t *>(table);
-  uint8_t *d = static_cast<uint8_t *>(dst);
-  const int64_t row = b.row_elements;
-  for (int64_t g = g0; g < g1;) {
-    const int64_t r = g / row, c = g - r * row;
-    const int64_t n = std::min(row - c, g1 - g);
-    const int64_t src_el = b.indices[static_cast<size_t>(r)] * row + c;
-    host_transform(p, k, sw, t + src_el * sw, d + (g - g0) * wout, 0, n);
-    g += n;
+  uint8_t *out = static_cast<uint8_t *>(dst);
+  const int64_t row = b.row_elements, row_in = row * sw;
+  const int64_t *idx = b.indices.data();
+  int64_t r = g0 / row, c = g0 - (g0 / row) * row, g = g0;
+  if (k == 0) { // bit copy: whole rows in a tight loop, partial rows at the ends
+    if (c) {
+      const int64_t n = std::min(row - c, g1 - g);
+      std::memcpy(out, t + idx[r] * row_in + c * sw, static_cast<size_t>(n * sw));
+      out += n * sw;
+      g += n;
+      ++r;
+    }
+    const int64_t full = (g1 - g) / row;
+    for (int64_t j = 0; j < full; ++j, ++r, out += row_in)
+      std::memcpy(out, t + idx[r] * row_in, static_cast<size_t>(row_in));
+    g += full * row;
+    if (g < g1)
+      std::memcpy(out, t + idx[r] * row_in, static_cast<size_t>((g1 - g) * sw));
+    return;
+  }
+  if (row >= 256) { // long rows: the stage's vector loop runs on each row
+    for (; g < g1; ++r, c = 0) {
+      const int64_t n = std::min(row - c, g1 - g);
+      host_transform(p, k, sw, t + (idx[r] * row + c) * sw, out + (g - g0) * wout, 0, n);
+      g += n;
+    }
+    return;
+  }
+  // Short rows with a stage: gather source values into a small buffer and
+  // convert them in batches (the vector conversions need long runs).
+  alignas(64) uint8_t tmp[16384];
+  const int64_t cap = static_cast<int64_t>(sizeof(tmp)) / sw;
+  while (g < g1) {
+    const int64_t base = g;
+    int64_t filled = 0;
+    while (g < g1 && filled < cap) {
+      const int64_t n = std::min(std::min(row - c, g1 - g), cap - filled);
+      std::memcpy(tmp + filled * sw, t + (idx[r] * row + c) * sw, static_cast<size_t>(n * sw));
+      filled += n;
+      g += n;
+      c += n;
+      if (c == row) {
+        c = 0;
+        ++r;
+      }
+    }
+    host_transform(p, k, sw, tmp, out + (base - g0) * wout, 0, filled);
   }
 }
 
