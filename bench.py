@@ -323,6 +323,33 @@ def e2e_rate(torch, ctx, case, samples, pinned, host_stages=-1):
     return p50, p95, rep
 
 
+def first_call_ms(torch, P, case):
+    """A cold call: new context, bind, first upload (ring, wire arena and
+    parameter upload allocated on the way), completion; pageable source."""
+    out = torch.empty(case.out_bytes, dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    ctx = P.Context(0)
+    b = P.Bound(case.plan, case.symbols, case.params if case.plan.typed else None)
+    ctx.execute_h2d(b, case.src.ctypes.data, case.src.nbytes, out.data_ptr(), case.out_bytes)
+    ms = (time.perf_counter() - t) * 1e3
+    ctx.close()
+    return round(ms, 3)
+
+
+def host_info():
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0))}
+
+
 def hbm_copy_ceiling(torch, nbytes=1 << 30, iters=20):
     a = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
     b = torch.empty_like(a)
@@ -606,7 +633,10 @@ def main():
 
     if args.report:
         print(json.dumps({"pinned_h2d_ceiling_GBps": round(h2d_ceiling, 2),
-                          "hbm_copy_GBps": round(hbm_copy_ceiling(torch), 1)}), flush=True)
+                          "hbm_copy_GBps": round(hbm_copy_ceiling(torch), 1),
+                          "vector_copy_GBps": {str(n >> 20) + "MiB": round(P.measure_copy(0, n, 50, 3), 1)
+                                               for n in (16 << 20, 64 << 20, 256 << 20, 1 << 30)}}),
+              flush=True)
         for name in args.configs.split(","):
             if name == "c4":
                 print(json.dumps(c4_report(torch, ctx, P, args, h2d_ceiling)), flush=True)
@@ -644,7 +674,15 @@ def main():
     p50, p95, rep = e2e_rate(torch, ctx, case, args.e2e_samples, pinned=False)
     q50, q95, prep = e2e_rate(torch, ctx, case, args.e2e_samples, pinned=True)
     f50, f95, frep = e2e_rate(torch, ctx, case, args.e2e_samples, pinned=False, host_stages=0)
-    cpu = None if args.no_cpu else cpu_baseline(case, args.cpu_seconds, 8)
+    first_ms = first_call_ms(torch, P, case)
+    # the size-matched copy ceiling: a 16-byte vector copy moving the same
+    # number of bytes (half read, half written)
+    copy_gbs = P.measure_copy(0, alg // 2, 200, 3)
+    cpu = cpu_all = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(case, args.cpu_seconds, 8)
+        cores = len(os.sched_getaffinity(0))
+        cpu_all = cpu_baseline(case, args.cpu_seconds, cores) if cores != 8 else cpu
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -665,8 +703,12 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_for("c2"), "kernel_ms": round(ms_step, 5),
                      "kernel_ms_per_launch_events": round(kms, 5),
-                     "algorithmic_bytes": alg},
+                     "algorithmic_bytes": alg,
+                     "copy_ceiling": {"GBps": round(copy_gbs, 1), "bytes": alg,
+                                      "kernel": "16-byte vector copy of the same bytes",
+                                      "frac": round(achieved / copy_gbs, 4)}},
         "e2e": {"pinned_h2d_ceiling_GBps": round(h2d_ceiling, 2),
+                "first_call_ms": first_ms,
                 "pageable": {"p50_ms": round(p50 * 1e3, 3), "p95_ms": round(p95 * 1e3, 3),
                              "effective_GBps": round(case.out_bytes / p50 / 1e9, 2),
                              "wire_bytes": rep["wire_bytes"], "implementation": rep["implementation"],
@@ -680,6 +722,8 @@ def main():
                            "wire_bytes": prep["wire_bytes"], "implementation": prep["implementation"],
                            "pcie_frac": round(prep["wire_bytes"] / q50 / 1e9 / h2d_ceiling, 4)}},
         "cpu_baseline": cpu,
+        "cpu_baseline_all_cores": cpu_all,
+        "host": host_info(),
     }
     ctx.close()
     print(json.dumps(line), flush=True)

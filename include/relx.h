@@ -336,6 +336,14 @@ double relx_measure_h2d(int device, size_t bytes, int iters, int rounds);
  * D2H direction of relx_execute_d2h is reported against. */
 double relx_measure_d2h(int device, size_t bytes, int iters, int rounds);
 
+/* Measured HBM copy ceiling (GB/s of bytes read + written): a 16-byte vector
+ * copy kernel of `bytes` (the stream kernel's access shape) over buffer pairs
+ * rotated past the Infinity Cache, `iters` copies, best of `rounds`. The
+ * device-side counterpart of relx_measure_h2d; the reference measures its
+ * copy kernel the same way (copyF32Vec4Kernel, libreloc/cuda/CudaKernels.cu:30-36).
+ * Returns -1 on failure. */
+double relx_measure_copy(int device, size_t bytes, int iters, int rounds);
+
 #ifdef __cplusplus
 }
 #endif

@@ -122,6 +122,7 @@ SIGNATURES = {
     "relx_host_free": (_I, [_VP]),
     "relx_measure_h2d": (ctypes.c_double, [_I, _SZ, _I, _I]),
     "relx_measure_d2h": (ctypes.c_double, [_I, _SZ, _I, _I]),
+    "relx_measure_copy": (ctypes.c_double, [_I, _SZ, _I, _I]),
 }
 
 _lib = None

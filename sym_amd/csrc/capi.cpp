@@ -563,6 +563,14 @@ double relx_measure_h2d(int device, size_t bytes, int iters, int rounds) {
   }
 }
 
+double relx_measure_copy(int device, size_t bytes, int iters, int rounds) {
+  try {
+    return relx::measure_device_copy(device, bytes, iters, rounds);
+  } catch (...) {
+    return -1.0;
+  }
+}
+
 double relx_measure_d2h(int device, size_t bytes, int iters, int rounds) {
   try {
     return relx::measure_copy(device, bytes, iters, rounds, true);

@@ -19,6 +19,7 @@
 #include <immintrin.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cstring>
 
 #include "../../include/relx.h"
@@ -34,6 +35,24 @@ namespace relx {
 
 // ------------------------------------------------------------ workers
 
+namespace {
+
+// How long an idle worker, or a caller waiting for its workers, spins
+// before blocking.
+constexpr auto kSpin = std::chrono::microseconds(200);
+
+template <class Pred> bool spin_until(Pred done) {
+  const auto t0 = std::chrono::steady_clock::now();
+  for (unsigned i = 0; !done(); ++i) {
+    _mm_pause();
+    if ((i & 63) == 63 && std::chrono::steady_clock::now() - t0 > kSpin)
+      return done();
+  }
+  return true;
+}
+
+} // namespace
+
 Workers::Workers(unsigned threads) {
   for (unsigned i = 1; i < std::max(1u, threads); ++i)
     threads_.emplace_back([this, i] { loop(i); });
@@ -42,7 +61,7 @@ Workers::Workers(unsigned threads) {
 Workers::~Workers() {
   {
     std::lock_guard<std::mutex> g(mu_);
-    stop_ = true;
+    stop_.store(true);
   }
   go_.notify_all();
   for (auto &t : threads_)
@@ -52,23 +71,21 @@ Workers::~Workers() {
 void Workers::loop(unsigned id) {
   uint64_t seen = 0;
   for (;;) {
-    std::pair<int64_t, int64_t> r;
-    const std::function<void(int64_t, int64_t)> *fn;
-    {
+    auto ready = [&] { return stop_.load() || generation_.load(std::memory_order_acquire) != seen; };
+    if (!spin_until(ready)) {
       std::unique_lock<std::mutex> g(mu_);
-      go_.wait(g, [&] { return stop_ || generation_ != seen; });
-      if (stop_)
-        return;
-      seen = generation_;
-      r = ranges_[id];
-      fn = fn_;
+      go_.wait(g, ready);
     }
+    if (stop_.load())
+      return;
+    seen = generation_.load(std::memory_order_acquire);
+    const std::pair<int64_t, int64_t> r = ranges_[id];
+    const std::function<void(int64_t, int64_t)> *fn = fn_;
     if (r.second > r.first)
       (*fn)(r.first, r.second);
-    {
+    if (pending_.fetch_sub(1, std::memory_order_acq_rel) == 1) {
       std::lock_guard<std::mutex> g(mu_);
-      if (--pending_ == 0)
-        done_.notify_one();
+      done_.notify_one();
     }
   }
 }
@@ -84,18 +101,23 @@ void Workers::parallel_for(int64_t n, int64_t grain,
     return;
   }
   {
+    // Workers read the ranges after they see the new generation (release
+    // here, acquire there); the lock orders it with a worker going to sleep.
     std::lock_guard<std::mutex> g(mu_);
     ranges_.assign(total, {0, 0});
     for (int64_t i = 0; i < parts; ++i)
       ranges_[static_cast<size_t>(i)] = {n * i / parts, n * (i + 1) / parts};
     fn_ = &fn;
-    pending_ = static_cast<unsigned>(threads_.size());
-    ++generation_;
+    pending_.store(static_cast<unsigned>(threads_.size()), std::memory_order_relaxed);
+    generation_.fetch_add(1, std::memory_order_release);
   }
   go_.notify_all();
   fn(ranges_[0].first, ranges_[0].second);
-  std::unique_lock<std::mutex> g(mu_);
-  done_.wait(g, [&] { return pending_ == 0; });
+  auto finished = [&] { return pending_.load(std::memory_order_acquire) == 0; };
+  if (!spin_until(finished)) {
+    std::unique_lock<std::mutex> g(mu_);
+    done_.wait(g, finished);
+  }
 }
 
 // ------------------------------------------------------------ staging
@@ -397,7 +419,7 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
   std::vector<ChunkPlan> plans;
   for (const Member &m : ms) {
     const DeviceProgram &dp = *m.dp;
-    const ChunkPlan p = chunk_plan(dp, source_width(*m.h->bound), opt.chunk_bytes);
+    const ChunkPlan p = chunk_plan(dp, source_width(*m.h->bound), opt.chunk_bytes, m.direct);
     if (!m.direct)
       max_slot = std::max(max_slot, static_cast<size_t>(p.per_chunk * p.unit_wire));
     plans.push_back(p);
@@ -415,6 +437,7 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
   if (caller) {
     HIPCHECK(hipEventRecord(ctx.start_ev, caller));
     HIPCHECK(hipStreamWaitEvent(ctx.copy, ctx.start_ev, 0));
+    HIPCHECK(hipStreamWaitEvent(ctx.copy2, ctx.start_ev, 0));
     HIPCHECK(hipStreamWaitEvent(ctx.compute, ctx.start_ev, 0));
   }
   bool any_generic = false;
@@ -426,6 +449,7 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
 
   int slot = 0;
   int ev = 0;
+  int64_t nchunk = 0; // chunks of every member so far: picks the copy stream
   relx_report sum{};
   for (size_t mi = 0; mi < ms.size(); ++mi) {
     Member &m = ms[mi];
@@ -439,9 +463,10 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
     for (int64_t v0 = 0; v0 < p.units; v0 += p.per_chunk) {
       const int64_t v1 = std::min(p.units, v0 + p.per_chunk);
       const int64_t woff = v0 * p.unit_wire, wbytes = (v1 - v0) * p.unit_wire;
+      hipStream_t cs = ctx.copy_stream(nchunk++);
       if (m.direct) {
         HIPCHECK(hipMemcpyAsync(wire + woff, m.src + woff, static_cast<size_t>(wbytes),
-                                hipMemcpyHostToDevice, ctx.copy));
+                                hipMemcpyHostToDevice, cs));
       } else {
         uint8_t *s = static_cast<uint8_t *>(ctx.slots[static_cast<size_t>(slot)]);
         HIPCHECK(hipEventSynchronize(ctx.slot_ev[static_cast<size_t>(slot)]));
@@ -463,13 +488,13 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
           });
         }
         HIPCHECK(hipMemcpyAsync(wire + woff, s, static_cast<size_t>(wbytes),
-                                hipMemcpyHostToDevice, ctx.copy));
-        HIPCHECK(hipEventRecord(ctx.slot_ev[static_cast<size_t>(slot)], ctx.copy));
+                                hipMemcpyHostToDevice, cs));
+        HIPCHECK(hipEventRecord(ctx.slot_ev[static_cast<size_t>(slot)], cs));
         slot = (slot + 1) % static_cast<int>(ctx.slots.size());
       }
       hipEvent_t ce = ctx.chunk_ev[static_cast<size_t>(ev)];
       ev = (ev + 1) % kChunkEvents;
-      HIPCHECK(hipEventRecord(ce, ctx.copy));
+      HIPCHECK(hipEventRecord(ce, cs));
       HIPCHECK(hipStreamWaitEvent(ctx.compute, ce, 0));
       launches += launch_program(dp, v0, v1, v0 == 0, v1 == p.units, wire, m.dst, par.pf, par.pi,
                                  status, ctx.compute);
@@ -538,7 +563,7 @@ void completion_wait(Completion &c) {
 
 // --------------------------------------------------------------- D2H
 
-D2hPlan d2h_plan(const DeviceProgram &dp, int64_t chunk_bytes) {
+D2hPlan d2h_plan(const DeviceProgram &dp, int64_t chunk_bytes, bool pinned) {
   const KArgs &a = dp.base;
   const int64_t out_bytes = dp.dst_elems * a.wout;
   D2hPlan p{-1, 1, 1, 1, out_bytes, out_bytes};
@@ -550,7 +575,7 @@ D2hPlan d2h_plan(const DeviceProgram &dp, int64_t chunk_bytes) {
   }
   if (!dense || run != dp.dst_elems || a.rank < 1)
     return p;
-  const int64_t want = chunk_bytes > 0 ? chunk_bytes : kDefaultChunkBytes;
+  const int64_t want = chunk_bytes > 0 ? chunk_bytes : default_chunk_bytes(out_bytes, false, pinned);
   p.copy_bytes = std::min(out_bytes, want);
   // the outermost axis one coordinate of which fits a chunk; the axes before
   // it must accept single-coordinate boxes
@@ -605,7 +630,7 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
   ensure_wire(ctx, static_cast<size_t>(out_bytes)); // the device result
   const bool pinned = opt.source_pinned > 0 || (opt.source_pinned < 0 && probe_pinned(dst));
 
-  const D2hPlan plan = d2h_plan(dp, opt.chunk_bytes);
+  const D2hPlan plan = d2h_plan(dp, opt.chunk_bytes, pinned);
   const int axis = plan.axis;
   // without a chunk axis the kernel runs once and only the copies are chunked
   const int64_t units = axis < 0 ? (out_bytes + plan.copy_bytes - 1) / plan.copy_bytes : plan.units;
@@ -624,6 +649,7 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
     HIPCHECK(hipEventRecord(ctx.start_ev, caller));
     HIPCHECK(hipStreamWaitEvent(ctx.compute, ctx.start_ev, 0));
     HIPCHECK(hipStreamWaitEvent(ctx.copy, ctx.start_ev, 0));
+    HIPCHECK(hipStreamWaitEvent(ctx.copy2, ctx.start_ev, 0));
   }
   int32_t *status = ctx.status + (ctx.status_next++ % kStatusSlots);
   if (dp.family == kFamGeneric)
@@ -646,6 +672,7 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
   };
   int64_t chunks = 0, launches = 0;
   int ev = 0;
+  hipEvent_t ke = nullptr; // the last kernel's event: each chunk's copy waits on it
   int64_t fixed[kMaxRank] = {};
   for (int64_t o = 0; o < plan.outer; ++o) {
    int64_t rem = o; // coordinates of the axes before `axis`
@@ -658,23 +685,24 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
     if (axis >= 0 || u0 == 0) {
       launches += launch_all(dp, prefix_launches(dp, fixed, axis, u0, u1), src, result, par.pf,
                              par.pi, status, ctx.compute);
-      hipEvent_t ke = ctx.chunk_ev[static_cast<size_t>(ev)];
+      ke = ctx.chunk_ev[static_cast<size_t>(ev)];
       ev = (ev + 1) % kChunkEvents;
       HIPCHECK(hipEventRecord(ke, ctx.compute));
-      HIPCHECK(hipStreamWaitEvent(ctx.copy, ke, 0));
     }
+    hipStream_t cs = ctx.copy_stream(chunks);
+    HIPCHECK(hipStreamWaitEvent(cs, ke, 0));
     const int64_t off = (o * units + u0) * row;
     const int64_t bytes = std::min((u1 - u0) * row, out_bytes - off);
     if (pinned) {
       HIPCHECK(hipMemcpyAsync(out + off, result + off, static_cast<size_t>(bytes),
-                              hipMemcpyDeviceToHost, ctx.copy));
+                              hipMemcpyDeviceToHost, cs));
     } else {
       const int slot = static_cast<int>(chunks % nslots);
       if (pending.size() - next >= static_cast<size_t>(nslots)) // the slot's last chunk
         consume(pending[next++]);
       HIPCHECK(hipMemcpyAsync(ctx.slots[static_cast<size_t>(slot)], result + off,
-                              static_cast<size_t>(bytes), hipMemcpyDeviceToHost, ctx.copy));
-      HIPCHECK(hipEventRecord(ctx.slot_ev[static_cast<size_t>(slot)], ctx.copy));
+                              static_cast<size_t>(bytes), hipMemcpyDeviceToHost, cs));
+      HIPCHECK(hipEventRecord(ctx.slot_ev[static_cast<size_t>(slot)], cs));
       pending.push_back({slot, off, bytes});
     }
     ++chunks;
@@ -682,6 +710,8 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
   }
   while (next < pending.size())
     consume(pending[next++]);
+  HIPCHECK(hipEventRecord(ctx.copy2_ev, ctx.copy2));
+  HIPCHECK(hipStreamWaitEvent(ctx.copy, ctx.copy2_ev, 0));
   HIPCHECK(hipEventRecord(ctx.done_ev, ctx.copy));
   if (caller)
     HIPCHECK(hipStreamWaitEvent(caller, ctx.done_ev, 0));
@@ -716,9 +746,11 @@ std::unique_ptr<Context> make_context(int device, int64_t max_retained) {
   ctx->max_retained = max_retained;
   DeviceGuard guard(device);
   HIPCHECK(hipStreamCreateWithFlags(&ctx->copy, hipStreamNonBlocking));
+  HIPCHECK(hipStreamCreateWithFlags(&ctx->copy2, hipStreamNonBlocking));
   HIPCHECK(hipStreamCreateWithFlags(&ctx->compute, hipStreamNonBlocking));
   HIPCHECK(hipEventCreateWithFlags(&ctx->start_ev, hipEventDisableTiming));
   HIPCHECK(hipEventCreateWithFlags(&ctx->done_ev, hipEventDisableTiming));
+  HIPCHECK(hipEventCreateWithFlags(&ctx->copy2_ev, hipEventDisableTiming));
   for (int i = 0; i < kChunkEvents; ++i) {
     hipEvent_t e;
     HIPCHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
@@ -740,8 +772,9 @@ Context::~Context() {
 bool drain(Context &ctx) {
   DeviceGuard guard(ctx.device);
   const bool a = hipStreamSynchronize(ctx.copy) == hipSuccess;
+  const bool a2 = hipStreamSynchronize(ctx.copy2) == hipSuccess;
   const bool b = hipStreamSynchronize(ctx.compute) == hipSuccess;
-  return a && b;
+  return a && a2 && b;
 }
 
 void destroy_context(Context &ctx) {
@@ -756,12 +789,16 @@ void destroy_context(Context &ctx) {
     (void)hipEventDestroy(ctx.start_ev);
   if (ctx.done_ev)
     (void)hipEventDestroy(ctx.done_ev);
+  if (ctx.copy2_ev)
+    (void)hipEventDestroy(ctx.copy2_ev);
   if (ctx.wire)
     (void)hipFree(ctx.wire);
   ctx.wire = nullptr;
   ctx.wire_cap = 0;
   if (ctx.copy)
     (void)hipStreamDestroy(ctx.copy);
+  if (ctx.copy2)
+    (void)hipStreamDestroy(ctx.copy2);
   if (ctx.compute)
     (void)hipStreamDestroy(ctx.compute);
   ctx.slots.clear();
@@ -772,8 +809,17 @@ uint32_t source_width(const Bound &b) {
   return b.typed ? b.source_type.width() : b.layout.element_size;
 }
 
-ChunkPlan chunk_plan(const DeviceProgram &dp, uint32_t src_width, int64_t chunk_bytes) {
-  const int64_t want_chunk = chunk_bytes > 0 ? chunk_bytes : kDefaultChunkBytes;
+int64_t default_chunk_bytes(int64_t total, bool h2d, bool direct) {
+  constexpr int64_t M = int64_t{1} << 20;
+  auto clamp = [](int64_t v, int64_t lo, int64_t hi) { return std::min(hi, std::max(lo, v)); };
+  if (h2d)
+    return direct ? clamp(total / 2, 32 * M, 64 * M) : clamp(total / 3, 4 * M, 16 * M);
+  return direct ? clamp(total / 4, 16 * M, 32 * M) : clamp(total / 8, 4 * M, 8 * M);
+}
+
+ChunkPlan chunk_plan(const DeviceProgram &dp, uint32_t src_width, int64_t chunk_bytes, bool direct) {
+  const int64_t want_chunk =
+      chunk_bytes > 0 ? chunk_bytes : default_chunk_bytes(dp.wire_bytes, true, direct);
   ChunkPlan p{};
   if (dp.chunk_axis >= 0) {
     p.units = dp.base.vext[dp.chunk_axis];
@@ -793,16 +839,20 @@ ChunkPlan chunk_plan(const DeviceProgram &dp, uint32_t src_width, int64_t chunk_
 
 int64_t verify_launches(BoundHandle &h, uint32_t k, int64_t chunk_bytes) {
   const DeviceProgram &dp = h.program(k);
-  const ChunkPlan p = chunk_plan(dp, source_width(*h.bound), chunk_bytes);
   int64_t n = 0;
-  for (int64_t v0 = 0; v0 < p.units; v0 += p.per_chunk) {
-    const int64_t v1 = std::min(p.units, v0 + p.per_chunk);
-    for (const KArgs &a : box_launches(dp, v0, v1, v0 == 0, v1 == p.units)) {
-      verify_launch(dp, a);
-      ++n;
+  bool whole = false;
+  for (int direct = 0; direct < (chunk_bytes > 0 ? 1 : 2); ++direct) {
+    const ChunkPlan p = chunk_plan(dp, source_width(*h.bound), chunk_bytes, direct != 0);
+    for (int64_t v0 = 0; v0 < p.units; v0 += p.per_chunk) {
+      const int64_t v1 = std::min(p.units, v0 + p.per_chunk);
+      for (const KArgs &a : box_launches(dp, v0, v1, v0 == 0, v1 == p.units)) {
+        verify_launch(dp, a);
+        ++n;
+      }
     }
+    whole = whole || (dp.chunk_axis >= 0 && p.units > p.per_chunk);
   }
-  if (dp.chunk_axis >= 0 && p.units > p.per_chunk)
+  if (whole)
     for (const KArgs &a : box_launches(dp, 0, 0, true, true)) { // the device-resident launch
       verify_launch(dp, a);
       ++n;
@@ -825,8 +875,9 @@ int64_t verify_launches(BoundHandle &h, uint32_t k, int64_t chunk_bytes) {
     }
     return n;
   }
-  if (k == 0) { // the device-to-host schedule (axis < 0: one whole launch)
-    const D2hPlan d = d2h_plan(dp, chunk_bytes);
+  // the device-to-host schedules (axis < 0: one whole launch)
+  for (int pinned = 0; k == 0 && pinned < (chunk_bytes > 0 ? 1 : 2); ++pinned) {
+    const D2hPlan d = d2h_plan(dp, chunk_bytes, pinned != 0);
     int64_t fixed[kMaxRank] = {};
     for (int64_t o = 0; o < d.outer; ++o) {
       int64_t rem = o;
@@ -893,6 +944,64 @@ double measure_copy(int device, size_t bytes, int iters, int rounds, bool d2h) {
   (void)hipStreamDestroy(s);
   (void)hipFree(d);
   (void)hipHostFree(h);
+  return best;
+}
+
+hipError_t copy16_launch(const void *src, void *dst, uint32_t n16, hipStream_t s);
+
+double measure_device_copy(int device, size_t bytes, int iters, int rounds) {
+  DeviceGuard guard(device);
+  const size_t n16 = bytes / 16;
+  if (n16 == 0 || n16 >= (size_t{1} << 31))
+    throw Error("invalid_argument", "copy size must be 16 B to 32 GiB");
+  bytes = n16 * 16;
+  // Rotate buffer pairs whose total exceeds the 256 MB Infinity Cache, so
+  // every copy reads and writes HBM.
+  const size_t sets = std::max<size_t>(2, std::min<size_t>(16, (size_t{600} << 20) / (2 * bytes) + 1));
+  std::vector<void *> src(sets, nullptr), dst(sets, nullptr);
+  hipStream_t s = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  double best = 0.0;
+  auto release = [&] {
+    for (void *p : src)
+      (void)hipFree(p);
+    for (void *p : dst)
+      (void)hipFree(p);
+    if (e0)
+      (void)hipEventDestroy(e0);
+    if (e1)
+      (void)hipEventDestroy(e1);
+    if (s)
+      (void)hipStreamDestroy(s);
+  };
+  try {
+    for (size_t i = 0; i < sets; ++i) {
+      HIPCHECK(hipMalloc(&src[i], bytes));
+      HIPCHECK(hipMalloc(&dst[i], bytes));
+      HIPCHECK(hipMemset(src[i], 1, bytes));
+    }
+    HIPCHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    HIPCHECK(hipEventCreate(&e0));
+    HIPCHECK(hipEventCreate(&e1));
+    for (size_t i = 0; i < 2 * sets; ++i)
+      HIPCHECK(copy16_launch(src[i % sets], dst[i % sets], static_cast<uint32_t>(n16), s));
+    HIPCHECK(hipStreamSynchronize(s));
+    for (int r = 0; r < rounds; ++r) {
+      HIPCHECK(hipEventRecord(e0, s));
+      for (int i = 0; i < iters; ++i)
+        HIPCHECK(copy16_launch(src[static_cast<size_t>(i) % sets], dst[static_cast<size_t>(i) % sets],
+                               static_cast<uint32_t>(n16), s));
+      HIPCHECK(hipEventRecord(e1, s));
+      HIPCHECK(hipEventSynchronize(e1));
+      float ms = 0.0f;
+      HIPCHECK(hipEventElapsedTime(&ms, e0, e1));
+      best = std::max(best, 2.0 * static_cast<double>(bytes) * iters / (ms * 1e-3) / 1e9);
+    }
+  } catch (...) {
+    release();
+    throw;
+  }
+  release();
   return best;
 }
 

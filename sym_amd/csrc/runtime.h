@@ -104,14 +104,22 @@ void verify_launch(const DeviceProgram &dp, const KArgs &a);
 struct ChunkPlan {
   int64_t units, per_chunk, unit_wire, unit_src;
 };
-constexpr int64_t kDefaultChunkBytes = int64_t{8} << 20;
+// Default chunk bytes for a transfer of `total` bytes, measured on the
+// MI355X's PCIe link with chunks alternating over two copy streams: staged
+// uploads a third of the wire within [4, 16] MiB, direct DMA half of it
+// within [32, 64] MiB; device-to-host into pinned memory a quarter of the
+// result within [16, 32] MiB, into pageable memory an eighth within [4, 8] MiB.
+int64_t default_chunk_bytes(int64_t total, bool h2d, bool direct);
 uint32_t source_width(const Bound &b);
-ChunkPlan chunk_plan(const DeviceProgram &dp, uint32_t src_width, int64_t chunk_bytes);
+ChunkPlan chunk_plan(const DeviceProgram &dp, uint32_t src_width, int64_t chunk_bytes, bool direct);
 
 // ------------------------------------------------------------ workers
 
 // Persistent worker threads; parallel_for splits [0, n) into contiguous
 // ranges (no smaller than `grain`), the calling thread runs one of them.
+// Between jobs the workers (and the caller, waiting for them) spin for a
+// short while before sleeping: a pipeline hands them one job per chunk, and
+// waking sleeping threads costs tens of microseconds per job.
 class Workers {
 public:
   explicit Workers(unsigned threads);
@@ -126,9 +134,9 @@ private:
   std::condition_variable go_, done_;
   const std::function<void(int64_t, int64_t)> *fn_ = nullptr;
   std::vector<std::pair<int64_t, int64_t>> ranges_;
-  uint64_t generation_ = 0;
-  unsigned pending_ = 0;
-  bool stop_ = false;
+  std::atomic<uint64_t> generation_{0};
+  std::atomic<unsigned> pending_{0};
+  std::atomic<bool> stop_{false};
 };
 
 // Host staging transform: source elements [e0, e1) at boundary 0 -> wire
@@ -192,7 +200,7 @@ struct D2hPlan {
   // axis < 0: one kernel launch, then copies of `copy_bytes` each
   int64_t copy_bytes;
 };
-D2hPlan d2h_plan(const DeviceProgram &dp, int64_t chunk_bytes);
+D2hPlan d2h_plan(const DeviceProgram &dp, int64_t chunk_bytes, bool pinned);
 
 struct Context;
 // Device-resident source -> host destination (see runtime.cpp).
@@ -204,22 +212,31 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
 void index_select_device(Context &ctx, BoundHandle &h, const void *table, size_t table_bytes,
                          void *dst, size_t dst_bytes, hipStream_t stream);
 
+// HBM copy ceiling: GB/s (bytes read + written) of a 16-byte vector copy of
+// `bytes`, best of `rounds` runs of `iters` copies over rotating buffers.
+double measure_device_copy(int device, size_t bytes, int iters, int rounds);
+
 // Leading per-tensor narrowing stages applied on the host for a pageable
 // source (halving PCIe bytes where a cast narrows).
 uint32_t auto_host_stages(const BoundHandle &h);
 
-// verify_launch over every launch of the chunk schedule for `chunk_bytes`
-// (and the whole-box launch of the device-resident path); returns the count.
+// verify_launch over every launch of the chunk schedules for `chunk_bytes`
+// (0: both defaults, staged and direct, in each direction) and the whole-box
+// launch of the device-resident path; returns the count.
 int64_t verify_launches(BoundHandle &h, uint32_t k, int64_t chunk_bytes);
 
 struct Context {
   int device = 0;
-  hipStream_t copy = nullptr, compute = nullptr;
+  // Two copy streams take alternate chunks: a DMA call costs tens of
+  // microseconds before its bytes move, and the second stream's call hides
+  // that behind the first one's transfer.
+  hipStream_t copy = nullptr, copy2 = nullptr, compute = nullptr;
+  hipStream_t copy_stream(int64_t chunk) const { return (chunk & 1) ? copy2 : copy; }
   std::vector<void *> slots;
   size_t slot_bytes = 0;
   std::vector<hipEvent_t> slot_ev;
   std::vector<hipEvent_t> chunk_ev;
-  hipEvent_t start_ev = nullptr, done_ev = nullptr;
+  hipEvent_t start_ev = nullptr, done_ev = nullptr, copy2_ev = nullptr;
   uint8_t *wire = nullptr;
   size_t wire_cap = 0;
   int32_t *status = nullptr; // kStatusSlots flags, one per call in flight

@@ -560,6 +560,12 @@ def measure_h2d(device=0, nbytes=256 << 20, iters=20, rounds=3):
     return N.lib().relx_measure_h2d(int(device), int(nbytes), int(iters), int(rounds))
 
 
+def measure_copy(device=0, nbytes=256 << 20, iters=20, rounds=3):
+    """HBM copy ceiling in GB/s (read + written bytes) of a 16-byte vector copy
+    of `nbytes`, over buffers rotated past the Infinity Cache."""
+    return N.lib().relx_measure_copy(int(device), int(nbytes), int(iters), int(rounds))
+
+
 def measure_d2h(device=0, nbytes=256 << 20, iters=20, rounds=3):
     """Pinned D2H ceiling in GB/s (the same measurement, device to host)."""
     return N.lib().relx_measure_d2h(int(device), int(nbytes), int(iters), int(rounds))
