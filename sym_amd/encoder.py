@@ -364,7 +364,15 @@ def encode(source_shape: Sequence, source_dtype: str, ops: Sequence, *, force_ty
             if any(p.axis == op.axis for p in pads):
                 raise EncodeError("one pad per axis")
             bits = op.bits if op.bits is not None else _value_bits(op.value, dtype)
-            pads.append(_PadState(op.axis, expr(op.lo), expr(op.hi), bits, bits, dtype, len(stages)))
+            lo = expr(op.lo)
+            pads.append(_PadState(op.axis, lo, expr(op.hi), bits, bits, dtype, len(stages)))
+            # earlier stages' channel maps read the padded axis shifted by the
+            # leading width (the reference builder does the same,
+            # sym/dialect/reloc/Transforms/PlanBuilder.h:44-47)
+            if not lo.is_const(0):
+                for s in stages:
+                    if s.channel is not None:
+                        s.channel = _shift_dim(s.channel, op.axis, lo)
         elif isinstance(op, (Cast, Quantize, Dequantize)):
             st = _stage(op, dtype, view_shape(), len(axes))
             for p in pads:
@@ -379,6 +387,15 @@ def encode(source_shape: Sequence, source_dtype: str, ops: Sequence, *, force_ty
     result_shape = view_shape()
     return _finalize(shape, source_dtype, axes, pads, stages, divisibility, dtype, result_shape,
                      typed)
+
+
+def _shift_dim(e: E, axis: int, lo: E) -> E:
+    """`e` with view coordinate `axis` replaced by (coordinate - lo)."""
+    if e.kind == "dim":
+        return E("sub", e, lo) if e.value == axis else e
+    if e.kind in ("const", "sym"):
+        return e
+    return E(e.kind, _shift_dim(e.a, axis, lo), _shift_dim(e.b, axis, lo))
 
 
 def _remap_dims(e: E, inv: List[int]) -> E:
