@@ -76,6 +76,10 @@ __global__ __launch_bounds__(kBlock) void k_gather(GatherArgs a) {
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = (blockIdx.x * kBlock + threadIdx.x) >> 6;
   const uint32_t stride = gridDim.x * (kBlock / 64) * (64 * U);
+  // every argument in one batch of scalar loads (see hot() in kernels.h)
+  asm volatile("" ::"s"(a.table), "s"(a.dst), "s"(a.idx), "s"(a.work), "s"(a.row_items),
+               "s"(stride));
+  hot(a.per_row);
   for (uint32_t base = wave * (64 * U) + lane; base < a.work; base += stride) {
     vec4 in[U];
     bool live[U];
