@@ -92,6 +92,7 @@ GatherPlan gather_plan(const Bound &b, const void *table, const void *dst) {
     g.nbo = v * static_cast<int>(rw);
   }
   g.row_items = b.row_elements * sw / g.nbi;
+  g.nt = g.nbi >= 8 && b.row_elements * sw >= 256;
   if (g.row_items >= kMaxLaunchWork)
     throw Error("unsupported_layout", "an indexed row spans 2^31 or more vector items");
   return g;
@@ -240,7 +241,7 @@ void index_select_device(Context &ctx, BoundHandle &h, const void *table, size_t
     verify_gather(b, g, launches, table, table_bytes, dst, dst_bytes, idx);
   hipStream_t s = stream ? stream : ctx.compute;
   for (const GatherArgs &a : launches)
-    hipcheck(gather_launch(a, g.op, g.nbi, g.iw, s), "gather launch");
+    hipcheck(gather_launch(a, g.op, g.nbi, g.iw, g.nt, s), "gather launch");
 }
 
 } // namespace relx

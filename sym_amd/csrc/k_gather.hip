@@ -7,12 +7,12 @@
 // few source rows, so loads and stores stay contiguous per row. The row index
 // of an item comes from one division by the row length in items; lanes of the
 // same row read the same index word. Output is written once and streamed past
-// the caches; table loads stay cached, since an index may repeat.
+// the caches. Table loads of long rows (256 bytes or more, 8- or 16-byte
+// items) stream too (3-4% faster); short rows load through the cache, where
+// neighbouring rows share lines (20-byte rows: 94 us cached, 128 us
+// streamed).
 #include "kernels.h"
 
-#ifndef RELX_GATHER_NT_LOAD
-#define RELX_GATHER_NT_LOAD false
-#endif
 #ifndef RELX_GATHER_NT_STORE
 #define RELX_GATHER_NT_STORE true
 #endif
@@ -68,11 +68,11 @@ template <int OP, int NBI> __device__ __forceinline__ vec4 convert(const vec4 &i
   }
 }
 
-template <int OP, int NBI, int IW>
+template <int OP, int NBI, int IW, bool NTL>
 __global__ __launch_bounds__(kBlock) void k_gather(GatherArgs a) {
   constexpr int NBO = gather_out_bytes(OP, NBI);
   constexpr int U = 2;
-  constexpr bool NTL = RELX_GATHER_NT_LOAD, NTS = RELX_GATHER_NT_STORE;
+  constexpr bool NTS = RELX_GATHER_NT_STORE;
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = (blockIdx.x * kBlock + threadIdx.x) >> 6;
   const uint32_t stride = gridDim.x * (kBlock / 64) * (64 * U);
@@ -110,12 +110,25 @@ __global__ __launch_bounds__(kBlock) void k_gather(GatherArgs a) {
 }
 
 template <int OP, int NBI>
-hipError_t gather_iw(const GatherArgs &a, int iw, hipStream_t s) {
+hipError_t gather_iw(const GatherArgs &a, int iw, bool nt, hipStream_t s) {
   const dim3 grid(grid_for((static_cast<int64_t>(a.work) + 1) / 2)), block(kBlock);
+  if constexpr (NBI >= 8) {
+    if (nt) {
+      if (iw == 4)
+        hipLaunchKernelGGL((k_gather<OP, NBI, 4, true>), grid, block, 0, s, a);
+      else if (iw == 8)
+        hipLaunchKernelGGL((k_gather<OP, NBI, 8, true>), grid, block, 0, s, a);
+      else
+        return hipErrorInvalidValue;
+      return hipGetLastError();
+    }
+  } else if (nt) {
+    return hipErrorInvalidValue;
+  }
   if (iw == 4)
-    hipLaunchKernelGGL((k_gather<OP, NBI, 4>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((k_gather<OP, NBI, 4, false>), grid, block, 0, s, a);
   else if (iw == 8)
-    hipLaunchKernelGGL((k_gather<OP, NBI, 8>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((k_gather<OP, NBI, 8, false>), grid, block, 0, s, a);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -124,43 +137,44 @@ hipError_t gather_iw(const GatherArgs &a, int iw, hipStream_t s) {
 } // namespace
 
 // Launch one gather: `op` a GatherOp, `nbi` source bytes per item (copy 1, 2,
-// 4, 8 or 16; f32 -> f16 4, 8 or 16; f16 -> f32 2, 4 or 8), `iw` index bytes.
-hipError_t gather_launch(const GatherArgs &a, int op, int nbi, int iw, hipStream_t s) {
+// 4, 8 or 16; f32 -> f16 4, 8 or 16; f16 -> f32 2, 4 or 8), `iw` index bytes,
+// `nt` streaming table loads (items of 8 bytes or more only).
+hipError_t gather_launch(const GatherArgs &a, int op, int nbi, int iw, bool nt, hipStream_t s) {
   if (a.work == 0)
     return hipSuccess;
   switch (op) {
   case kGatherCopy:
     switch (nbi) {
     case 1:
-      return gather_iw<kGatherCopy, 1>(a, iw, s);
+      return gather_iw<kGatherCopy, 1>(a, iw, nt, s);
     case 2:
-      return gather_iw<kGatherCopy, 2>(a, iw, s);
+      return gather_iw<kGatherCopy, 2>(a, iw, nt, s);
     case 4:
-      return gather_iw<kGatherCopy, 4>(a, iw, s);
+      return gather_iw<kGatherCopy, 4>(a, iw, nt, s);
     case 8:
-      return gather_iw<kGatherCopy, 8>(a, iw, s);
+      return gather_iw<kGatherCopy, 8>(a, iw, nt, s);
     case 16:
-      return gather_iw<kGatherCopy, 16>(a, iw, s);
+      return gather_iw<kGatherCopy, 16>(a, iw, nt, s);
     }
     break;
   case kGatherF32F16:
     switch (nbi) {
     case 4:
-      return gather_iw<kGatherF32F16, 4>(a, iw, s);
+      return gather_iw<kGatherF32F16, 4>(a, iw, nt, s);
     case 8:
-      return gather_iw<kGatherF32F16, 8>(a, iw, s);
+      return gather_iw<kGatherF32F16, 8>(a, iw, nt, s);
     case 16:
-      return gather_iw<kGatherF32F16, 16>(a, iw, s);
+      return gather_iw<kGatherF32F16, 16>(a, iw, nt, s);
     }
     break;
   case kGatherF16F32:
     switch (nbi) {
     case 2:
-      return gather_iw<kGatherF16F32, 2>(a, iw, s);
+      return gather_iw<kGatherF16F32, 2>(a, iw, nt, s);
     case 4:
-      return gather_iw<kGatherF16F32, 4>(a, iw, s);
+      return gather_iw<kGatherF16F32, 4>(a, iw, nt, s);
     case 8:
-      return gather_iw<kGatherF16F32, 8>(a, iw, s);
+      return gather_iw<kGatherF16F32, 8>(a, iw, nt, s);
     }
     break;
   }

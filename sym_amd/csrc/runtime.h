@@ -172,6 +172,7 @@ struct GatherPlan {
   int op = kGatherCopy;
   int nbi = 1, nbo = 1; // source / destination bytes per item
   int iw = 4;           // index bytes
+  bool nt = false;      // streaming table loads (long rows)
   int64_t row_items = 1;
 };
 GatherPlan gather_plan(const Bound &b, const void *table, const void *dst);
@@ -183,7 +184,7 @@ std::vector<GatherArgs> gather_launches(const Bound &b, const GatherPlan &g, con
 void verify_gather(const Bound &b, const GatherPlan &g, const std::vector<GatherArgs> &launches,
                    const void *table, size_t table_bytes, const void *dst, size_t dst_bytes,
                    const void *idx);
-hipError_t gather_launch(const GatherArgs &a, int op, int nbi, int iw, hipStream_t s);
+hipError_t gather_launch(const GatherArgs &a, int op, int nbi, int iw, bool nt, hipStream_t s);
 // Host staging of an indexed plan: selected elements [g0, g1) (dense
 // selected-row order) gathered from the table through stages [0, k) into
 // `dst`, which receives element g0 first.
