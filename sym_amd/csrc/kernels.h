@@ -488,6 +488,54 @@ __device__ __forceinline__ void chain_vec(const KArgs &a, uint32_t (&v)[V], int6
   }
 }
 
+// Per-vector stage parameters of the compile-time bodies with a per-channel
+// stage, for vectors whose channel is constant (DevStage::vec == 0): fetched
+// right after a kernel issues its data loads, so that every vector's
+// parameter load is in flight with them instead of waited for one by one
+// while the vectors are converted. The loads are unconditional (a vector
+// with one channel per element reads its first element's entry, in range)
+// so that no branch forces an early wait.
+struct VecParams {
+  float sc;
+  int32_t zp;
+};
+
+template <int CH> __device__ __forceinline__ VecParams fetch_params(const KArgs &a, int64_t o) {
+  VecParams p{0.0f, 0};
+  if constexpr (CH == kChainDeqF16) {
+    const DevStage &s = a.chain.st[0];
+    const uint32_t c = chan_of(s, o);
+    p.sc = a.pf[s.scale_off + c];
+    p.zp = a.pi[s.zp_off + (s.zp_per_ch ? c : 0u)];
+  } else if constexpr (CH == kChainF16Quant) {
+    const DevStage &s = a.chain.st[1];
+    p.sc = a.pf[s.scale_off + chan_of(s, o)];
+  }
+  return p;
+}
+
+// chain_vec with the parameters of a channel-constant vector given.
+template <int CH, int V>
+__device__ __forceinline__ void chain_vec_p(const KArgs &a, uint32_t (&v)[V], int64_t o,
+                                            const VecParams &p) {
+  if constexpr (CH == kChainDeqF16) {
+    if (a.chain.st[0].vec == 0) {
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+        v[e] = op_f32_f16(op_dequant(v[e], p.sc, p.zp));
+      return;
+    }
+  } else if constexpr (CH == kChainF16Quant) {
+    if (a.chain.st[1].vec == 0) {
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+        v[e] = quant_value(op_f16_f32_value(v[e]), p.sc);
+      return;
+    }
+  }
+  chain_vec<CH, V>(a, v, o);
+}
+
 // ---------------------------------------------------------------- stream
 
 // Stream work items hold V = 16/max(win, wout) elements: the wider side
@@ -532,6 +580,10 @@ __global__ __launch_bounds__(kBlock) void k_stream(KArgs a) {
       if (live[u] && !pad[u])
         in[u] = ld_n<BI, NTL>(a.src + sof[u] * WIN);
     }
+    VecParams par[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      par[u] = fetch_params<CH>(a, dof[u]);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (!live[u])
@@ -543,7 +595,7 @@ __global__ __launch_bounds__(kBlock) void k_stream(KArgs a) {
           v[e] = a.fill;
       } else {
         unpack<WIN, V>(&in[u], v);
-        chain_vec<CH, V>(a, v, dof[u]);
+        chain_vec_p<CH, V>(a, v, dof[u], par[u]);
       }
       vec4 out = {0u, 0u, 0u, 0u};
       pack<WOUT, V>(v, &out);
@@ -593,6 +645,14 @@ __global__ __launch_bounds__(kBlock) void k_transpose(KArgs a) {
     in[j] = ld16<NTL>(reinterpret_cast<const vec4 *>(
         a.src + (sbase + (c0 + row) * a.t_ssc + q0 + cv * VI) * WIN));
   }
+  // the store phase's stage parameters, in flight with the tile loads
+  VecParams par[NO];
+#pragma unroll
+  for (int j = 0; j < NO; ++j) {
+    const int vid = threadIdx.x + j * kBlock;
+    const int row = vid / VPRO, cv = vid % VPRO;
+    par[j] = fetch_params<CH>(a, dbase + (q0 + row) * a.t_dsq + c0 + cv * VO);
+  }
 #pragma unroll
   for (int j = 0; j < NI; ++j) {
     const int vid = threadIdx.x + j * kBlock;
@@ -614,7 +674,7 @@ __global__ __launch_bounds__(kBlock) void k_transpose(KArgs a) {
     for (int e = 0; e < VO; ++e)
       v[e] = tile[(cv * VO + e) * kPitch + row];
     const int64_t dof = dbase + (q0 + row) * a.t_dsq + c0 + cv * VO;
-    chain_vec<CH, VO>(a, v, dof);
+    chain_vec_p<CH, VO>(a, v, dof, par[j]);
     vec4 out;
     pack<WOUT, VO>(v, &out);
     st16<NTS>(reinterpret_cast<vec4 *>(a.dst + dof * WOUT), out);
@@ -749,6 +809,22 @@ __global__ __launch_bounds__(kBlock) void k_permute(KArgs a) {
       if (v < nvec)
         in[u] = ld16<NTL>(reinterpret_cast<const vec4 *>(src) + v);
     }
+    // each vector's place: (t, c, e) in the block and its dense result offset
+    uint32_t lds_off[U];
+    int64_t ro[U];
+    VecParams par[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t v = v0 + u * kBlock < nvec ? v0 + u * kBlock : v0;
+      const uint32_t off = v * VI; // element offset in the block's source run
+      const uint32_t tt = fdiv(off, a.p_ce);
+      const uint32_t rem = off - tt * CE;
+      const uint32_t c = fdiv(rem, a.p_e);
+      const uint32_t e = rem - c * E;
+      lds_off[u] = ((c * a.p_t + tt) * E + e) * WOUT;
+      ro[u] = dbase + c * a.p_dsc + static_cast<int64_t>(m0 + tt) * E + e;
+      par[u] = fetch_params<CH>(a, ro[u]);
+    }
     // one body per vector with a compile-time index, so `in` stays in
     // registers whatever the chain's size
     auto emit = [&](auto uc) {
@@ -756,18 +832,13 @@ __global__ __launch_bounds__(kBlock) void k_permute(KArgs a) {
       const uint32_t v = v0 + u * kBlock;
       if (v >= nvec)
         return;
-      const uint32_t off = v * VI; // element offset in the block's source run
-      const uint32_t tt = fdiv(off, a.p_ce);
-      const uint32_t rem = off - tt * CE;
-      const uint32_t c = fdiv(rem, a.p_e);
-      const uint32_t e = rem - c * E;
       uint32_t x[VI];
       unpack<WIN, VI>(&in[u], x);
-      chain_vec<CH, VI>(a, x, dbase + c * a.p_dsc + static_cast<int64_t>(m0 + tt) * E + e);
+      chain_vec_p<CH, VI>(a, x, ro[u], par[u]);
       vec4 o[(BO + 15) / 16];
       o[0] = vec4{0u, 0u, 0u, 0u};
       pack<WOUT, VI>(x, o);
-      uint8_t *dstl = lds + ((c * a.p_t + tt) * E + e) * WOUT;
+      uint8_t *dstl = lds + lds_off[u];
       if constexpr (BO >= 16) {
 #pragma unroll
         for (int j = 0; j < BO / 16; ++j)
