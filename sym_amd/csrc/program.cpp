@@ -16,6 +16,10 @@
 
 #include "index.h"
 
+#ifndef RELX_PERMUTE_SOURCE_BYTES
+#define RELX_PERMUTE_SOURCE_BYTES 16384
+#endif
+
 namespace relx {
 
 FastDiv make_div(int64_t d64) {
@@ -417,7 +421,7 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
     int64_t T = 0;
     if (ok) {
       T = 1;
-      while (T * 2 <= M && M % (T * 2) == 0 && T * 2 * C * E * win <= 16384 &&
+      while (T * 2 <= M && M % (T * 2) == 0 && T * 2 * C * E * win <= RELX_PERMUTE_SOURCE_BYTES &&
              T * 2 * C * E * wout <= 32768)
         T *= 2;
       ok = T * C * E * wout <= 32768;
