@@ -25,7 +25,7 @@ DEVICE = ["--offload-arch=" + ARCH, "-mcode-object-version=5", "-fno-gpu-flush-d
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 SOURCES = ["plan.cpp", "program.cpp", "runtime.cpp", "indexed.cpp", "capi.cpp", "kernels.hip",
            "k_stream_fast.hip", "k_stream_generic.hip", "k_transpose.hip", "k_interleave.hip",
-           "k_permute.hip", "k_gather.hip", "k_copy.hip"]
+           "k_interleave_generic.hip", "k_permute.hip", "k_gather.hip", "k_copy.hip"]
 
 
 def _compile(src):

@@ -1,6 +1,7 @@
 // kernels.hip - the generic kernel's launch and the family dispatcher.
 // Kernel bodies live in kernels.h; the fast families are instantiated in
-// k_stream_fast.hip, k_stream_generic.hip, k_transpose.hip, k_interleave.hip, k_permute.hip.
+// k_stream_fast.hip, k_stream_generic.hip, k_transpose.hip, k_interleave.hip,
+// k_interleave_generic.hip, k_permute.hip.
 #include "kernels.h"
 
 namespace relx {
