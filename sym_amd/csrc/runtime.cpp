@@ -9,10 +9,10 @@
 //     the host while it stages), never the widened result;
 //   * chunks follow the source-outer axis, so each chunk's wire bytes are one
 //     contiguous range and the kernel for that chunk needs nothing else;
-//   * copy stream: host workers fill pinned ring slot i (event-gated reuse),
-//     hipMemcpyAsync moves it to the device wire buffer, an event marks it;
-//   * compute stream: waits on the chunk's event and relayouts that chunk's
-//     box while the next chunk is in flight.
+//   * two copy streams take alternate chunks: host workers fill pinned ring
+//     slot i (event-gated reuse), hipMemcpyAsync moves it to the device wire
+//     buffer, and the chunk's relayout kernel follows on the same stream
+//     while the next chunk is in flight on the other one.
 // A page-locked source skips the ring and is DMA'd in place.
 #include "runtime.h"
 
@@ -23,6 +23,7 @@
 #include <cstring>
 
 #include "../../include/relx.h"
+
 
 namespace relx {
 
@@ -263,12 +264,14 @@ struct DeviceGuard {
   }
 };
 
-constexpr int kChunkEvents = 32;
+constexpr int kChunkEvents = 32; // device-to-host kernel events, reused round robin
 
 void ensure_wire(Context &ctx, size_t bytes) {
   if (ctx.wire_cap >= bytes)
     return;
   if (ctx.wire) {
+    HIPCHECK(hipStreamSynchronize(ctx.copy));
+    HIPCHECK(hipStreamSynchronize(ctx.copy2));
     HIPCHECK(hipStreamSynchronize(ctx.compute));
     HIPCHECK(hipFree(ctx.wire));
     ctx.wire = nullptr;
@@ -424,6 +427,10 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
       max_slot = std::max(max_slot, static_cast<size_t>(p.per_chunk * p.unit_wire));
     plans.push_back(p);
   }
+  int64_t total_chunks = 0;
+  for (const ChunkPlan &p : plans)
+    total_chunks += (p.units + p.per_chunk - 1) / p.per_chunk;
+  const bool two_streams = total_chunks > 1; // else the second copy stream stays idle
   const int nslots = opt.n_buffers > 0 ? opt.n_buffers : 3;
   if (max_slot)
     ensure_ring(ctx, nslots, max_slot);
@@ -433,22 +440,32 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
     ctx.worker_threads = threads;
   }
 
+  // Each chunk's kernel runs on the stream that copied the chunk (a kernel
+  // behind a copy on one stream starts about 10 us sooner than one ordered
+  // by an event from another stream); both copy streams join at the end.
+  if (ctx.unsynced) { // the previous call may still read the wire arena
+    HIPCHECK(hipStreamWaitEvent(ctx.copy, ctx.done_ev, 0));
+    HIPCHECK(hipStreamWaitEvent(ctx.copy2, ctx.done_ev, 0));
+  }
   hipStream_t caller = reinterpret_cast<hipStream_t>(opt.caller_stream);
   if (caller) {
     HIPCHECK(hipEventRecord(ctx.start_ev, caller));
     HIPCHECK(hipStreamWaitEvent(ctx.copy, ctx.start_ev, 0));
     HIPCHECK(hipStreamWaitEvent(ctx.copy2, ctx.start_ev, 0));
-    HIPCHECK(hipStreamWaitEvent(ctx.compute, ctx.start_ev, 0));
   }
   bool any_generic = false;
   for (const Member &m : ms)
     any_generic = any_generic || m.dp->family == kFamGeneric;
   int32_t *status = ctx.status + (ctx.status_next++ % kStatusSlots);
-  if (any_generic)
-    HIPCHECK(hipMemsetAsync(status, 0, sizeof(int32_t), ctx.compute));
+  if (any_generic) { // cleared before any kernel of either stream
+    HIPCHECK(hipMemsetAsync(status, 0, sizeof(int32_t), ctx.copy));
+    if (two_streams) {
+      HIPCHECK(hipEventRecord(ctx.copy2_ev, ctx.copy));
+      HIPCHECK(hipStreamWaitEvent(ctx.copy2, ctx.copy2_ev, 0));
+    }
+  }
 
   int slot = 0;
-  int ev = 0;
   int64_t nchunk = 0; // chunks of every member so far: picks the copy stream
   relx_report sum{};
   for (size_t mi = 0; mi < ms.size(); ++mi) {
@@ -492,12 +509,8 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
         HIPCHECK(hipEventRecord(ctx.slot_ev[static_cast<size_t>(slot)], cs));
         slot = (slot + 1) % static_cast<int>(ctx.slots.size());
       }
-      hipEvent_t ce = ctx.chunk_ev[static_cast<size_t>(ev)];
-      ev = (ev + 1) % kChunkEvents;
-      HIPCHECK(hipEventRecord(ce, cs));
-      HIPCHECK(hipStreamWaitEvent(ctx.compute, ce, 0));
       launches += launch_program(dp, v0, v1, v0 == 0, v1 == p.units, wire, m.dst, par.pf, par.pi,
-                                 status, ctx.compute);
+                                 status, cs);
       ++chunks;
     }
     if (m.report) {
@@ -525,7 +538,14 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
       sum.kernel_launches += r.kernel_launches;
     }
   }
-  HIPCHECK(hipEventRecord(ctx.done_ev, ctx.compute));
+  // join on the stream of the last chunk (the other one is usually done)
+  hipStream_t last = nchunk > 0 ? ctx.copy_stream(nchunk - 1) : ctx.copy;
+  hipStream_t other = last == ctx.copy ? ctx.copy2 : ctx.copy;
+  if (two_streams) {
+    HIPCHECK(hipEventRecord(ctx.copy2_ev, other));
+    HIPCHECK(hipStreamWaitEvent(last, ctx.copy2_ev, 0));
+  }
+  HIPCHECK(hipEventRecord(ctx.done_ev, last));
   if (caller)
     HIPCHECK(hipStreamWaitEvent(caller, ctx.done_ev, 0));
   if (total) {
@@ -533,14 +553,18 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
     *total = sum;
   }
   if (comp) {
-    HIPCHECK(hipEventRecord(comp->ev, ctx.compute));
+    HIPCHECK(hipEventRecord(comp->ev, last));
     comp->status = status;
     comp->generic = any_generic;
+    ctx.unsynced = true;
     return;
   }
-  if (opt.no_wait)
+  if (opt.no_wait) {
+    ctx.unsynced = true;
     return;
+  }
   HIPCHECK(hipEventSynchronize(ctx.done_ev));
+  ctx.unsynced = false;
   if (any_generic) {
     int32_t flag = 0;
     HIPCHECK(hipMemcpy(&flag, status, sizeof(flag), hipMemcpyDeviceToHost));
@@ -644,6 +668,11 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
     ctx.workers = std::make_unique<Workers>(threads);
     ctx.worker_threads = threads;
   }
+  if (ctx.unsynced) { // a submitted upload may still read the arena this call writes
+    HIPCHECK(hipStreamWaitEvent(ctx.compute, ctx.done_ev, 0));
+    HIPCHECK(hipStreamWaitEvent(ctx.copy, ctx.done_ev, 0));
+    HIPCHECK(hipStreamWaitEvent(ctx.copy2, ctx.done_ev, 0));
+  }
   hipStream_t caller = reinterpret_cast<hipStream_t>(opt.caller_stream);
   if (caller) { // the source is produced on the caller's stream
     HIPCHECK(hipEventRecord(ctx.start_ev, caller));
@@ -671,8 +700,11 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
     });
   };
   int64_t chunks = 0, launches = 0;
+  // The kernels run back to back on the compute stream, ahead of the copies
+  // (on the copy streams a kernel would queue behind the copy before it);
+  // each copy waits on its chunk's kernel event.
   int ev = 0;
-  hipEvent_t ke = nullptr; // the last kernel's event: each chunk's copy waits on it
+  hipEvent_t ke = nullptr;
   int64_t fixed[kMaxRank] = {};
   for (int64_t o = 0; o < plan.outer; ++o) {
    int64_t rem = o; // coordinates of the axes before `axis`
@@ -716,6 +748,7 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
   if (caller)
     HIPCHECK(hipStreamWaitEvent(caller, ctx.done_ev, 0));
   HIPCHECK(hipEventSynchronize(ctx.done_ev));
+  ctx.unsynced = false;
   if (dp.family == kFamGeneric) {
     int32_t flag = 0;
     HIPCHECK(hipMemcpy(&flag, status, sizeof(flag), hipMemcpyDeviceToHost));
@@ -813,7 +846,7 @@ int64_t default_chunk_bytes(int64_t total, bool h2d, bool direct) {
   constexpr int64_t M = int64_t{1} << 20;
   auto clamp = [](int64_t v, int64_t lo, int64_t hi) { return std::min(hi, std::max(lo, v)); };
   if (h2d)
-    return direct ? clamp(total / 2, 32 * M, 64 * M) : clamp(total / 3, 4 * M, 16 * M);
+    return direct ? clamp(total / 2, 32 * M, 64 * M) : clamp(total / 4, 2 * M, 8 * M);
   return direct ? clamp(total / 4, 16 * M, 32 * M) : clamp(total / 8, 4 * M, 8 * M);
 }
 

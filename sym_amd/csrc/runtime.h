@@ -106,7 +106,7 @@ struct ChunkPlan {
 };
 // Default chunk bytes for a transfer of `total` bytes, measured on the
 // MI355X's PCIe link with chunks alternating over two copy streams: staged
-// uploads a third of the wire within [4, 16] MiB, direct DMA half of it
+// uploads a quarter of the wire within [2, 8] MiB, direct DMA half of it
 // within [32, 64] MiB; device-to-host into pinned memory a quarter of the
 // result within [16, 32] MiB, into pageable memory an eighth within [4, 8] MiB.
 int64_t default_chunk_bytes(int64_t total, bool h2d, bool direct);
@@ -247,6 +247,10 @@ struct Context {
   int64_t max_retained = 0;
   std::mutex mu;
   int64_t calls = 0, failures = 0;
+  // The last call returned before its work completed (a submitted group or
+  // no_wait): done_ev marks its end, and the next call that reuses the wire
+  // arena orders its streams after it.
+  bool unsynced = false;
   bool quarantined = false;
   bool closed = false;
   ~Context(); // frees the status flags (the rest goes in destroy_context)

@@ -241,6 +241,25 @@ def test_submitted_groups_overlap_and_order_a_stream(resources, rng, pinned):
     cb.close()
 
 
+@pytest.mark.parametrize("pinned", [False, True])
+def test_call_after_submitted_group_waits_for_its_wire(resources, rng, pinned):
+    """A blocking group right after a submitted one reuses the context's wire
+    arena: it must not overwrite wire bytes the first group's kernels have
+    yet to read."""
+    ea, oa, wa, ka = _expert_group(rng, 2048, 2048, 3, pinned)
+    eb, ob, wb, kb = _expert_group(rng, 256, 512, 2, pinned)
+    say("submit, then a blocking group on the same resources", "pinned" if pinned else "pageable")
+    ca = P.submit_dispatch_group(P.prepare_dispatch_group(ea), resources=resources,
+                                 owners=(tuple(ka), tuple(oa)))
+    P.execute_dispatch_group(P.prepare_dispatch_group(eb), resources=resources)
+    for out, want in zip(ob, wb):
+        assert np.array_equal(out.cpu().numpy().view(np.uint16), want)
+    ca.wait()
+    for out, want in zip(oa, wa):
+        assert np.array_equal(out.cpu().numpy().view(np.uint16), want)
+    ca.close()
+
+
 def test_abandoned_completion_drains(resources, rng):
     e, o, w, k = _expert_group(rng, 256, 256, 2, True)
     c = P.submit_dispatch_group(P.prepare_dispatch_group(e), resources=resources,
