@@ -3,13 +3,16 @@
 // libreloc/src/Bind.cpp:701-819; dispatch prepareIndexSelect,
 // libreloc/src/Dispatch.cpp:1269-1283).
 //
-// Two paths:
+// Three paths:
 //   upload  the host gathers the selected rows of a host table (through the
 //           leading stages the staging applies) into the pinned ring, and the
 //           device runs the rest of the plan on the dense selected rows
 //           (runtime.cpp). The reference does the same gather on the host
 //           and runs no part of such a plan on the GPU
 //           (libreloc/src/Dispatch.cpp:1397-1404).
+//   table   a long selection from a table no larger than the gathered rows
+//           (table_upload_pays): the table itself crosses PCIe into the wire
+//           arena and the device gathers from it (runtime.cpp).
 //   device  a device-resident table: one gather kernel per launch box, with
 //           the cast fused (k_gather.hip).
 #include <algorithm>
@@ -218,8 +221,13 @@ void host_gather(const Bound &b, const Prepared &p, uint32_t k, const void *tabl
   }
 }
 
-void index_select_device(Context &ctx, BoundHandle &h, const void *table, size_t table_bytes,
-                         void *dst, size_t dst_bytes, hipStream_t stream) {
+bool table_upload_pays(const Bound &b, int64_t gathered_wire) {
+  return b.indexed && static_cast<int64_t>(b.indices.size()) >= kTableUploadRows &&
+         b.table_bytes <= gathered_wire;
+}
+
+int64_t index_select_device(Context &ctx, BoundHandle &h, const void *table, size_t table_bytes,
+                            void *dst, size_t dst_bytes, hipStream_t stream) {
   const Bound &b = *h.bound;
   if (!b.indexed)
     throw Error("plan_mismatch", "index_select needs an indexed plan");
@@ -242,6 +250,7 @@ void index_select_device(Context &ctx, BoundHandle &h, const void *table, size_t
   hipStream_t s = stream ? stream : ctx.compute;
   for (const GatherArgs &a : launches)
     hipcheck(gather_launch(a, g.op, g.nbi, g.iw, g.nt, s), "gather launch");
+  return static_cast<int64_t>(launches.size());
 }
 
 } // namespace relx

@@ -24,7 +24,6 @@
 
 #include "../../include/relx.h"
 
-
 namespace relx {
 
 #define HIPCHECK(expr)                                                                      \
@@ -351,6 +350,8 @@ struct Member {
   const DeviceProgram *dp;
   bool direct;
   size_t wire_off;
+  bool table; // indexed: the table crosses PCIe and the device gathers the rows
+  int64_t arena_bytes; // wire arena bytes of this member
 };
 
 } // namespace
@@ -375,7 +376,7 @@ void execute_members(Context &ctx, int n, BoundHandle *const *bounds, const void
     BoundHandle *h = bounds[i];
     Member m{h, static_cast<const uint8_t *>(srcs[i]), src_bytes[i],
              static_cast<uint8_t *>(dsts[i]), dst_bytes[i], reports ? &reports[i] : nullptr, 0,
-             nullptr, false, 0};
+             nullptr, false, 0, false, 0};
     const bool indexed = h->bound->indexed;
     // An indexed plan's rows are scattered over the table: always staged.
     const bool pinned = !indexed && (opt.source_pinned > 0 ||
@@ -391,6 +392,15 @@ void execute_members(Context &ctx, int n, BoundHandle *const *bounds, const void
     m.dp = &h->program(m.k);
     m.direct = pinned && m.k == 0;
     const Bound &b = *h->bound;
+    m.arena_bytes = m.dp->wire_bytes;
+    if (indexed && hs < 0 && table_upload_pays(b, m.dp->wire_bytes) &&
+        reinterpret_cast<uintptr_t>(m.dst) % b.result_type.width() == 0) {
+      m.table = true;
+      m.k = 0;
+      m.dp = &h->program(0);
+      m.direct = opt.source_pinned > 0 || (opt.source_pinned < 0 && probe_pinned(m.src));
+      m.arena_bytes = b.table_bytes;
+    }
     const int64_t need_src = indexed ? b.table_bytes
                              : b.typed ? b.source_bytes
                                        : m.dp->wire_elems * static_cast<int64_t>(b.layout.element_size);
@@ -404,7 +414,7 @@ void execute_members(Context &ctx, int n, BoundHandle *const *bounds, const void
     if (!m.src || !m.dst)
       throw Error("invalid_view", "null source or destination");
     m.wire_off = wire_total;
-    wire_total += (static_cast<size_t>(m.dp->wire_bytes) + 255) / 256 * 256;
+    wire_total += (static_cast<size_t>(m.arena_bytes) + 255) / 256 * 256;
     ms.push_back(m);
   }
   execute(ctx, ms, opt, total, comp);
@@ -414,15 +424,26 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
              relx_report *total, Completion *comp) {
   size_t wire_total = 0;
   for (const Member &m : ms)
-    wire_total = std::max(wire_total, m.wire_off + static_cast<size_t>(m.dp->wire_bytes));
+    wire_total = std::max(wire_total, m.wire_off + static_cast<size_t>(m.arena_bytes));
   ensure_wire(ctx, wire_total);
 
-  // Chunk plan per member: units of the chunk axis per chunk.
+  // Chunk plan per member: units of the chunk axis per chunk (a table upload:
+  // byte ranges of the table, multiples of 256 bytes).
   size_t max_slot = 0;
   std::vector<ChunkPlan> plans;
   for (const Member &m : ms) {
     const DeviceProgram &dp = *m.dp;
-    const ChunkPlan p = chunk_plan(dp, source_width(*m.h->bound), opt.chunk_bytes, m.direct);
+    ChunkPlan p{};
+    if (m.table) {
+      const int64_t tb = m.h->bound->table_bytes;
+      const int64_t want =
+          opt.chunk_bytes > 0 ? opt.chunk_bytes : default_chunk_bytes(tb, true, m.direct);
+      p.units = tb;
+      p.per_chunk = std::min(tb, std::max<int64_t>(256, want / 256 * 256));
+      p.unit_wire = p.unit_src = 1;
+    } else {
+      p = chunk_plan(dp, source_width(*m.h->bound), opt.chunk_bytes, m.direct);
+    }
     if (!m.direct)
       max_slot = std::max(max_slot, static_cast<size_t>(p.per_chunk * p.unit_wire));
     plans.push_back(p);
@@ -477,7 +498,39 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
                                           : m.h->bound->layout.element_size;
     uint8_t *wire = ctx.wire + m.wire_off;
     int64_t chunks = 0, launches = 0;
-    for (int64_t v0 = 0; v0 < p.units; v0 += p.per_chunk) {
+    if (m.table) {
+      // The table crosses as it is (byte chunks); the gather reads rows from
+      // every chunk, so it waits for both copy streams.
+      const Bound &bd = *m.h->bound;
+      (void)m.h->device_indices(ctx.device); // uploaded before the copies start
+      hipStream_t cs = ctx.copy;
+      for (int64_t b0 = 0; b0 < p.units; b0 += p.per_chunk) {
+        const int64_t n = std::min(p.per_chunk, p.units - b0);
+        cs = ctx.copy_stream(nchunk++);
+        if (m.direct) {
+          HIPCHECK(hipMemcpyAsync(wire + b0, m.src + b0, static_cast<size_t>(n),
+                                  hipMemcpyHostToDevice, cs));
+        } else {
+          uint8_t *s = static_cast<uint8_t *>(ctx.slots[static_cast<size_t>(slot)]);
+          HIPCHECK(hipEventSynchronize(ctx.slot_ev[static_cast<size_t>(slot)]));
+          const uint8_t *from = m.src + b0;
+          ctx.workers->parallel_for(n, int64_t{1} << 18, [&](int64_t x, int64_t y) {
+            std::memcpy(s + x, from + x, static_cast<size_t>(y - x));
+          });
+          HIPCHECK(hipMemcpyAsync(wire + b0, s, static_cast<size_t>(n), hipMemcpyHostToDevice, cs));
+          HIPCHECK(hipEventRecord(ctx.slot_ev[static_cast<size_t>(slot)], cs));
+          slot = (slot + 1) % static_cast<int>(ctx.slots.size());
+        }
+        ++chunks;
+      }
+      if (chunks > 1) {
+        HIPCHECK(hipEventRecord(ctx.copy2_ev, cs == ctx.copy ? ctx.copy2 : ctx.copy));
+        HIPCHECK(hipStreamWaitEvent(cs, ctx.copy2_ev, 0));
+      }
+      launches = index_select_device(ctx, *m.h, wire, static_cast<size_t>(bd.table_bytes), m.dst,
+                                     m.dst_bytes, cs);
+    }
+    for (int64_t v0 = 0; v0 < (m.table ? 0 : p.units); v0 += p.per_chunk) {
       const int64_t v1 = std::min(p.units, v0 + p.per_chunk);
       const int64_t woff = v0 * p.unit_wire, wbytes = (v1 - v0) * p.unit_wire;
       hipStream_t cs = ctx.copy_stream(nchunk++);
@@ -516,15 +569,16 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
     if (m.report) {
       relx_report &r = *m.report;
       std::memset(&r, 0, sizeof(r));
-      const std::string impl =
-          m.k == 0 ? std::string("hip_relayout") : "hip_relayout@" + std::to_string(m.k);
+      const std::string impl = m.table  ? std::string("hip_table_gather")
+                               : m.k == 0 ? std::string("hip_relayout")
+                                          : "hip_relayout@" + std::to_string(m.k);
       std::snprintf(r.implementation, sizeof(r.implementation), "%s", impl.c_str());
       const Bound &b = *m.h->bound;
       r.source_bytes = b.indexed ? b.table_bytes : b.typed ? b.source_bytes : dp.wire_elems * sw;
-      r.wire_bytes = dp.wire_bytes;
+      r.wire_bytes = m.arena_bytes;
       r.destination_bytes = dp.dst_elems * dp.base.wout;
       r.parameter_bytes = b.parameter_bytes;
-      r.payload_bytes_transferred = dp.wire_bytes;
+      r.payload_bytes_transferred = m.arena_bytes;
       r.chunks = chunks;
       r.kernel_launches = launches;
       r.wire_boundary = static_cast<int>(m.k);

@@ -209,9 +209,18 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
                  size_t dst_bytes, const relx_options &opt, relx_report *report);
 
 // Device-resident table -> device destination: the row gather with the
-// plan's cast fused, asynchronous on `stream`.
-void index_select_device(Context &ctx, BoundHandle &h, const void *table, size_t table_bytes,
-                         void *dst, size_t dst_bytes, hipStream_t stream);
+// plan's cast fused, asynchronous on `stream`; returns the launch count.
+int64_t index_select_device(Context &ctx, BoundHandle &h, const void *table, size_t table_bytes,
+                            void *dst, size_t dst_bytes, hipStream_t stream);
+
+// Selected rows from which an upload sends the whole table instead of the
+// gathered rows (when the table is no larger than the gathered wire).
+constexpr int64_t kTableUploadRows = int64_t{1} << 16;
+// The upload of an indexed plan whose gathered wire is `gathered_wire` bytes
+// sends its table and gathers on the device: the table is no larger, and the
+// selection is long enough that the host's random row reads, not the
+// transfer, would set the pace.
+bool table_upload_pays(const Bound &b, int64_t gathered_wire);
 
 // HBM copy ceiling: GB/s (bytes read + written) of a 16-byte vector copy of
 // `bytes`, best of `rounds` runs of `iters` copies over rotating buffers.

@@ -17,8 +17,11 @@ cuda_stages_then_cpu rows with every stage on the device).
 Indexed (wire v2) plans go through `prepare_index_select_program(bound,
 source_view)` (reference prepareIndexSelect, libreloc/src/Dispatch.cpp:
 1269-1283): the source view is the whole host table; the host gathers the
-selected rows while staging and the device runs the rest. They have no
-device-to-host row.
+selected rows while staging and the device runs the rest. The automatic
+row sends the table itself instead when the selection is long (2^16 rows
+or more) and the table is no larger than the gathered rows; the device
+then gathers the rows (report implementation `hip_table_gather`). They
+have no device-to-host row.
 
 Names, argument meaning and error codes follow the reference so that
 `reloc_torch.dispatch` can call these functions in place of `_pyreloc`'s.
@@ -298,7 +301,8 @@ def _report(rep, request):
             "device_temp_bytes": rep["wire_bytes"],
             "artifact_version": 2 if request.template.bound.indexed else 1, "executed": True,
             "host_pipeline": "pinned_ring" if not rep["direct_dma"] else "direct_dma",
-            "host_kernel": "index_select" if request.template.bound.indexed else
+            "host_kernel": "copy" if rep["implementation"] == "hip_table_gather" else
+            "index_select" if request.template.bound.indexed else
             "host_stages" if rep["wire_boundary"] else "copy",
             "host_chunks": rep["chunks"], "host_chunk_bytes": 0, "host_buffers": 0,
             "kernel_launches": rep["kernel_launches"], "staging": []}

@@ -74,6 +74,7 @@ class Plan:
         if N.lib().relx_plan_load(self.blob, len(self.blob), ctypes.byref(h), ctypes.byref(err)):
             _raise(err)
         self._h = h
+        self._free = N.lib().relx_plan_free  # kept: module globals may be gone at exit
 
     @property
     def typed(self):
@@ -87,7 +88,7 @@ class Plan:
     def __del__(self):
         h = getattr(self, "_h", None)
         if h:
-            N.lib().relx_plan_free(h)
+            self._free(h)
             self._h = None
 
 
@@ -221,6 +222,7 @@ class Bound:
 
     def _adopt(self, h):
         self._h = h
+        self._free = N.lib().relx_bound_free  # kept: module globals may be gone at exit
         info = N.relx_bound_info()
         N.lib().relx_bound_query(h, ctypes.byref(info))
         self.info = info
@@ -282,7 +284,7 @@ class Bound:
     def __del__(self):
         h = getattr(self, "_h", None)
         if h:
-            N.lib().relx_bound_free(h)
+            self._free(h)
             self._h = None
 
 
@@ -503,6 +505,7 @@ class Completion:
 
     def __init__(self, handle, reports, total, keep):
         self._h = handle
+        self._free = N.lib().relx_completion_free  # kept: module globals may be gone at exit
         self.reports = reports
         self.total = total
         self._keep = keep
@@ -528,7 +531,7 @@ class Completion:
     def close(self):
         h = getattr(self, "_h", None)
         if h:
-            N.lib().relx_completion_free(h)
+            self._free(h)
             self._h = None
             self._keep = None
 

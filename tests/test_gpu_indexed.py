@@ -164,6 +164,42 @@ def test_cast_rounding_edges(resources):
 
 @pytest.mark.parametrize("sd,rd", PAIRS)
 @pytest.mark.parametrize("pinned", [False, True])
+def test_long_selection_from_a_small_table_sends_the_table(resources, rng, sd, rd, pinned):
+    """A selection of at least 2^16 rows from a table no larger than the
+    gathered rows: the table crosses PCIe as it is (byte chunks, 256-byte
+    multiples) and the device gathers the rows with the cast fused. Explicit
+    host stages keep the host gather."""
+    shape, count = (1500, 7), 70000
+    idx = rng.integers(0, shape[0], count)
+    x = table(rng, sd, shape)
+    b, ob = bind(shape, sd, rd, "int64", idx)
+    want = O.execute_indexed(ob, x)
+    src, keep = x, None
+    if pinned:
+        keep = torch.from_numpy(x.view(np.uint8).reshape(-1).copy()).pin_memory()
+        src = keep.numpy().view(x.dtype).reshape(shape)
+    for chunk in (0, 4096, 4000):
+        say("table upload", sd, rd, "pinned" if pinned else "pageable", "chunk", chunk)
+        out = empty_out(b, rd)
+        rep = resources.execute_h2d(b, src.ctypes.data, src.nbytes, out.data_ptr(),
+                                    out.numel() * out.element_size(), chunk_bytes=chunk)
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy().view(np.uint8).reshape(-1), want), chunk
+        assert rep["implementation"] == "hip_table_gather"
+        assert rep["wire_bytes"] == rep["payload_bytes_transferred"] == x.nbytes
+        assert rep["direct_dma"] == (1 if pinned else 0)
+        assert rep["chunks"] == (1 if chunk == 0 else -(-x.nbytes // (chunk // 256 * 256)))
+    say("host gather kept", sd, rd)
+    out = empty_out(b, rd)
+    rep = resources.execute_h2d(b, src.ctypes.data, src.nbytes, out.data_ptr(),
+                                out.numel() * out.element_size(), host_stages=0)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint8).reshape(-1), want)
+    assert rep["implementation"] == "hip_relayout"
+
+
+@pytest.mark.parametrize("sd,rd", PAIRS)
+@pytest.mark.parametrize("pinned", [False, True])
 def test_chunked_uploads_split_rows(resources, rng, sd, rd, pinned):
     """Chunks of a few KiB cut selected rows at arbitrary elements; every
     host boundary, pinned and pageable tables."""
