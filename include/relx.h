@@ -196,7 +196,7 @@ typedef struct relx_options {
 /* Scalar report of one call (reference dispatch::Report,
  * libreloc/include/reloc/Dispatch.h:104-124). */
 typedef struct relx_report {
-  char implementation[40]; /* e.g. "hip_relayout", "hip_relayout@1" */
+  char implementation[40]; /* "hip_relayout", "hip_relayout@k", "hip_table_gather" */
   int64_t source_bytes;
   int64_t wire_bytes;
   int64_t destination_bytes;
