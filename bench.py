@@ -492,8 +492,10 @@ def summarize_pmc(fetch_dir, write_dir, probe):
 
 def one_config(torch, ctx, P, name, args, h2d_ceiling):
     case = make_case(name)
-    ms_step, kms = device_rate(torch, ctx, case.bound, case.wire_bytes, case.out_bytes,
-                               max(50, args.steps // 10), 20)
+    # as many warmup launches as timed ones: after the small end-to-end calls
+    # before it, a short warmup left small kernels timed at lower clocks
+    steps = max(50, args.steps // 10)
+    ms_step, kms = device_rate(torch, ctx, case.bound, case.wire_bytes, case.out_bytes, steps, steps)
     alg = case.wire_bytes + case.out_bytes + case.bound.parameter_bytes
     p50, p95, rep = e2e_rate(torch, ctx, case, max(10, args.e2e_samples // 2), pinned=False)
     q50, q95, prep = e2e_rate(torch, ctx, case, max(10, args.e2e_samples // 2), pinned=True)
