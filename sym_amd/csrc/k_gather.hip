@@ -2,7 +2,7 @@
 // axis 0 of a device-resident table, with the plan's optional cast fused).
 //
 // Each lane moves one vector item (up to 16 bytes of a row) at a time, two
-// items 64 apart per trip, like the stream kernel: a wave covers 64
+// or four items 64 apart per trip (gather_items), like the stream kernel: a wave covers 64
 // consecutive items of the output, which are consecutive items of one or a
 // few source rows, so loads and stores stay contiguous per row. The row index
 // of an item comes from one division by the row length in items; lanes of the
@@ -47,6 +47,11 @@ constexpr int gather_out_bytes(int op, int nbi) {
   return op == kGatherCopy ? nbi : op == kGatherF32F16 ? nbi / 2 : nbi * 2;
 }
 
+// Items per lane: a widening gather loads half its store bytes per item and
+// takes four items 64 apart (f16 -> f32 rows of 2 KiB: 75.7 -> 72.5 us); the
+// others take two (four slowed them by 3-4%).
+constexpr int gather_items(int op) { return op == kGatherF16F32 ? 4 : 2; }
+
 // One item's value conversion: NBI source bytes -> the item's output bytes.
 template <int OP, int NBI> __device__ __forceinline__ vec4 convert(const vec4 &in) {
   if constexpr (OP == kGatherCopy) {
@@ -71,7 +76,7 @@ template <int OP, int NBI> __device__ __forceinline__ vec4 convert(const vec4 &i
 template <int OP, int NBI, int IW, bool NTL>
 __global__ __launch_bounds__(kBlock) void k_gather(GatherArgs a) {
   constexpr int NBO = gather_out_bytes(OP, NBI);
-  constexpr int U = 2;
+  constexpr int U = gather_items(OP);
   constexpr bool NTS = RELX_GATHER_NT_STORE;
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = (blockIdx.x * kBlock + threadIdx.x) >> 6;
@@ -111,7 +116,8 @@ __global__ __launch_bounds__(kBlock) void k_gather(GatherArgs a) {
 
 template <int OP, int NBI>
 hipError_t gather_iw(const GatherArgs &a, int iw, bool nt, hipStream_t s) {
-  const dim3 grid(grid_for((static_cast<int64_t>(a.work) + 1) / 2)), block(kBlock);
+  constexpr int U = gather_items(OP);
+  const dim3 grid(grid_for((static_cast<int64_t>(a.work) + U - 1) / U)), block(kBlock);
   if constexpr (NBI >= 8) {
     if (nt) {
       if (iw == 4)
