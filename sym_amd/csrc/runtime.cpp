@@ -33,93 +33,6 @@ namespace relx {
       throw Error("backend_failure", std::string(#expr) + ": " + hipGetErrorString(e_));    \
   } while (0)
 
-// ------------------------------------------------------------ workers
-
-namespace {
-
-// How long an idle worker, or a caller waiting for its workers, spins
-// before blocking.
-constexpr auto kSpin = std::chrono::microseconds(200);
-
-template <class Pred> bool spin_until(Pred done) {
-  const auto t0 = std::chrono::steady_clock::now();
-  for (unsigned i = 0; !done(); ++i) {
-    _mm_pause();
-    if ((i & 63) == 63 && std::chrono::steady_clock::now() - t0 > kSpin)
-      return done();
-  }
-  return true;
-}
-
-} // namespace
-
-Workers::Workers(unsigned threads) {
-  for (unsigned i = 1; i < std::max(1u, threads); ++i)
-    threads_.emplace_back([this, i] { loop(i); });
-}
-
-Workers::~Workers() {
-  {
-    std::lock_guard<std::mutex> g(mu_);
-    stop_.store(true);
-  }
-  go_.notify_all();
-  for (auto &t : threads_)
-    t.join();
-}
-
-void Workers::loop(unsigned id) {
-  uint64_t seen = 0;
-  for (;;) {
-    auto ready = [&] { return stop_.load() || generation_.load(std::memory_order_acquire) != seen; };
-    if (!spin_until(ready)) {
-      std::unique_lock<std::mutex> g(mu_);
-      go_.wait(g, ready);
-    }
-    if (stop_.load())
-      return;
-    seen = generation_.load(std::memory_order_acquire);
-    const std::pair<int64_t, int64_t> r = ranges_[id];
-    const std::function<void(int64_t, int64_t)> *fn = fn_;
-    if (r.second > r.first)
-      (*fn)(r.first, r.second);
-    if (pending_.fetch_sub(1, std::memory_order_acq_rel) == 1) {
-      std::lock_guard<std::mutex> g(mu_);
-      done_.notify_one();
-    }
-  }
-}
-
-void Workers::parallel_for(int64_t n, int64_t grain,
-                           const std::function<void(int64_t, int64_t)> &fn) {
-  const unsigned total = size();
-  const int64_t parts =
-      std::max<int64_t>(1, std::min<int64_t>(total, n / std::max<int64_t>(1, grain)));
-  if (parts <= 1 || threads_.empty()) {
-    if (n > 0)
-      fn(0, n);
-    return;
-  }
-  {
-    // Workers read the ranges after they see the new generation (release
-    // here, acquire there); the lock orders it with a worker going to sleep.
-    std::lock_guard<std::mutex> g(mu_);
-    ranges_.assign(total, {0, 0});
-    for (int64_t i = 0; i < parts; ++i)
-      ranges_[static_cast<size_t>(i)] = {n * i / parts, n * (i + 1) / parts};
-    fn_ = &fn;
-    pending_.store(static_cast<unsigned>(threads_.size()), std::memory_order_relaxed);
-    generation_.fetch_add(1, std::memory_order_release);
-  }
-  go_.notify_all();
-  fn(ranges_[0].first, ranges_[0].second);
-  auto finished = [&] { return pending_.load(std::memory_order_acquire) == 0; };
-  if (!spin_until(finished)) {
-    std::unique_lock<std::mutex> g(mu_);
-    done_.wait(g, finished);
-  }
-}
-
 // ------------------------------------------------------------ staging
 
 namespace {

@@ -1,5 +1,5 @@
 // runtime.h - internal declarations shared by program.cpp, runtime.cpp,
-// staging.cpp and capi.cpp.
+// indexed.cpp and capi.cpp.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -18,6 +18,7 @@
 #include "../../include/relx.h"
 #include "plan.h"
 #include "program.h"
+#include "workers.h"
 
 namespace relx {
 
@@ -112,32 +113,6 @@ struct ChunkPlan {
 int64_t default_chunk_bytes(int64_t total, bool h2d, bool direct);
 uint32_t source_width(const Bound &b);
 ChunkPlan chunk_plan(const DeviceProgram &dp, uint32_t src_width, int64_t chunk_bytes, bool direct);
-
-// ------------------------------------------------------------ workers
-
-// Persistent worker threads; parallel_for splits [0, n) into contiguous
-// ranges (no smaller than `grain`), the calling thread runs one of them.
-// Between jobs the workers (and the caller, waiting for them) spin for a
-// short while before sleeping: a pipeline hands them one job per chunk, and
-// waking sleeping threads costs tens of microseconds per job.
-class Workers {
-public:
-  explicit Workers(unsigned threads);
-  ~Workers();
-  unsigned size() const { return static_cast<unsigned>(threads_.size()) + 1; }
-  void parallel_for(int64_t n, int64_t grain, const std::function<void(int64_t, int64_t)> &fn);
-
-private:
-  void loop(unsigned id);
-  std::vector<std::thread> threads_;
-  std::mutex mu_;
-  std::condition_variable go_, done_;
-  const std::function<void(int64_t, int64_t)> *fn_ = nullptr;
-  std::vector<std::pair<int64_t, int64_t>> ranges_;
-  std::atomic<uint64_t> generation_{0};
-  std::atomic<unsigned> pending_{0};
-  std::atomic<bool> stop_{false};
-};
 
 // Host staging transform: source elements [e0, e1) at boundary 0 -> wire
 // elements at boundary `k` (leading per-tensor stages applied elementwise).
