@@ -279,6 +279,14 @@ def device_rate(torch, ctx, bound, wire_bytes, out_bytes, steps, warmup, sets=No
     for i in range(warmup):
         ctx.relayout_device(bound, wires[i % sets].data_ptr(), outs[i % sets].data_ptr(), stream=sp)
     torch.cuda.synchronize()
+    # and at least 30 ms of back-to-back launches: after idle stretches (the
+    # latency-bound end-to-end calls before it) the clocks take a few ms to
+    # come back, which a short timed region would see
+    t_warm = time.perf_counter()
+    while time.perf_counter() - t_warm < 0.03:
+        for i in range(50):
+            ctx.relayout_device(bound, wires[i % sets].data_ptr(), outs[i % sets].data_ptr(), stream=sp)
+        torch.cuda.synchronize()
     # whole-job: K steps bracketed by synchronize
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
@@ -492,10 +500,8 @@ def summarize_pmc(fetch_dir, write_dir, probe):
 
 def one_config(torch, ctx, P, name, args, h2d_ceiling):
     case = make_case(name)
-    # as many warmup launches as timed ones: after the small end-to-end calls
-    # before it, a short warmup left small kernels timed at lower clocks
-    steps = max(50, args.steps // 10)
-    ms_step, kms = device_rate(torch, ctx, case.bound, case.wire_bytes, case.out_bytes, steps, steps)
+    ms_step, kms = device_rate(torch, ctx, case.bound, case.wire_bytes, case.out_bytes,
+                               max(50, args.steps // 10), 20)
     alg = case.wire_bytes + case.out_bytes + case.bound.parameter_bytes
     p50, p95, rep = e2e_rate(torch, ctx, case, max(10, args.e2e_samples // 2), pinned=False)
     q50, q95, prep = e2e_rate(torch, ctx, case, max(10, args.e2e_samples // 2), pinned=True)
