@@ -90,19 +90,22 @@ __global__ __launch_bounds__(kBlock) void k_gather(GatherArgs a) {
     bool live[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint32_t i = base + 64u * u;
-      live[u] = u == 0 || i < a.work;
-      if (live[u]) {
-        const uint32_t r = fdiv(i, a.per_row);
-        const uint32_t c = i - r * a.row_items;
-        int64_t row;
-        if constexpr (IW == 4)
-          row = reinterpret_cast<const int32_t *>(a.idx)[r];
-        else
-          row = reinterpret_cast<const int64_t *>(a.idx)[r];
-        const uint64_t item = static_cast<uint64_t>(row) * a.row_items + c;
-        in[u] = gload<NBI, NTL>(a.table + item * NBI);
-      }
+      const uint32_t i0 = base + 64u * u;
+      live[u] = u == 0 || i0 < a.work;
+      // a lane past the end re-reads its first item: every load of the trip
+      // is unconditional, so the index and table loads of all items issue
+      // back to back (a load under a per-lane branch is waited for before
+      // the branch ends)
+      const uint32_t i = live[u] ? i0 : base;
+      const uint32_t r = fdiv(i, a.per_row);
+      const uint32_t c = i - r * a.row_items;
+      int64_t row;
+      if constexpr (IW == 4)
+        row = reinterpret_cast<const int32_t *>(a.idx)[r];
+      else
+        row = reinterpret_cast<const int64_t *>(a.idx)[r];
+      const uint64_t item = static_cast<uint64_t>(row) * a.row_items + c;
+      in[u] = gload<NBI, NTL>(a.table + item * NBI);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {

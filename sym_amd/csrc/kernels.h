@@ -193,6 +193,13 @@ template <bool NT> __device__ __forceinline__ void st16(vec4 *p, const vec4 &v) 
 typedef uint32_t vec2 __attribute__((ext_vector_type(2)));
 
 // NB-byte (4, 8 or 16) access into the low words of a 16-byte vector.
+// 16 readable bytes for loads whose value is not used (a lane past the end
+// of its launch, or a pad plane): pointing such a load here instead of
+// branching around it keeps every load of a trip unconditional, so they
+// issue back to back. A load under a per-lane branch makes the compiler wait
+// for it before the branch ends, which serialises the loads.
+__device__ __align__(16) uint8_t g_unused_src[16];
+
 template <int NB, bool NT> __device__ __forceinline__ vec4 ld_n(const uint8_t *p) {
   vec4 r = {0u, 0u, 0u, 0u};
   if constexpr (NB == 16) {
@@ -728,8 +735,8 @@ __global__ __launch_bounds__(kBlock) void k_interleave(KArgs a) {
       for (int ch = 0; ch < CP; ++ch) {
         const int32_t vc = ch - a.i_loc;
         valid[u][ch] = live[u] && !pad && static_cast<uint32_t>(vc) < static_cast<uint32_t>(a.i_vc);
-        if (valid[u][ch])
-          in[u][ch] = ld_n<BI, NTL>(a.src + (sbase + vc * a.i_ssc + p0[u]) * WIN);
+        in[u][ch] = ld_n<BI, NTL>(valid[u][ch] ? a.src + (sbase + vc * a.i_ssc + p0[u]) * WIN
+                                               : g_unused_src);
       }
     }
     // one body per item with a compile-time index (a runtime-indexed loop
