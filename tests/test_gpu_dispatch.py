@@ -260,6 +260,30 @@ def test_call_after_submitted_group_waits_for_its_wire(resources, rng, pinned):
     ca.close()
 
 
+def test_device_to_host_after_a_submitted_group(resources, rng):
+    """A device-to-host call writes the wire arena that a submitted upload
+    may still be reading: it is ordered after that upload."""
+    ea, oa, wa, ka = _expert_group(rng, 2048, 2048, 3, True)
+    rows, cols = 256, 512
+    q, s = W.int8_weight(rows, cols, rng), W.scales(cols, rng)
+    b = P.Bound(P.Plan(W.c3_plan().blob), {"s0": rows, "s1": cols}, W.param("scale", s))
+    qd = torch.from_numpy(q.view(np.uint8).copy()).cuda()
+    dev = torch.empty(rows * cols * 2, dtype=torch.uint8, device="cuda")
+    resources.execute_h2d(b, q.ctypes.data, q.nbytes, dev.data_ptr(), dev.numel())
+    torch.cuda.synchronize()
+    want = dev.cpu().numpy()
+    say("submit, then a device-to-host call on the same resources")
+    ca = P.submit_dispatch_group(P.prepare_dispatch_group(ea), resources=resources,
+                                 owners=(tuple(ka), tuple(oa)))
+    out = np.empty(rows * cols * 2, np.uint8)
+    resources.execute_d2h(b, qd.data_ptr(), q.nbytes, out.ctypes.data, out.nbytes)
+    assert np.array_equal(out, want)
+    ca.wait()
+    for o, w in zip(oa, wa):
+        assert np.array_equal(o.cpu().numpy().view(np.uint16), w)
+    ca.close()
+
+
 def test_abandoned_completion_drains(resources, rng):
     e, o, w, k = _expert_group(rng, 256, 256, 2, True)
     c = P.submit_dispatch_group(P.prepare_dispatch_group(e), resources=resources,

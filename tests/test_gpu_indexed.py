@@ -298,6 +298,35 @@ def test_device_gather_rejects_bad_buffers(resources):
         resources.execute_d2h(b, t.data_ptr(), 128, np.zeros(16, np.float16).ctypes.data, 32)
 
 
+@pytest.mark.parametrize("table_first", [True, False])
+def test_table_upload_member_in_a_group(resources, rng, table_first):
+    """A long selection from a small table (sent whole, gathered on the
+    device) next to an ordinary typed member, in either order, through the
+    dispatch API: the two members' chunks go to different copy streams."""
+    say("group with a table upload", "first" if table_first else "second")
+    shape, count = (700, 9), 80000
+    idx = rng.integers(0, shape[0], count)
+    x = rng.standard_normal(shape).astype(np.float32)
+    b, ob = bind(shape, "float32", "float16", "int64", idx)
+    from sym_amd.encoder import Cast, encode
+    y = rng.standard_normal((129, 65)).astype(np.float32)
+    tb = P.bind_typed(P.load_typed_plan(encode([129, 65], "float32", [Cast("float16")]).blob), {}, {})
+    o1 = torch.empty((count, 9), dtype=torch.float16, device="cuda")
+    o2 = torch.empty((129, 65), dtype=torch.float16, device="cuda")
+    prog = P.prepare_index_select_program(b, host_view(x))
+    items = [(prog, host_view(x), device_view(o1), "h2d"), (tb, host_view(y), device_view(o2), "h2d")]
+    if not table_first:
+        items.reverse()
+    g = P.prepare_dispatch_group(items)
+    rep = P.execute_dispatch_group(g, resources=resources, gather_threads=3)
+    torch.cuda.synchronize()
+    assert np.array_equal(o1.cpu().numpy().view(np.uint8).reshape(-1), O.execute_indexed(ob, x))
+    assert np.array_equal(o2.cpu().numpy(), y.astype(np.float16))
+    it = rep["items"][0 if table_first else 1]
+    assert it["implementation"] == "hip_table_gather" and it["host_kernel"] == "copy"
+    assert it["payload_bytes_transferred"] == x.nbytes and it["artifact_version"] == 2
+
+
 def test_indexed_member_in_a_group(resources, rng):
     """An indexed upload and a typed cast in one group schedule."""
     say("group")
