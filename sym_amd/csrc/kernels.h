@@ -337,7 +337,10 @@ __global__ __launch_bounds__(kBlock) __attribute__((unused)) void k_generic(KArg
         else if (s.mode == kChanExpr)
           c = eval_channel(a, s, dof);
         if (c < 0 || c >= s.len) {
-          atomicExch(status, 1); // channel_out_of_range, reported by the host
+          // channel_out_of_range, reported by the host: a plain store (the
+          // flag is in pinned host memory, where atomics would need PCIe
+          // atomics; every writer stores the same 1)
+          *static_cast<volatile int32_t *>(status) = 1;
           c = 0;
         }
         x = apply(s, static_cast<uint32_t>(x), static_cast<uint32_t>(c), a.pf, a.pi);

@@ -291,3 +291,47 @@ def test_abandoned_completion_drains(resources, rng):
     c.close()  # waits for the work before releasing the handle
     for out, want in zip(o, w):
         assert np.array_equal(out.cpu().numpy().view(np.uint16), want)
+
+
+# ------------------------------------------------------------ error flag
+
+def _shifted_channel_plan(monkeypatch):
+    """A per-row dequantize whose channel expression is `row + 1`: the last
+    row selects a channel one past its scale table (the element-wise kernel's
+    range check, reported through the call's status flag)."""
+    from sym_amd import encoder as EN
+    orig = EN._stage
+
+    def shifted(op, dtype, shape, rank):
+        st = orig(op, dtype, shape, rank)
+        if st.channel is not None:
+            st.channel = EN.E("add", st.channel, EN.E.c(1))
+        return st
+
+    monkeypatch.setattr(EN, "_stage", shifted)
+    scales = EN.InlineParam((0.5, 0.25, 0.125, 2.0), "float32", 1)
+    return EN.encode([4, 6], "int8", [EN.Dequantize(scales, axis=0)])
+
+
+def test_channel_outside_the_table_is_reported(resources, rng, monkeypatch):
+    plan = _shifted_channel_plan(monkeypatch)
+    monkeypatch.undo()  # the plans below come from the ordinary encoder
+    q = rng.integers(-128, 128, (4, 6), dtype=np.int8)
+    with pytest.raises(O.ExecutionError, match="channel_out_of_range"):
+        O.run_typed(plan.blob, {}, {}, q)
+    b = P.bind_typed(P.load_typed_plan(plan.blob), {}, {})
+    out = torch.empty((4, 6), dtype=torch.float32, device="cuda")
+    say("channel out of range, h2d then d2h")
+    with pytest.raises(P.TransferError, match="channel_out_of_range"):
+        resources.execute_h2d(b, q.ctypes.data, q.nbytes, out.data_ptr(), out.numel() * 4)
+    qd = torch.from_numpy(q.view(np.uint8).copy()).cuda()
+    host = np.empty(24, np.float32)
+    with pytest.raises(P.TransferError, match="channel_out_of_range"):
+        resources.execute_d2h(b, qd.data_ptr(), q.nbytes, host.ctypes.data, host.nbytes)
+    # the flag belongs to its call: a good call on the same resources is clean
+    rows, cols = 64, 128
+    q2, s2 = W.int8_weight(rows, cols, rng), W.scales(cols, rng)
+    b2 = P.Bound(P.Plan(W.c3_plan().blob), {"s0": rows, "s1": cols}, W.param("scale", s2))
+    dev = torch.empty(rows * cols * 2, dtype=torch.uint8, device="cuda")
+    resources.execute_h2d(b2, q2.ctypes.data, q2.nbytes, dev.data_ptr(), dev.numel())
+    torch.cuda.synchronize()
