@@ -187,12 +187,29 @@ int32_t read_status(const int32_t *status) {
 
 void clear_status(int32_t *status) { *static_cast<volatile int32_t *>(status) = 0; }
 
+// `s` waits for the work enqueued so far on the other copy streams among
+// the first `used` (chunk c goes to stream c mod kCopyStreams).
+void join_copy_streams(Context &ctx, hipStream_t s, int64_t used) {
+  for (int i = 0; i < kCopyStreams && i < used; ++i) {
+    if (ctx.copies[i] == s)
+      continue;
+    HIPCHECK(hipEventRecord(ctx.join_ev[i], ctx.copies[i]));
+    HIPCHECK(hipStreamWaitEvent(s, ctx.join_ev[i], 0));
+  }
+}
+
+// Every copy stream waits for `ev`.
+void copy_streams_wait(Context &ctx, hipEvent_t ev) {
+  for (hipStream_t c : ctx.copies)
+    HIPCHECK(hipStreamWaitEvent(c, ev, 0));
+}
+
 void ensure_wire(Context &ctx, size_t bytes) {
   if (ctx.wire_cap >= bytes)
     return;
   if (ctx.wire) {
-    HIPCHECK(hipStreamSynchronize(ctx.copy));
-    HIPCHECK(hipStreamSynchronize(ctx.copy2));
+    for (hipStream_t c : ctx.copies)
+      HIPCHECK(hipStreamSynchronize(c));
     HIPCHECK(hipStreamSynchronize(ctx.compute));
     HIPCHECK(hipFree(ctx.wire));
     ctx.wire = nullptr;
@@ -225,7 +242,7 @@ void ensure_ring(Context &ctx, int n, size_t slot_bytes) {
     ctx.slots.push_back(p);
     hipEvent_t e;
     HIPCHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
-    HIPCHECK(hipEventRecord(e, ctx.copy)); // a recorded, completed state
+    HIPCHECK(hipEventRecord(e, ctx.copies[0])); // a recorded, completed state
     ctx.slot_ev.push_back(e);
   }
 }
@@ -373,7 +390,7 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
   int64_t total_chunks = 0;
   for (const ChunkPlan &p : plans)
     total_chunks += (p.units + p.per_chunk - 1) / p.per_chunk;
-  const bool two_streams = total_chunks > 1; // else the second copy stream stays idle
+  const bool two_streams = total_chunks > 1; // else one copy stream does everything
   const int nslots = opt.n_buffers > 0 ? opt.n_buffers : 3;
   if (max_slot)
     ensure_ring(ctx, nslots, max_slot);
@@ -385,16 +402,13 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
 
   // Each chunk's kernel runs on the stream that copied the chunk (a kernel
   // behind a copy on one stream starts about 10 us sooner than one ordered
-  // by an event from another stream); both copy streams join at the end.
-  if (ctx.unsynced) { // the previous call may still read the wire arena
-    HIPCHECK(hipStreamWaitEvent(ctx.copy, ctx.done_ev, 0));
-    HIPCHECK(hipStreamWaitEvent(ctx.copy2, ctx.done_ev, 0));
-  }
+  // by an event from another stream); the copy streams join at the end.
+  if (ctx.unsynced) // the previous call may still read the wire arena
+    copy_streams_wait(ctx, ctx.done_ev);
   hipStream_t caller = reinterpret_cast<hipStream_t>(opt.caller_stream);
   if (caller) {
     HIPCHECK(hipEventRecord(ctx.start_ev, caller));
-    HIPCHECK(hipStreamWaitEvent(ctx.copy, ctx.start_ev, 0));
-    HIPCHECK(hipStreamWaitEvent(ctx.copy2, ctx.start_ev, 0));
+    copy_streams_wait(ctx, ctx.start_ev);
   }
   bool any_generic = false;
   for (const Member &m : ms)
@@ -420,7 +434,7 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
       // every chunk, so it waits for both copy streams.
       const Bound &bd = *m.h->bound;
       (void)m.h->device_indices(ctx.device); // uploaded before the copies start
-      hipStream_t cs = ctx.copy;
+      hipStream_t cs = ctx.copies[0];
       for (int64_t b0 = 0; b0 < p.units; b0 += p.per_chunk) {
         const int64_t n = std::min(p.per_chunk, p.units - b0);
         cs = ctx.copy_stream(nchunk++);
@@ -440,10 +454,8 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
         }
         ++chunks;
       }
-      if (chunks > 1) {
-        HIPCHECK(hipEventRecord(ctx.copy2_ev, cs == ctx.copy ? ctx.copy2 : ctx.copy));
-        HIPCHECK(hipStreamWaitEvent(cs, ctx.copy2_ev, 0));
-      }
+      if (chunks > 1)
+        join_copy_streams(ctx, cs, nchunk);
       launches = index_select_device(ctx, *m.h, wire, static_cast<size_t>(bd.table_bytes), m.dst,
                                      m.dst_bytes, cs);
     }
@@ -509,13 +521,10 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
       sum.kernel_launches += r.kernel_launches;
     }
   }
-  // join on the stream of the last chunk (the other one is usually done)
-  hipStream_t last = nchunk > 0 ? ctx.copy_stream(nchunk - 1) : ctx.copy;
-  hipStream_t other = last == ctx.copy ? ctx.copy2 : ctx.copy;
-  if (two_streams) {
-    HIPCHECK(hipEventRecord(ctx.copy2_ev, other));
-    HIPCHECK(hipStreamWaitEvent(last, ctx.copy2_ev, 0));
-  }
+  // join on the stream of the last chunk (the others are usually done)
+  hipStream_t last = nchunk > 0 ? ctx.copy_stream(nchunk - 1) : ctx.copies[0];
+  if (two_streams)
+    join_copy_streams(ctx, last, nchunk);
   HIPCHECK(hipEventRecord(ctx.done_ev, last));
   if (caller)
     HIPCHECK(hipStreamWaitEvent(caller, ctx.done_ev, 0));
@@ -637,15 +646,13 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
   }
   if (ctx.unsynced) { // a submitted upload may still read the arena this call writes
     HIPCHECK(hipStreamWaitEvent(ctx.compute, ctx.done_ev, 0));
-    HIPCHECK(hipStreamWaitEvent(ctx.copy, ctx.done_ev, 0));
-    HIPCHECK(hipStreamWaitEvent(ctx.copy2, ctx.done_ev, 0));
+    copy_streams_wait(ctx, ctx.done_ev);
   }
   hipStream_t caller = reinterpret_cast<hipStream_t>(opt.caller_stream);
   if (caller) { // the source is produced on the caller's stream
     HIPCHECK(hipEventRecord(ctx.start_ev, caller));
     HIPCHECK(hipStreamWaitEvent(ctx.compute, ctx.start_ev, 0));
-    HIPCHECK(hipStreamWaitEvent(ctx.copy, ctx.start_ev, 0));
-    HIPCHECK(hipStreamWaitEvent(ctx.copy2, ctx.start_ev, 0));
+    copy_streams_wait(ctx, ctx.start_ev);
   }
   int32_t *status = ctx.status + (ctx.status_next++ % kStatusSlots);
   if (dp.family == kFamGeneric)
@@ -709,9 +716,8 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
   }
   while (next < pending.size())
     consume(pending[next++]);
-  HIPCHECK(hipEventRecord(ctx.copy2_ev, ctx.copy2));
-  HIPCHECK(hipStreamWaitEvent(ctx.copy, ctx.copy2_ev, 0));
-  HIPCHECK(hipEventRecord(ctx.done_ev, ctx.copy));
+  join_copy_streams(ctx, ctx.copies[0], chunks);
+  HIPCHECK(hipEventRecord(ctx.done_ev, ctx.copies[0]));
   if (caller)
     HIPCHECK(hipStreamWaitEvent(caller, ctx.done_ev, 0));
   HIPCHECK(hipEventSynchronize(ctx.done_ev));
@@ -743,12 +749,13 @@ std::unique_ptr<Context> make_context(int device, int64_t max_retained) {
   ctx->device = device;
   ctx->max_retained = max_retained;
   DeviceGuard guard(device);
-  HIPCHECK(hipStreamCreateWithFlags(&ctx->copy, hipStreamNonBlocking));
-  HIPCHECK(hipStreamCreateWithFlags(&ctx->copy2, hipStreamNonBlocking));
+  for (int i = 0; i < kCopyStreams; ++i) {
+    HIPCHECK(hipStreamCreateWithFlags(&ctx->copies[i], hipStreamNonBlocking));
+    HIPCHECK(hipEventCreateWithFlags(&ctx->join_ev[i], hipEventDisableTiming));
+  }
   HIPCHECK(hipStreamCreateWithFlags(&ctx->compute, hipStreamNonBlocking));
   HIPCHECK(hipEventCreateWithFlags(&ctx->start_ev, hipEventDisableTiming));
   HIPCHECK(hipEventCreateWithFlags(&ctx->done_ev, hipEventDisableTiming));
-  HIPCHECK(hipEventCreateWithFlags(&ctx->copy2_ev, hipEventDisableTiming));
   for (int i = 0; i < kChunkEvents; ++i) {
     hipEvent_t e;
     HIPCHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
@@ -770,13 +777,13 @@ Context::~Context() {
   }
 }
 
-// Drain both streams. False when completion cannot be proven.
+// Drain every stream. False when completion cannot be proven.
 bool drain(Context &ctx) {
   DeviceGuard guard(ctx.device);
-  const bool a = hipStreamSynchronize(ctx.copy) == hipSuccess;
-  const bool a2 = hipStreamSynchronize(ctx.copy2) == hipSuccess;
-  const bool b = hipStreamSynchronize(ctx.compute) == hipSuccess;
-  return a && a2 && b;
+  bool ok = hipStreamSynchronize(ctx.compute) == hipSuccess;
+  for (hipStream_t c : ctx.copies)
+    ok = hipStreamSynchronize(c) == hipSuccess && ok;
+  return ok;
 }
 
 void destroy_context(Context &ctx) {
@@ -791,16 +798,16 @@ void destroy_context(Context &ctx) {
     (void)hipEventDestroy(ctx.start_ev);
   if (ctx.done_ev)
     (void)hipEventDestroy(ctx.done_ev);
-  if (ctx.copy2_ev)
-    (void)hipEventDestroy(ctx.copy2_ev);
+  for (hipEvent_t e : ctx.join_ev)
+    if (e)
+      (void)hipEventDestroy(e);
   if (ctx.wire)
     (void)hipFree(ctx.wire);
   ctx.wire = nullptr;
   ctx.wire_cap = 0;
-  if (ctx.copy)
-    (void)hipStreamDestroy(ctx.copy);
-  if (ctx.copy2)
-    (void)hipStreamDestroy(ctx.copy2);
+  for (hipStream_t c : ctx.copies)
+    if (c)
+      (void)hipStreamDestroy(c);
   if (ctx.compute)
     (void)hipStreamDestroy(ctx.compute);
   ctx.slots.clear();
