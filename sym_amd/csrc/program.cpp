@@ -453,7 +453,9 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
         if (a.ss[i] == 1 && a.vext[i] > 1)
           qa = i;
       const int VI = 16 / win, VO = 16 / wout;
-      if (qa >= 0 && a.vext[qa] % 64 == 0 && a.vext[r - 1] % 64 == 0 && a.ss[r - 1] % VI == 0 &&
+      // extents need not be multiples of 64: the launches split off the
+      // partial tiles at the q and c edges and run them element-wise
+      if (qa >= 0 && a.vext[qa] >= 64 && a.vext[r - 1] >= 64 && a.ss[r - 1] % VI == 0 &&
           a.ds[qa] % VO == 0) {
         bool ok = true;
         for (int i = 0; i < r - 1; ++i)
@@ -700,6 +702,26 @@ Level axis_level(const KArgs &a, const Box &b, int i, int64_t unit) {
   return l;
 }
 
+int64_t box_elements(const Box &b, int rank) {
+  int64_t n = 1;
+  for (int i = 0; i < rank; ++i)
+    n *= b.ext[i];
+  return n;
+}
+
+// Arguments of an edge box: the element-wise kernel over the box.
+KArgs edge_args(const DeviceProgram &dp, const Box &b) {
+  KArgs a = dp.base;
+  for (int i = 0; i < a.rank; ++i) {
+    a.box_lo[i] = b.lo[i];
+    a.box_ext[i] = b.ext[i];
+  }
+  a.work64 = box_elements(b, a.rank);
+  a.work = 0;
+  a.edge_box = 1;
+  return a;
+}
+
 KArgs launch_args(const DeviceProgram &dp, const Box &b) {
   KArgs a = dp.base;
   const int r = a.rank;
@@ -823,13 +845,42 @@ std::vector<KArgs> prefix_launches(const DeviceProgram &dp, const int64_t *fixed
     b.lo[axis] = plo;
     b.ext[axis] = phi - plo;
   }
-  std::vector<Box> boxes;
-  split_box(dp, b, boxes);
   std::vector<KArgs> out;
-  out.reserve(boxes.size());
+  // A transpose box whose q or c extent is not a multiple of the tile: the
+  // whole tiles go to the tile kernel, the strips past them (the q strip
+  // over the whole c range, the c strip beside the whole q tiles) to the
+  // element-wise kernel. Box starts on those axes are multiples of 64
+  // (chunks and splits keep the tile alignment).
+  std::vector<Box> edges;
+  if (dp.family == kFamTranspose) {
+    const int q = dp.qa, c = dp.ca;
+    const int64_t mq = b.ext[q] / 64 * 64, mc = b.ext[c] / 64 * 64;
+    if (mq < b.ext[q]) {
+      Box e = b;
+      e.lo[q] = b.lo[q] + mq;
+      e.ext[q] = b.ext[q] - mq;
+      edges.push_back(e);
+    }
+    if (mc < b.ext[c] && mq > 0) {
+      Box e = b;
+      e.ext[q] = mq;
+      e.lo[c] = b.lo[c] + mc;
+      e.ext[c] = b.ext[c] - mc;
+      edges.push_back(e);
+    }
+    b.ext[q] = mq;
+    b.ext[c] = mc;
+  }
+  std::vector<Box> boxes;
+  if (box_elements(b, a.rank) > 0)
+    split_box(dp, b, boxes);
+  out.reserve(boxes.size() + edges.size());
   for (const Box &x : boxes)
     if (box_work(dp, x) > 0)
       out.push_back(launch_args(dp, x));
+  for (const Box &x : edges)
+    if (box_elements(x, a.rank) > 0)
+      out.push_back(edge_args(dp, x));
   return out;
 }
 
@@ -904,7 +955,13 @@ struct Checker {
 
 } // namespace
 
-void verify_launch(const DeviceProgram &dp, const KArgs &a) {
+void verify_launch(const DeviceProgram &dp_in, const KArgs &a) {
+  DeviceProgram edge;
+  if (a.edge_box && dp_in.family != kFamGeneric) { // run by the element-wise kernel
+    edge = dp_in;
+    edge.family = kFamGeneric;
+  }
+  const DeviceProgram &dp = a.edge_box && dp_in.family != kFamGeneric ? edge : dp_in;
   const Checker ck{dp, a, dp.wire_elems, dp.dst_elems, dp.pf.size(), dp.pi.size()};
   if (dp.family != kFamGeneric) { // the levels' 32-bit offsets cannot wrap
     int64_t ss = 0, ds = 0;
@@ -957,8 +1014,12 @@ void verify_launch(const DeviceProgram &dp, const KArgs &a) {
         bad_launch(dp, "a transpose tile reaches a pad");
       const int64_t q0 = int64_t{tq} * 64, c0 = int64_t{tc} * 64;
       for (int row = 0; row < 64; row += 63) {
-        ck.src_run(sbase + (c0 + row) * a.t_ssc + q0, 64, true);
-        ck.dst_run(dbase + (q0 + row) * a.t_dsq + c0, 64, true);
+        // a tile row moves as 16-byte vectors
+        const int64_t so = sbase + (c0 + row) * a.t_ssc + q0, d = dbase + (q0 + row) * a.t_dsq + c0;
+        ck.src_run(so, 64, false);
+        ck.dst_run(d, 64, false);
+        if ((so * win) % 16 != 0 || (d * wout) % 16 != 0)
+          bad_launch(dp, "a tile row is not 16-byte aligned");
       }
       if ((a.t_ssc * win) % 16 != 0 || (a.t_dsq * wout) % 16 != 0)
         bad_launch(dp, "row strides break 16-byte alignment");
@@ -1070,7 +1131,7 @@ int64_t launch_all(const DeviceProgram &dp, std::vector<KArgs> launches, const v
                        reinterpret_cast<uintptr_t>(dst) % 16 == 0;
   int64_t n = 0;
   for (KArgs &a : launches) {
-    int family = dp.family;
+    int family = a.edge_box ? kFamGeneric : dp.family;
     if (!aligned && family != kFamGeneric) {
       family = kFamGeneric;
       int64_t e = 1;

@@ -180,6 +180,8 @@ struct KArgs {
   int32_t cpad;      // interleave: padded inner extent
   int32_t vec;       // stream: elements per vector; interleave: pixels per thread
   int32_t res_rank;
+  int32_t edge_box;  // 1: a box of a fast-family program at its unaligned edge,
+                     // run by the generic kernel
   int64_t work64;    // generic: elements of the box
   uint64_t fill64;
   int64_t pext[kMaxRank]; // padded extents

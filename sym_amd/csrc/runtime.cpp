@@ -850,22 +850,42 @@ int64_t verify_launches(BoundHandle &h, uint32_t k, int64_t chunk_bytes) {
   const DeviceProgram &dp = h.program(k);
   int64_t n = 0;
   bool whole = false;
+  // The boxes of one schedule partition the padded destination: their
+  // elements add up to it exactly.
+  int64_t total = 1;
+  for (int i = 0; i < dp.base.rank; ++i)
+    total *= dp.base.pext[i];
+  int64_t covered = 0;
+  auto check = [&](const KArgs &a) {
+    verify_launch(dp, a);
+    int64_t e = 1;
+    for (int i = 0; i < a.rank; ++i)
+      e *= a.box_ext[i];
+    covered += e;
+    ++n;
+  };
+  auto schedule_done = [&] {
+    if (covered != total)
+      throw Error("internal_launch_check", "launch boxes cover " + std::to_string(covered) +
+                                               " of " + std::to_string(total) +
+                                               " destination elements");
+    covered = 0;
+  };
   for (int direct = 0; direct < (chunk_bytes > 0 ? 1 : 2); ++direct) {
     const ChunkPlan p = chunk_plan(dp, source_width(*h.bound), chunk_bytes, direct != 0);
     for (int64_t v0 = 0; v0 < p.units; v0 += p.per_chunk) {
       const int64_t v1 = std::min(p.units, v0 + p.per_chunk);
-      for (const KArgs &a : box_launches(dp, v0, v1, v0 == 0, v1 == p.units)) {
-        verify_launch(dp, a);
-        ++n;
-      }
+      for (const KArgs &a : box_launches(dp, v0, v1, v0 == 0, v1 == p.units))
+        check(a);
     }
+    schedule_done();
     whole = whole || (dp.chunk_axis >= 0 && p.units > p.per_chunk);
   }
-  if (whole)
-    for (const KArgs &a : box_launches(dp, 0, 0, true, true)) { // the device-resident launch
-      verify_launch(dp, a);
-      ++n;
-    }
+  if (whole) {
+    for (const KArgs &a : box_launches(dp, 0, 0, true, true)) // the device-resident launch
+      check(a);
+    schedule_done();
+  }
   if (h.bound->indexed) {
     // The device gather, at the natural alignment and one element off it
     // (addresses only: nothing is dereferenced).

@@ -168,6 +168,32 @@ def test_c3_weight_full(ctx, opts):
         assert rep["chunks"] > 10
 
 
+@pytest.mark.parametrize("rows,cols", [(4000, 1104), (200, 336), (64 * 3, 80)])
+@pytest.mark.parametrize("opts", [{}, {"chunk_bytes": 256 << 10}, {"source_pinned": 1}])
+def test_transpose_with_partial_tiles(ctx, rows, cols, opts):
+    """C3's dequantizing transpose at extents that are not multiples of the
+    64x64 tile (rows still 16-byte aligned on both sides): whole tiles in the
+    tile kernel, the q and c edge strips in the element-wise kernel;
+    chunked, pinned, and from HBM."""
+    rng = np.random.default_rng(rows * 7919 + cols)
+    q = W.int8_weight(rows, cols, rng)
+    s = W.scales(cols, rng)
+    src = q
+    if opts.get("source_pinned"):
+        src = torch.from_numpy(q.view(np.uint8).copy()).pin_memory().numpy().view(np.int8).reshape(q.shape)
+    out, rep, b = run_h2d(ctx, W.c3_plan().blob, {"s0": rows, "s1": cols}, W.param("scale", s), src,
+                          "c3 %dx%d %s" % (rows, cols, opts), **opts)
+    assert b.kernel == "transpose"
+    want = f16_bits(O.dequantize_s8_f32(q, s[None, :], np.int32(0)).T)
+    assert np.array_equal(out.view(np.uint16).reshape(cols, rows), want)
+    # the same launches over a device-resident wire
+    qd = torch.from_numpy(q.view(np.uint8).copy()).cuda()
+    dev = torch.empty(rows * cols * 2, dtype=torch.uint8, device="cuda")
+    ctx.relayout_device(b, qd.data_ptr(), dev.data_ptr())
+    torch.cuda.synchronize()
+    assert np.array_equal(dev.cpu().numpy().view(np.uint16).reshape(cols, rows), want)
+
+
 # ------------------------------------------------------------------ C4
 
 def _c4_expected_rows(q, s, rows):
