@@ -435,7 +435,10 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
   }
   if (family == kFamGeneric && widths_ok && dense && !needs_expr) {
     // stream: innermost axis contiguous on both sides, unpadded
-    if (a.ss[r - 1] == 1 && a.ds[r - 1] == 1 && !inner_pad && a.vext[r - 1] % V == 0) {
+    // a single contiguous axis need not be a multiple of the vector: its
+    // tail (fewer than V elements) runs element-wise (prefix_launches)
+    if (a.ss[r - 1] == 1 && a.ds[r - 1] == 1 && !inner_pad &&
+        (a.vext[r - 1] % V == 0 || (r == 1 && a.vext[0] >= V))) {
       bool ok = true;
       for (int i = 0; i < r - 1; ++i)
         ok = ok && a.ss[i] % V == 0;
@@ -852,6 +855,15 @@ std::vector<KArgs> prefix_launches(const DeviceProgram &dp, const int64_t *fixed
   // element-wise kernel. Box starts on those axes are multiples of 64
   // (chunks and splits keep the tile alignment).
   std::vector<Box> edges;
+  if (dp.family == kFamStream && a.rank == 1 && b.ext[0] % a.vec != 0) {
+    // the tail of a single contiguous axis (box starts are multiples of V)
+    const int64_t m = b.ext[0] / a.vec * a.vec;
+    Box e = b;
+    e.lo[0] = b.lo[0] + m;
+    e.ext[0] = b.ext[0] - m;
+    edges.push_back(e);
+    b.ext[0] = m;
+  }
   if (dp.family == kFamTranspose) {
     const int q = dp.qa, c = dp.ca;
     const int64_t mq = b.ext[q] / 64 * 64, mc = b.ext[c] / 64 * 64;

@@ -194,6 +194,34 @@ def test_transpose_with_partial_tiles(ctx, rows, cols, opts):
     assert np.array_equal(dev.cpu().numpy().view(np.uint16).reshape(cols, rows), want)
 
 
+@pytest.mark.parametrize("n", [1000003, 4099, 13, 5])
+@pytest.mark.parametrize("dtype", ["float32", "int8"])
+def test_flat_stream_with_a_tail(ctx, n, dtype):
+    """A flat tensor whose length is not a multiple of the 16-byte vector:
+    the vector kernel takes the whole vectors, the tail runs element-wise;
+    staged, chunked (4 KiB), pinned and from HBM."""
+    from sym_amd import encoder as EN
+    rng = np.random.default_rng(n)
+    if dtype == "float32":
+        x = (rng.standard_normal(n) * 100).astype(np.float32)
+        ops = [EN.Cast("float16")]
+    else:
+        x = rng.integers(-128, 128, n, dtype=np.int8)
+        ops = [EN.Dequantize(EN.InlineParam((0.0625,), "float32", 0))]
+    plan = EN.encode([n], dtype, ops)
+    want = O.run_typed(plan.blob, {}, {}, x).tobytes()
+    pin = torch.from_numpy(x.view(np.uint8).copy()).pin_memory().numpy().view(x.dtype)
+    for src, opts in ((x, {}), (x, {"chunk_bytes": 4096}), (pin, {"source_pinned": 1})):
+        out, rep, b = run_h2d(ctx, plan.blob, {}, {}, src, "flat %s n=%d" % (dtype, n), **opts)
+        assert b.kernel == "stream"
+        assert out.tobytes() == want, opts
+    xd = torch.from_numpy(x.view(np.uint8).copy()).cuda()
+    dev = torch.empty(len(want), dtype=torch.uint8, device="cuda")
+    ctx.relayout_device(b, xd.data_ptr(), dev.data_ptr())
+    torch.cuda.synchronize()
+    assert dev.cpu().numpy().tobytes() == want
+
+
 # ------------------------------------------------------------------ C4
 
 def _c4_expected_rows(q, s, rows):
