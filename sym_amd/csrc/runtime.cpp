@@ -765,8 +765,9 @@ std::unique_ptr<Context> make_context(int device, int64_t max_retained) {
   // directly: the host clears and reads a flag with plain accesses, instead
   // of a device memset and a blocking 4-byte copy per call (15 us of a small
   // call's latency).
-  HIPCHECK(hipHostMalloc(reinterpret_cast<void **>(&ctx->status), 256, hipHostMallocDefault));
-  std::memset(ctx->status, 0, 256);
+  HIPCHECK(hipHostMalloc(reinterpret_cast<void **>(&ctx->status), kStatusSlots * sizeof(int32_t),
+                         hipHostMallocDefault));
+  std::memset(ctx->status, 0, kStatusSlots * sizeof(int32_t));
   return ctx;
 }
 

@@ -236,7 +236,7 @@ struct Context {
   uint8_t *wire = nullptr;
   size_t wire_cap = 0;
   int32_t *status = nullptr; // kStatusSlots flags, one per call in flight
-  int status_next = 0;
+  uint32_t status_next = 0; // wraps
   std::unique_ptr<Workers> workers;
   unsigned worker_threads = 0;
   int64_t max_retained = 0;
@@ -251,7 +251,7 @@ struct Context {
   ~Context(); // frees the status flags (the rest goes in destroy_context)
 };
 
-constexpr int kStatusSlots = 64;
+constexpr uint32_t kStatusSlots = 1024;
 
 // An asynchronous call's completion: an event recorded after its last kernel
 // and the status flag its element-wise kernels report into. Holds the context
