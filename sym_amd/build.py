@@ -29,9 +29,15 @@ SOURCES = ["plan.cpp", "program.cpp", "runtime.cpp", "workers.cpp", "indexed.cpp
            "k_interleave_generic.hip", "k_permute.hip", "k_gather.hip", "k_copy.hip"]
 
 
+# The one-level interleave takes its hot arguments as leading scalars that
+# the dispatch preloads into scalar registers.
+EXTRA = {"k_interleave.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
+
+
 def _compile(src):
     obj = os.path.join(OUT_DIR, os.path.basename(src) + ".o")
-    cmd = [HIPCC] + COMMON + DEVICE + ["-I" + CSRC, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC] + COMMON + DEVICE + EXTRA.get(src, []) + ["-I" + CSRC, "-c",
+                                                            os.path.join(CSRC, src), "-o", obj]
     if src.endswith(".hip"):
         cmd[1:1] = ["-x", "hip"]
     r = subprocess.run(cmd, capture_output=True, text=True)
