@@ -141,6 +141,44 @@ def test_c2_image_batch_full(ctx, host_stages):
     assert rep["destination_bytes"] == 12845056
 
 
+@pytest.mark.parametrize("shape,lo,hi", [((3, 3, 20, 24), 0, 1), ((1, 1, 16, 8), 1, 0),
+                                          ((2, 5, 12, 16), 1, 2), ((2, 3, 3, 10, 8), 0, 1)])
+@pytest.mark.parametrize("dtype,cast", [("float32", "float16"), ("float32", None),
+                                        ("float16", None), ("int8", None), ("float16", "float32")])
+def test_planar_to_interleaved_with_channel_pad(ctx, shape, lo, hi, dtype, cast):
+    """C2's pattern over channel counts, pads, batch ranks and element
+    types: NC...HW -> N...HWC with the channel axis padded (the fill folds
+    through the cast); contiguous batch axes merge into one level, which
+    takes the preloaded-argument variant for per-tensor chains."""
+    from sym_amd import encoder as EN
+    rng = np.random.default_rng(sum(shape) * 31 + lo + 7 * hi)
+    caxis = len(shape) - 3
+    n = int(np.prod(shape))
+    if dtype == "int8":
+        x = rng.integers(-128, 128, n, dtype=np.int8).reshape(shape)
+        fill = -5
+    else:
+        x = (rng.standard_normal(n) * 10).astype(dtype).reshape(shape)
+        fill = 1.5
+    perm = tuple(range(caxis)) + (caxis + 1, caxis + 2, caxis)
+    ops = [EN.Pad(caxis, lo, hi, fill), EN.Transpose(perm)] + ([EN.Cast(cast)] if cast else [])
+    try:
+        plan = EN.encode(list(shape), dtype, ops)
+    except EN.EncodeError as e:
+        pytest.skip("not encodable: %s" % e)
+    want = (O.run_typed(plan.blob, {}, {}, x).tobytes() if plan.typed else
+            O.execute_layout(O.bind(O.decode_plan(plan.blob), {}), x.tobytes()))
+    for hs in (0, -1):
+        out, rep, b = run_h2d(ctx, plan.blob, {}, {}, x, "interleave %s %s %s->%s" % (shape, (lo, hi), dtype, cast),
+                              host_stages=hs)
+        assert out.tobytes() == want, hs
+    xd = torch.from_numpy(x.view(np.uint8).reshape(-1).copy()).cuda()
+    dev = torch.empty(len(want), dtype=torch.uint8, device="cuda")
+    ctx.relayout_device(b, xd.data_ptr(), dev.data_ptr())
+    torch.cuda.synchronize()
+    assert dev.cpu().numpy().tobytes() == want
+
+
 def test_c2_pinned_source_direct_dma(ctx):
     x = torch.from_numpy(W.c2_input()).pin_memory()
     plan = P.Plan(W.c2_plan().blob)
