@@ -699,8 +699,9 @@ __global__ __launch_bounds__(kBlock) void k_transpose(KArgs a) {
 // plane, one packed run of G*CP output elements (16 bytes when a pixel allows).
 // Each lane takes U items 64 apart, so every plane load and every store
 // instruction of a wave covers one contiguous run. Stages are per tensor.
-// The batch index is decomposed over the innermost NL batch levels (NL = 1
-// when the outer two are unit levels: an NCHW batch).
+// The batch index is decomposed over the innermost NL batch levels; the
+// launches use all kBatchLevels (an NCHW batch with a per-tensor chain takes
+// k_interleave1p below instead).
 template <int WIN, int WOUT, int CP, int CH, int NL>
 __global__ __launch_bounds__(kBlock) void k_interleave(KArgs a) {
   constexpr int G = interleave_pixels(WIN, WOUT, CP);
