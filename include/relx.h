@@ -153,7 +153,7 @@ int relx_bound_query(const relx_bound *bound, relx_bound_info *out);
 
 /* ------------------------------------------------------------- contexts */
 
-/* A retained per-device context: a copy stream and a compute stream, a
+/* A retained per-device context: two copy streams and a compute stream, a
  * pinned host staging ring, device wire scratch and events. Replaces
  * CudaBackend (libreloc/cuda/CudaBackend.cu:55-282) and the retained
  * ScratchBackend of dispatch::Resources
@@ -188,9 +188,15 @@ typedef struct relx_options {
   int gather_threads;   /* host staging threads (0 = default 8) */
   int source_pinned;    /* 1: source is page-locked; DMA it directly.
                            -1: probe; 0: pageable (stage through the ring) */
-  uint64_t caller_stream; /* hipStream_t the call is ordered after (0 = none) */
+  uint64_t caller_stream; /* hipStream_t the call is ordered after and that
+                             waits for the call's end, when has_caller_stream
+                             is set; 0 is HIP's legacy null stream */
   int no_wait;          /* 1: return after enqueue; the caller's stream (or
                            relx_ctx_synchronize) orders later work */
+  int has_caller_stream; /* 1: order after caller_stream (reference
+                            TransferOptions::hasCallerStream,
+                            libreloc/include/reloc/Transfer.h:126-128);
+                            0: no producer stream to order after */
 } relx_options;
 
 /* Scalar report of one call (reference dispatch::Report,
@@ -211,7 +217,10 @@ typedef struct relx_report {
 /* Run one bound plan: host source (dense, source layout, source dtype) ->
  * device destination (dense result layout). The source bytes move through
  * the chunked pinned H2D pipeline on the copy stream; relayout and value
- * stages run as HIP kernels on the compute stream, overlapped per chunk.
+ * stages run as HIP kernels behind each chunk's copy on its copy stream, while
+ * the next chunk's copy runs on the other copy stream. With
+ * `has_caller_stream` the copies start after the work enqueued on
+ * `caller_stream` so far, and `caller_stream` waits for the call's end.
  * Replaces dispatch::executeDispatch (libreloc/src/Dispatch.cpp:1983-2046)
  * for the H2D direction, executeTransfer (libreloc/src/Transfer.cpp:493-544)
  * for layout plans, and pyreloc.execute_dispatch / execute_transfer
@@ -275,7 +284,8 @@ void relx_completion_free(relx_completion *c);
  * runs. For this call `opt->source_pinned` describes the HOST buffer (the
  * destination): 1 pinned (direct DMA), 0 pageable (pinned ring, worker
  * threads copy each slot out), -1 probe; `host_stages` must be 0 or -1. The
- * source is ordered after `opt->caller_stream`. Blocks until the
+ * source is ordered after `opt->caller_stream` when `has_caller_stream` is
+ * set (0 being the legacy null stream). Blocks until the
  * destination holds the result. */
 int relx_execute_d2h(relx_ctx *ctx, const relx_bound *bound, const void *src, size_t src_bytes,
                      void *dst, size_t dst_bytes, const relx_options *opt, relx_report *report,
@@ -283,18 +293,23 @@ int relx_execute_d2h(relx_ctx *ctx, const relx_bound *bound, const void *src, si
 
 /* Device-resident relayout: `wire` is already in device memory (dense source
  * layout at boundary `wire_boundary`); run the relayout + stages
- * [wire_boundary, stages) into `dst` on `stream` (0 = the context's compute
- * stream). Asynchronous: returns after the launch. This is the device half of
- * relx_execute_h2d and the unit the kernel roofline is measured on; it
- * replaces the reference's kernel launch wrappers reloc::cuda::*
- * (libreloc/include/reloc/CudaKernels.h:28-122). */
+ * [wire_boundary, stages) into `dst` on `stream`, a hipStream_t where 0 is
+ * HIP's legacy null stream, as the reference's wrappers take a null stream
+ * (void *stream = nullptr). Asynchronous: returns after the launch. This is
+ * the device half of relx_execute_h2d and the unit the kernel roofline is
+ * measured on; it replaces the reference's kernel launch wrappers
+ * reloc::cuda::* (libreloc/include/reloc/CudaKernels.h:28-122).
+ * A program on the element-wise kernel reports a stage channel outside its
+ * parameters through a status flag of its own; the next
+ * relx_ctx_synchronize waits for such launches and fails with
+ * "channel_out_of_range" once for all of them. */
 int relx_relayout_device(relx_ctx *ctx, const relx_bound *bound, int wire_boundary,
                          const void *wire, void *dst, uint64_t stream, relx_err *err);
 
 /* Indexed plans with a device-resident table: gather the bound's selected
  * rows of `table` (table_rows x row_elements source elements, dense) into
  * `dst` (dense selected rows of the result type), the plan's cast fused into
- * the gather, on `stream` (0 = the context's compute stream). Asynchronous:
+ * the gather, on `stream` (0 = HIP's legacy null stream). Asynchronous:
  * returns after the launch. The reference executes indexed plans only from
  * host memory, gathering on the CPU (libreloc/src/Dispatch.cpp:1269-1283,
  * 1397-1404); this is the device form of its index_select. Errors:
@@ -321,7 +336,10 @@ int relx_host_stage(const relx_bound *bound, int host_stages, const void *src, v
 int relx_verify_launches(const relx_bound *bound, int wire_boundary, int64_t chunk_bytes,
                          int64_t *launches, relx_err *err);
 
-/* Block until every call on the context has completed. */
+/* Block until every call on the context has completed: its own streams, and
+ * the device-resident launches that report a status (see
+ * relx_relayout_device). Fails with "channel_out_of_range" when one of those
+ * launches selected a channel outside its parameters. */
 int relx_ctx_synchronize(relx_ctx *ctx, relx_err *err);
 
 /* Pinned host memory helpers (hipHostMalloc / hipHostFree). */

@@ -59,7 +59,7 @@ class relx_options(ctypes.Structure):
     _fields_ = [("n_buffers", ctypes.c_int), ("chunk_bytes", ctypes.c_int64),
                 ("host_stages", ctypes.c_int), ("gather_threads", ctypes.c_int),
                 ("source_pinned", ctypes.c_int), ("caller_stream", ctypes.c_uint64),
-                ("no_wait", ctypes.c_int)]
+                ("no_wait", ctypes.c_int), ("has_caller_stream", ctypes.c_int)]
 
 
 class relx_report(ctypes.Structure):

@@ -19,6 +19,7 @@ bool drain(Context &ctx);
 void destroy_context(Context &ctx);
 void relayout_device(Context &ctx, BoundHandle &h, uint32_t k, const void *wire, void *dst,
                      hipStream_t stream);
+void resolve_checks(Context &ctx);
 double measure_h2d(int device, size_t bytes, int iters, int rounds);
 double measure_copy(int device, size_t bytes, int iters, int rounds, bool d2h);
 } // namespace relx
@@ -468,6 +469,9 @@ int relx_relayout_device(relx_ctx *ctx, const relx_bound *bound, int wire_bounda
       throw relx::Error("invalid_argument", "null argument");
     if (wire_boundary < 0)
       throw relx::Error("invalid_boundary", "negative wire boundary");
+    std::lock_guard<std::mutex> g(ctx->ctx->mu);
+    if (ctx->ctx->closed || ctx->ctx->quarantined)
+      throw relx::Error("resources_closed", "context is closed or quarantined");
     relx::relayout_device(*ctx->ctx, const_cast<relx::BoundHandle &>(bound->h),
                           static_cast<uint32_t>(wire_boundary), wire, dst,
                           reinterpret_cast<hipStream_t>(stream));
@@ -539,8 +543,10 @@ int relx_ctx_synchronize(relx_ctx *ctx, relx_err *err) {
   return guarded(err, [&] {
     if (!ctx)
       throw relx::Error("invalid_argument", "null context");
+    std::lock_guard<std::mutex> g(ctx->ctx->mu);
     if (!relx::drain(*ctx->ctx))
       throw relx::Error("backend_failure", "stream synchronize failed");
+    relx::resolve_checks(*ctx->ctx);
   });
 }
 

@@ -247,9 +247,9 @@ int64_t index_select_device(Context &ctx, BoundHandle &h, const void *table, siz
   const std::vector<GatherArgs> launches = gather_launches(b, g, table, dst, idx);
   if (verify_env())
     verify_gather(b, g, launches, table, table_bytes, dst, dst_bytes, idx);
-  hipStream_t s = stream ? stream : ctx.compute;
+  // `stream` as given: 0 is the legacy null stream
   for (const GatherArgs &a : launches)
-    hipcheck(gather_launch(a, g.op, g.nbi, g.iw, g.nt, s), "gather launch");
+    hipcheck(gather_launch(a, g.op, g.nbi, g.iw, g.nt, stream), "gather launch");
   return static_cast<int64_t>(launches.size());
 }
 

@@ -405,8 +405,13 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
   // by an event from another stream); the copy streams join at the end.
   if (ctx.unsynced) // the previous call may still read the wire arena
     copy_streams_wait(ctx, ctx.done_ev);
+  // The caller's stream (0 being the legacy null stream) may still be
+  // producing the destination's previous users or a device source: every
+  // private stream starts after the work enqueued on it so far
+  // (libreloc/src/Dispatch.cpp:1995, libreloc/cuda/CudaBackend.cu:190-208).
+  const bool ordered = opt.has_caller_stream != 0;
   hipStream_t caller = reinterpret_cast<hipStream_t>(opt.caller_stream);
-  if (caller) {
+  if (ordered) {
     HIPCHECK(hipEventRecord(ctx.start_ev, caller));
     copy_streams_wait(ctx, ctx.start_ev);
   }
@@ -526,7 +531,7 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
   if (two_streams)
     join_copy_streams(ctx, last, nchunk);
   HIPCHECK(hipEventRecord(ctx.done_ev, last));
-  if (caller)
+  if (ordered)
     HIPCHECK(hipStreamWaitEvent(caller, ctx.done_ev, 0));
   if (total) {
     std::snprintf(sum.implementation, sizeof(sum.implementation), "hip_relayout_group");
@@ -648,8 +653,9 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
     HIPCHECK(hipStreamWaitEvent(ctx.compute, ctx.done_ev, 0));
     copy_streams_wait(ctx, ctx.done_ev);
   }
+  const bool ordered = opt.has_caller_stream != 0;
   hipStream_t caller = reinterpret_cast<hipStream_t>(opt.caller_stream);
-  if (caller) { // the source is produced on the caller's stream
+  if (ordered) { // the source is produced on the caller's stream (0: the null stream)
     HIPCHECK(hipEventRecord(ctx.start_ev, caller));
     HIPCHECK(hipStreamWaitEvent(ctx.compute, ctx.start_ev, 0));
     copy_streams_wait(ctx, ctx.start_ev);
@@ -718,7 +724,7 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
     consume(pending[next++]);
   join_copy_streams(ctx, ctx.copies[0], chunks);
   HIPCHECK(hipEventRecord(ctx.done_ev, ctx.copies[0]));
-  if (caller)
+  if (ordered)
     HIPCHECK(hipStreamWaitEvent(caller, ctx.done_ev, 0));
   HIPCHECK(hipEventSynchronize(ctx.done_ev));
   ctx.unsynced = false;
@@ -765,9 +771,11 @@ std::unique_ptr<Context> make_context(int device, int64_t max_retained) {
   // directly: the host clears and reads a flag with plain accesses, instead
   // of a device memset and a blocking 4-byte copy per call (15 us of a small
   // call's latency).
-  HIPCHECK(hipHostMalloc(reinterpret_cast<void **>(&ctx->status), kStatusSlots * sizeof(int32_t),
-                         hipHostMallocDefault));
-  std::memset(ctx->status, 0, kStatusSlots * sizeof(int32_t));
+  const size_t flags = (kStatusSlots + kDeviceChecks + 1) * sizeof(int32_t); // + the sink
+  HIPCHECK(hipHostMalloc(reinterpret_cast<void **>(&ctx->status), flags, hipHostMallocDefault));
+  std::memset(ctx->status, 0, flags);
+  for (uint32_t i = 0; i < kDeviceChecks; ++i)
+    HIPCHECK(hipEventCreateWithFlags(&ctx->check_ev[i], hipEventDisableTiming));
   return ctx;
 }
 
@@ -784,6 +792,17 @@ bool drain(Context &ctx) {
   bool ok = hipStreamSynchronize(ctx.compute) == hipSuccess;
   for (hipStream_t c : ctx.copies)
     ok = hipStreamSynchronize(c) == hipSuccess && ok;
+  // device-resident launches on callers' streams still write their flags
+  for (uint32_t i = 0; i < kDeviceChecks; ++i)
+    if (ctx.check_pending[i]) {
+      const bool done = hipEventSynchronize(ctx.check_ev[i]) == hipSuccess;
+      ok = done && ok;
+      if (done) {
+        ctx.check_pending[i] = false;
+        if (read_status(ctx.status + kStatusSlots + i))
+          ctx.channel_error = true;
+      }
+    }
   return ok;
 }
 
@@ -802,6 +821,11 @@ void destroy_context(Context &ctx) {
   for (hipEvent_t e : ctx.join_ev)
     if (e)
       (void)hipEventDestroy(e);
+  for (hipEvent_t &e : ctx.check_ev)
+    if (e) {
+      (void)hipEventDestroy(e);
+      e = nullptr;
+    }
   if (ctx.wire)
     (void)hipFree(ctx.wire);
   ctx.wire = nullptr;
@@ -925,13 +949,50 @@ int64_t verify_launches(BoundHandle &h, uint32_t k, int64_t chunk_bytes) {
   return n;
 }
 
+// Reads device-check slot i once its launch has completed; a set flag makes
+// the context's channel error sticky until synchronize reports it.
+void resolve_check(Context &ctx, uint32_t i) {
+  if (!ctx.check_pending[i])
+    return;
+  HIPCHECK(hipEventSynchronize(ctx.check_ev[i]));
+  ctx.check_pending[i] = false;
+  if (read_status(ctx.status + kStatusSlots + i))
+    ctx.channel_error = true;
+}
+
+// Waits for every device-resident launch that reports a status; throws
+// channel_out_of_range (once) when one of them set its flag.
+void resolve_checks(Context &ctx) {
+  for (uint32_t i = 0; i < kDeviceChecks; ++i)
+    resolve_check(ctx, i);
+  if (ctx.channel_error) {
+    ctx.channel_error = false;
+    throw Error("channel_out_of_range",
+                "a device-resident launch selected a stage channel outside its parameters");
+  }
+}
+
+// The program's launches on `stream` as given: 0 is the legacy null stream,
+// as for the reference's kernel wrappers (void *stream = nullptr).
 void relayout_device(Context &ctx, BoundHandle &h, uint32_t k, const void *wire, void *dst,
                      hipStream_t stream) {
   DeviceGuard guard(ctx.device);
   const DeviceProgram &dp = h.program(k);
   const BoundHandle::DevParams par = h.device_params(ctx.device, k);
-  launch_program(dp, 0, 0, true, true, wire, dst, par.pf, par.pi, ctx.status,
-                 stream ? stream : ctx.compute);
+  if (dp.family != kFamGeneric) {
+    // Fast families have their channels proven in range when the program is
+    // built; their edge boxes (element-wise) get the sink flag, never read.
+    launch_program(dp, 0, 0, true, true, wire, dst, par.pf, par.pi,
+                   ctx.status + kStatusSlots + kDeviceChecks, stream);
+    return;
+  }
+  const uint32_t i = ctx.check_next++ % kDeviceChecks;
+  resolve_check(ctx, i); // its previous launch, kDeviceChecks calls ago
+  int32_t *status = ctx.status + kStatusSlots + i;
+  clear_status(status);
+  launch_program(dp, 0, 0, true, true, wire, dst, par.pf, par.pi, status, stream);
+  HIPCHECK(hipEventRecord(ctx.check_ev[i], stream));
+  ctx.check_pending[i] = true;
 }
 
 double measure_copy(int device, size_t bytes, int iters, int rounds, bool d2h);

@@ -235,8 +235,17 @@ struct Context {
   hipEvent_t join_ev[kCopyStreams] = {}; // one per copy stream, for joins
   uint8_t *wire = nullptr;
   size_t wire_cap = 0;
-  int32_t *status = nullptr; // kStatusSlots flags, one per call in flight
+  int32_t *status = nullptr; // kStatusSlots flags, one per call in flight,
+                             // then kDeviceChecks flags of device-resident calls
   uint32_t status_next = 0; // wraps
+  // Device-resident element-wise launches (relx_relayout_device) run on the
+  // caller's stream and return at once: each takes the next of kDeviceChecks
+  // flags and records check_ev after its launch. The flag is read once that
+  // event completes: when the slot comes round again, or at synchronize.
+  hipEvent_t check_ev[64] = {};
+  bool check_pending[64] = {};
+  uint32_t check_next = 0;
+  bool channel_error = false; // a resolved check found its flag set
   std::unique_ptr<Workers> workers;
   unsigned worker_threads = 0;
   int64_t max_retained = 0;
@@ -252,6 +261,7 @@ struct Context {
 };
 
 constexpr uint32_t kStatusSlots = 1024;
+constexpr uint32_t kDeviceChecks = 64; // size of Context::check_ev
 
 // An asynchronous call's completion: an event recorded after its last kernel
 // and the status flag its element-wise kernels report into. Holds the context

@@ -336,7 +336,7 @@ def execute_dispatch(request, *, caller_stream=None, n_buffers=2, n_streams=2, g
                   n_buffers=n_buffers, chunk_bytes=int(chunk_size or 0),
                   host_stages=request.selected["host_stages"],
                   gather_threads=gather_threads, source_pinned=_pinning(pinning),
-                  caller_stream=int(caller_stream or 0))
+                  caller_stream=caller_stream)
         request.consumed = True
         request.report = _report(rep, request)
         return dict(request.report)
@@ -394,7 +394,7 @@ def execute_dispatch_group(group, *, caller_stream=None, gather_threads=1, gathe
                 for r in group.items]
         reps, total = ctx.execute_group_h2d(bounds, srcs, dsts, n_buffers=n_buffers,
                                             gather_threads=gather_threads,
-                                            caller_stream=int(caller_stream or 0))
+                                            caller_stream=caller_stream)
         items = []
         for r, rep in zip(group.items, reps):
             r.consumed = True
@@ -486,7 +486,7 @@ def submit_dispatch_group(group, *, caller_stream=None, gather_threads=8, gather
     try:
         native = ctx.submit_group_h2d(bounds, srcs, dsts, owners=owners, n_buffers=n_buffers,
                                       gather_threads=gather_threads,
-                                      caller_stream=int(caller_stream or 0))
+                                      caller_stream=caller_stream)
     except Exception:
         group.executing = False
         raise

@@ -374,9 +374,15 @@ def bind_typed(plan, symbols, parameters):
 
 
 def _options(n_buffers=0, chunk_bytes=0, host_stages=-1, gather_threads=0, source_pinned=-1,
-             caller_stream=0, no_wait=False):
+             caller_stream=None, no_wait=False):
+    """Per-call options. `caller_stream` is a hipStream_t handle the call is
+    ordered after (0 is the legacy null stream, torch's default stream);
+    None means no producer stream, as the reference's caller_stream=None
+    (libreloc/python/PyDispatch.cpp:199-202)."""
+    has = caller_stream is not None
     return N.relx_options(int(n_buffers), int(chunk_bytes), int(host_stages), int(gather_threads),
-                          int(source_pinned), int(caller_stream or 0), 1 if no_wait else 0)
+                          int(source_pinned), int(caller_stream) if has else 0,
+                          1 if no_wait else 0, 1 if has else 0)
 
 
 class Context:
@@ -453,14 +459,18 @@ class Context:
 
     def index_select_device(self, bound, table_ptr, table_nbytes, dst_ptr, dst_nbytes, stream=0):
         """Gather an indexed plan's selected rows from a device-resident
-        table into `dst`, cast fused (async on `stream`)."""
+        table into `dst`, cast fused (async on `stream`, a hipStream_t
+        handle; 0 is the legacy null stream, torch's default stream)."""
         err = N.relx_err()
         if N.lib().relx_index_select_device(self._h, bound._h, table_ptr, table_nbytes, dst_ptr,
                                             dst_nbytes, int(stream or 0), ctypes.byref(err)):
             _raise(err)
 
     def relayout_device(self, bound, wire_ptr, dst_ptr, wire_boundary=0, stream=0):
-        """Launch the device relayout on a device-resident wire (async)."""
+        """Launch the device relayout on a device-resident wire (async on
+        `stream`, a hipStream_t handle; 0 is the legacy null stream, torch's
+        default stream). A channel outside the parameters is reported by the
+        next synchronize()."""
         err = N.relx_err()
         if N.lib().relx_relayout_device(self._h, bound._h, int(wire_boundary), wire_ptr, dst_ptr,
                                         int(stream or 0), ctypes.byref(err)):

@@ -155,3 +155,20 @@ def test_fastdiv_is_exact_on_the_host():
         hi = (ns * np.uint64(m)) >> np.uint64(32)
         q = (hi + ns) >> np.uint64(s)
         assert np.array_equal(q, ns // np.uint64(d)), d
+
+
+def test_caller_stream_option_mapping():
+    """None means no producer stream; any handle, 0 (the legacy null stream,
+    torch's default) included, orders the call after that stream
+    (reference hasCallerStream, libreloc/python/PyDispatch.cpp:199-202)."""
+    none = P._options()
+    assert none.has_caller_stream == 0 and none.caller_stream == 0
+    null = P._options(caller_stream=0)
+    assert null.has_caller_stream == 1 and null.caller_stream == 0
+    other = P._options(caller_stream=0x1234)
+    assert other.has_caller_stream == 1 and other.caller_stream == 0x1234
+    # the ctypes layout matches the header's field order
+    text = open(os.path.join(ROOT, "include", "relx.h")).read()
+    body = text[text.index("typedef struct relx_options"):text.index("} relx_options;")]
+    fields = re.findall(r"^\s+(?:int|int64_t|uint64_t)\s+(\w+);", body, re.M)
+    assert fields == [f for f, _ in N.relx_options._fields_]

@@ -328,6 +328,11 @@ def test_channel_outside_the_table_is_reported(resources, rng, monkeypatch):
     host = np.empty(24, np.float32)
     with pytest.raises(P.TransferError, match="channel_out_of_range"):
         resources.execute_d2h(b, qd.data_ptr(), q.nbytes, host.ctypes.data, host.nbytes)
+    say("channel out of range, device-resident")
+    resources.relayout_device(b, qd.data_ptr(), out.data_ptr(), stream=0)
+    with pytest.raises(P.TransferError, match="channel_out_of_range"):
+        resources.synchronize()
+    resources.synchronize()  # reported once
     # the flag belongs to its call: a good call on the same resources is clean
     rows, cols = 64, 128
     q2, s2 = W.int8_weight(rows, cols, rng), W.scales(cols, rng)

@@ -64,16 +64,20 @@ def test_random_plans_on_the_gpu(ctx, block):
                 say("fuzz seed", seed, "kernel", b.kernel, "h2d k", k, "pinned", pinned, "chunk", chunk)
                 s = torch.from_numpy(src_u8.copy()).pin_memory() if pinned else None
                 ptr, nb = (s.data_ptr(), s.numel()) if pinned else (src.ctypes.data, src.nbytes)
+                # the fill runs on torch's stream: the call is ordered after it
                 out.fill_(0xA5)
                 ctx.execute_h2d(b, ptr, nb, out.data_ptr(), out_bytes, host_stages=k,
-                                chunk_bytes=chunk, source_pinned=1 if pinned else 0)
+                                chunk_bytes=chunk, source_pinned=1 if pinned else 0,
+                                caller_stream=torch.cuda.current_stream().cuda_stream)
                 torch.cuda.synchronize()
                 assert out[:out_bytes].cpu().numpy().tobytes() == want, (seed, ops, k, pinned, chunk)
         d_src = torch.from_numpy(src_u8.copy()).cuda()
         say("fuzz seed", seed, "device-resident")
         out.fill_(0xA5)
-        ctx.relayout_device(b, d_src.data_ptr(), out.data_ptr())
+        ctx.relayout_device(b, d_src.data_ptr(), out.data_ptr(),
+                            stream=torch.cuda.current_stream().cuda_stream)
         ctx.synchronize()
+        torch.cuda.synchronize()
         assert out[:out_bytes].cpu().numpy().tobytes() == want, (seed, ops, "device")
         for pinned in (False, True):
             say("fuzz seed", seed, "d2h pinned", pinned)
@@ -81,7 +85,8 @@ def test_random_plans_on_the_gpu(ctx, block):
             if pinned:
                 host = host.pin_memory()
             ctx.execute_d2h(b, d_src.data_ptr(), d_src.numel(), host.data_ptr(), out_bytes,
-                            chunk_bytes=4096 if seed % 2 else 0, source_pinned=1 if pinned else 0)
+                            chunk_bytes=4096 if seed % 2 else 0, source_pinned=1 if pinned else 0,
+                            caller_stream=torch.cuda.current_stream().cuda_stream)
             assert host[:out_bytes].numpy().tobytes() == want, (seed, ops, "d2h", pinned)
         n_run += 1
     assert n_run > 30
