@@ -1,22 +1,27 @@
 #!/usr/bin/env python3
 """Benchmark of the libreloc plan-execution hot path on one MI355X.
 
-Headline (C2 image-batch relayout): fp32 NCHW
-[32,3,224,224] -> pad C 3->4 -> NHWC -> fp16.
+Headline: the metric of BASELINE.json (effective GB/s of output, fused
+relayout + H2D) on its largest single-GPU configuration, C5 at B=64,
+S=4096: f16 [64,4096,32,128] in host memory -> permute to [B,32,S,128] ->
+f32 -> int8 quantize (per-head scale) in HBM; 2 GiB cross PCIe, 1 GiB is
+written.
 
-* `value`: output GB/s of the fused device relayout with the wire already
-  resident in HBM (K back-to-back launches over rotating buffer sets that
-  together exceed the 256 MB Infinity Cache).
-* `roofline`: the dominant kernel's algorithmic bytes per launch over its
-  average launch duration (per-launch HIP events on the launch stream),
-  against 8 TB/s; `traffic` from the committed rocprofv3 PMC summary.
-* `e2e`: the PCIe-inclusive rate (pageable and pinned host source) against
-  the measured pinned H2D ceiling -- reported, never `value`.
-* `cpu_baseline`: the reference's own compiled CPU executor (oracle/_ref,
-  typed::executeHost) on this host, on a bounded sample.
+* A step is one blocking call of the reference-shaped dispatch API from a
+  pageable host tensor: fresh output allocation, bind, prepare, execute and
+  completion, as the reference times its typed H2D rows.
+* `value`: output bytes x steps / wall time of the K steps.
+* `pcie`: the same steps in wire bytes against the measured pinned H2D
+  ceiling, plus the pinned-source (direct DMA) rate.
+* `roofline`: the dominant kernel, the per-chunk k_permute launch inside the
+  timed steps, timed by event pairs on the copy stream it runs on;
+  algorithmic bytes per launch over its mean duration, against 8 TB/s.
+  `traffic` comes from the committed rocprofv3 PMC summary.
+* `cpu_baseline`: the reference's own cpu_reference row (oracle/_ref: CPU
+  transform into a 2-slot pinned ring, then H2D) on the same batch and host.
 
-`--report` prints one JSON line per config (C1..C5, and the indexed-plan
-gathers ix_*) instead.
+`--report` prints one JSON line per config (C1..C5, device-resident kernel
+rates, and the indexed-plan gathers ix_*) instead.
 """
 import argparse
 import json
@@ -30,14 +35,21 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-METRIC = "effective GB/s (output bytes/s) fused relayout+H2D; % of PCIe and HBM roofline"
+
+
+def log(*a):
+    """Progress on stderr (the JSON line is the only stdout output)."""
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+METRIC ="effective GB/s (output bytes/s) fused relayout+H2D; % of PCIe and HBM roofline"
 
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--e2e-samples", type=int, default=40)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -47,6 +59,9 @@ def parse():
                     help="run a plain copy of known size, then each config's kernel (for rocprofv3 --pmc)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn two rocprofv3 --pmc runs of --traffic-probe into profiles/traffic.json")
+    ap.add_argument("--summarize-trace", metavar="TRACE_DIR",
+                    help="per-call copy/kernel/staging timeline of a rocprofv3 marker + memory-copy "
+                         "+ kernel trace of the headline (RELX_TRACE=1)")
     return ap.parse_args()
 
 
@@ -427,6 +442,22 @@ def traffic_probe(torch, ctx, names):
     del a, b
     kernels = {}
     for name in names:
+        if name == "c5_e2e":
+            # the headline steps: each chunk's k_permute launch inside the upload
+            from sym_amd import pyreloc as P
+            from sym_amd import workloads as W
+            x, sc = W.c5_input(HEADLINE_B, HEADLINE_S)
+            plan = P.load_typed_plan(W.c5_plan().blob)
+            bound = P.bind_typed(plan, {"B": HEADLINE_B, "S": HEADLINE_S}, W.param("scale", sc))
+            out = torch.empty(x.size, dtype=torch.int8, device="cuda")
+            for _ in range(3):
+                rep = ctx.execute_h2d(bound, x.ctypes.data, x.nbytes, out.data_ptr(), x.size)
+            kernels[name] = {"family": "permute", "win": 2, "wout": 1, "output_bytes": x.size,
+                             "algorithmic_bytes": (x.nbytes + x.size) // rep["kernel_launches"]
+                                                  + sc.nbytes,
+                             "launches_per_call": rep["kernel_launches"]}
+            del out, x
+            continue
         if name in IX:
             from sym_amd import pyreloc as P
             b, shape, sd, rd, idx = ix_bound(P, name)
@@ -461,6 +492,79 @@ def _pmc_rows(d, counter):
                 if r.get("Counter_Name") == counter:
                     rows.append((r["Kernel_Name"], float(r["Counter_Value"]) * 1024.0))
     return rows
+
+
+def _csv_rows(d, suffix):
+    import csv
+    import glob
+    rows = []
+    for path in glob.glob(os.path.join(d, "**", "*" + suffix), recursive=True):
+        with open(path) as f:
+            rows += list(csv.DictReader(f))
+    return rows
+
+
+def _union(intervals):
+    """Total length of the union of (start, end) intervals."""
+    total, cur_s, cur_e = 0, None, None
+    for s, e in sorted(intervals):
+        if cur_e is None or s > cur_e:
+            if cur_e is not None:
+                total += cur_e - cur_s
+            cur_s, cur_e = s, e
+        else:
+            cur_e = max(cur_e, e)
+    return total + (cur_e - cur_s if cur_e is not None else 0)
+
+
+def summarize_trace(d):
+    """Per-call timeline of the headline upload from a rocprofv3
+    --kernel-trace --memory-copy-trace --marker-trace run with RELX_TRACE=1:
+    host staging ranges, H2D copies and relayout kernels of each call, the
+    share of the call the DMA engines were busy, and how much of each
+    kernel ran under a copy. Prints a markdown table."""
+    marks = _csv_rows(d, "marker_api_trace.csv")
+    copies = [(int(r["Start_Timestamp"]), int(r["End_Timestamp"]))
+              for r in _csv_rows(d, "memory_copy_trace.csv")
+              if r["Direction"] == "MEMORY_COPY_HOST_TO_DEVICE"]
+    kernels = [(int(r["Start_Timestamp"]), int(r["End_Timestamp"]))
+               for r in _csv_rows(d, "kernel_trace.csv") if "k_permute" in r["Kernel_Name"]]
+    # calls begin at chunk 0 of a staged ("stage") or direct ("submit") upload
+    starts = sorted((int(r["Start_Timestamp"]), r["Function"].split()[0])
+                    for r in marks if r["Function"].endswith(" chunk=0") and
+                    r["Function"].split()[0] in ("relx.h2d.stage", "relx.h2d.submit"))
+    stage = [(int(r["Start_Timestamp"]), int(r["End_Timestamp"]))
+             for r in marks if r["Function"].startswith("relx.h2d.stage")]
+    waits = [(int(r["Start_Timestamp"]), int(r["End_Timestamp"]))
+             for r in marks if r["Function"].startswith("relx.h2d.slot_wait")]
+    lines = ["| call | source | span ms | first copy after ms | copies | DMA busy | host staging ms | "
+             "slot waits ms | kernels | kernel time under a copy | tail after last copy us |",
+             "|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    for i, (t0, kind) in enumerate(starts):
+        t1 = starts[i + 1][0] if i + 1 < len(starts) else float("inf")
+        cs = [c for c in copies if t0 <= c[0] < t1]
+        if not cs:
+            continue
+        # the call's kernels: those issued before its last copy landed, and
+        # the batch that follows it (later launches belong to other work)
+        last = max(c[1] for c in cs)
+        ks = [k for k in kernels if t0 <= k[0] < min(t1, last + 1000000)]
+        if not ks:
+            continue
+        end = max(k[1] for k in ks)
+        span = end - t0
+        busy = _union(cs)
+        under = sum(_union([(max(k[0], c[0]), min(k[1], c[1])) for c in cs if c[0] < k[1] and c[1] > k[0]])
+                    for k in ks)
+        ktime = sum(k[1] - k[0] for k in ks)
+        st = sum(e - s for s, e in stage if t0 <= s < end)
+        wt = sum(e - s for s, e in waits if t0 <= s < end)
+        lines.append("| %d | %s | %.3f | %.3f | %d | %.1f%% | %.2f | %.2f | %d | %.1f%% | %.1f |" % (
+            i, "pageable (staged)" if kind == "relx.h2d.stage" else "pinned (direct DMA)",
+            span / 1e6, (min(c[0] for c in cs) - t0) / 1e6, len(cs), 100.0 * busy / span,
+            st / 1e6, wt / 1e6, len(ks), 100.0 * under / max(1, ktime),
+            (end - max(c[1] for c in cs)) / 1e3))
+    print("\n".join(lines))
 
 
 def summarize_pmc(fetch_dir, write_dir, probe):
@@ -603,8 +707,204 @@ def c4_report(torch, ctx, P, args, h2d_ceiling):
                              "steps": len(steps)}}
 
 
+# ------------------------------------------------------------- headline
+
+HEADLINE_B, HEADLINE_S = 64, 4096  # C5 at its largest shape: 2 GiB f16 in, 1 GiB int8 out
+# Staging of the headline's pageable source: the 8 worker threads the
+# reference's typed transfers use (reloc_torch execute_typed_transfer passes
+# the template's threads, 8), and this library's 3-slot pinned ring (measured
+# 98.8% of the PCIe ceiling on C5 64x4096, against 96% with 2 slots).
+GATHER_THREADS, RING_SLOTS = 8, 3
+
+
+def host_view(P, a):
+    return P.BufferView(a.ctypes.data, a.nbytes, 0, list(a.shape),
+                        [st // a.dtype.itemsize for st in a.strides], a.dtype.itemsize, "host")
+
+
+def device_view(P, t):
+    return P.BufferView(t.data_ptr(), t.numel() * t.element_size(), 0, list(t.shape),
+                        list(t.stride()), t.element_size(), "cuda", t.device.index)
+
+
+def cpu_reference_h2d(torch, blob, symbols, params, src, out_bytes, seconds, threads, device=0):
+    """The reference's own `cpu_reference` H2D row (oracle/_ref): its CPU
+    transform of every stage into a 2-slot pinned ring, each slot's H2D on a
+    HIP copy stream (libreloc/src/Dispatch.cpp:452-546,1983-2046;
+    bench/results/typed-h2d-221/README.md:23-36), timed on this host over
+    whole calls until `seconds` have passed (at least two)."""
+    from oracle import ref
+    if not ref.hip_available():
+        return None
+    r = ref.CpuH2dRef(blob, symbols, params, threads=threads, buffers=2, queues=1, device=device)
+    out = torch.empty(out_bytes, dtype=torch.uint8, device="cuda:%d" % device)
+    r.execute(src.ctypes.data, src.nbytes, out.data_ptr(), out_bytes)  # warm: ring, pool
+    n, t0 = 0, time.perf_counter()
+    while True:
+        r.execute(src.ctypes.data, src.nbytes, out.data_ptr(), out_bytes)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and n >= 2:
+            break
+    del r, out
+    return {"value": round(out_bytes * n / el / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "reference",
+            "sample": "%d whole calls in %.1f s of the reference's cpu_reference H2D row "
+                      "(CPU transform into 2 pinned slots, then H2D) on the full headline batch"
+                      % (n, el)}
+
+
+def headline(torch, P, args, h2d_ceiling):
+    """C5 at B=64, S=4096 end to end: one step is one blocking call of the
+    reference-shaped dispatch API from a pageable host tensor (fresh output
+    allocation, bind, prepare, execute, completion), as the reference times
+    its typed H2D rows (bench/results/typed-h2d-221/README.md:31-35)."""
+    from sym_amd import workloads as W
+    B, S = HEADLINE_B, HEADLINE_S
+    log("generating the C5 %dx%d input" % (B, S))
+    x, sc = W.c5_input(B, S)
+    blob = W.c5_plan().blob
+    plan = P.load_typed_plan(blob)
+    syms = {"B": B, "S": S}
+    params = W.param("scale", sc)
+    E = B * S * 4096
+    out_bytes, wire_bytes = E, 2 * E
+    src_view = host_view(P, x)
+    stream = torch.cuda.current_stream().cuda_stream
+    res = P.Resources(0)
+
+    def step(view=src_view):
+        out = torch.empty((B, 32, S, 128), dtype=torch.int8, device="cuda")
+        bound = P.bind_typed(plan, syms, params)
+        req = P.prepare_dispatch(bound, view, device_view(P, out), "h2d")
+        rep = P.execute_dispatch(req, caller_stream=stream, resources=res,
+                                 gather_threads=GATHER_THREADS, n_buffers=RING_SLOTS)
+        return out, rep
+
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    out, rep = step()  # the cold call: ring, wire arena and parameters allocated on the way
+    first_ms = round((time.perf_counter() - t) * 1e3, 3)
+    for _ in range(max(0, args.warmup - 1)):
+        out, rep = step()
+    del out
+    log("first call %.1f ms; %d warmup steps done" % (first_ms, args.warmup))
+    res.time_kernels(True)
+    ts = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ta = time.perf_counter()
+        out, rep = step()
+        ts.append(time.perf_counter() - ta)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    kt = res.kernel_times()
+    res.time_kernels(False)
+    log("%d timed steps: %.2f ms per step" % (args.steps, elapsed / args.steps * 1e3))
+    del out
+    ms_step = elapsed / args.steps * 1e3
+    value = out_bytes * args.steps / elapsed / 1e9
+    p50, p95 = float(np.percentile(ts, 50)), float(np.percentile(ts, 95))
+
+    # The dominant kernel: k_permute, one launch per kernel batch of the
+    # upload (whole batch entries). Its launches inside the steps are timed
+    # by event pairs on their copy stream, which also count the wait from
+    # the batch's last copy to the kernel's start; the roofline takes the
+    # same launch, the same box over B' = B / launches entries, back to back
+    # on one stream with an event pair per launch.
+    launches_per_call = kt["launches"] // max(1, kt["calls"])
+    units = B // max(1, launches_per_call)
+    assert units * launches_per_call == B, (B, launches_per_call)
+    pipeline_ms = kt["ms"] / max(1, kt["chunks"])
+    unit_bytes = S * 4096 * 3  # one batch entry: 2 B of f16 read + 1 B of int8 written per element
+    alg_per_launch = units * unit_bytes + sc.nbytes
+    ub = P.bind_typed(plan, {"B": units, "S": S}, params)
+    _, kernel_ms = device_rate(torch, res, ub, 2 * units * S * 4096, units * S * 4096,
+                               max(100, 4 * args.steps), 10)
+    achieved = alg_per_launch / (kernel_ms * 1e-3) / 1e9
+    copy_gbs = P.measure_copy(0, alg_per_launch // 2, 200, 3)
+
+    # the same steps from a pinned source (direct DMA)
+    pinned = torch.from_numpy(x).pin_memory()
+    pview = P.BufferView(pinned.data_ptr(), x.nbytes, 0, list(x.shape),
+                         [st // 2 for st in x.strides], 2, "host")
+    out, prep_rep = step(pview)
+    pts = []
+    for _ in range(max(5, args.steps // 2)):
+        ta = time.perf_counter()
+        out, prep_rep = step(pview)
+        pts.append(time.perf_counter() - ta)
+    q50 = float(np.percentile(pts, 50))
+    del out, pinned
+    res.close()
+    torch.cuda.synchronize()
+
+    log("pinned source p50 %.2f ms" % (q50 * 1e3))
+    cpu = cpu_all = None
+    if not args.no_cpu:
+        log("cpu baseline")
+        cpu = cpu_reference_h2d(torch, blob, syms, params, x, out_bytes, args.cpu_seconds, 8)
+        cores = len(os.sched_getaffinity(0))
+        cpu_all = (cpu_reference_h2d(torch, blob, syms, params, x, out_bytes, args.cpu_seconds,
+                                     cores) if cores != 8 else cpu)
+    traffic = traffic_for("c5_e2e")
+    return {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seed 20260710: activations N(0,1) as f16, per-head scales U[0.02,0.05])",
+        "config": {"workload": "C5 f16 [64,4096,32,128] -> [B,32,S,128] -> f32 -> int8 "
+                               "(per-head scale, zero-point 0), pageable host source -> HBM",
+                   "B": B, "S": S, "output_bytes": out_bytes, "wire_bytes_per_step": rep["wire_bytes"],
+                   "implementation": rep["implementation"], "chunks_per_step": rep["host_chunks"],
+                   "kernel_launches_per_step": rep["kernel_launches"],
+                   "gather_threads": GATHER_THREADS, "ring_slots": RING_SLOTS,
+                   "step": "torch.empty output + bind_typed + prepare_dispatch + execute_dispatch "
+                           "(blocking, ordered after torch's stream)",
+                   "value_definition": "output bytes x steps / wall time of the steps"},
+        "pcie": {"pinned_h2d_ceiling_GBps": round(h2d_ceiling, 2),
+                 "wire_GBps": round(rep["wire_bytes"] * args.steps / elapsed / 1e9, 2),
+                 "frac": round(rep["wire_bytes"] * args.steps / elapsed / 1e9 / h2d_ceiling, 4),
+                 "p50_ms": round(p50 * 1e3, 3), "p95_ms": round(p95 * 1e3, 3),
+                 "first_call_ms": first_ms,
+                 "pinned_source": {"p50_ms": round(q50 * 1e3, 3),
+                                   "effective_GBps": round(out_bytes / q50 / 1e9, 2),
+                                   "frac": round(prep_rep["wire_bytes"] / q50 / 1e9 / h2d_ceiling, 4),
+                                   "implementation": prep_rep["implementation"]}},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "k_permute<2, 1, 6> (f16 -> f32 -> int8, [B,S,32,128] -> [B,32,S,128])",
+                     "launch": "one kernel batch of the upload: %d batch entries [%d,%d,32,128]"
+                               % (units, units, S),
+                     "kernel_ms_per_launch_events": round(kernel_ms, 5),
+                     "algorithmic_bytes_per_launch": alg_per_launch,
+                     "algorithmic_bytes_per_unit": unit_bytes, "units_per_launch": units,
+                     "in_pipeline": {"launches_timed": kt["launches"],
+                                     "ms_per_launch_events": round(pipeline_ms, 5),
+                                     "achieved": round(alg_per_launch / (pipeline_ms * 1e-3) / 1e9, 1)},
+                     "copy_ceiling": {"GBps": round(copy_gbs, 1), "bytes": alg_per_launch,
+                                      "kernel": "16-byte vector copy of the same bytes",
+                                      "frac": round(achieved / copy_gbs, 4)}},
+        "cpu_baseline": cpu,
+        "cpu_baseline_all_cores": cpu_all,
+        "host": host_info(),
+    }
+
+
 def main():
     args = parse()
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace)
+        return
     if args.summarize_pmc:
         probe = None
         for d in args.summarize_pmc:
@@ -676,67 +976,7 @@ def main():
         ctx.close()
         return
 
-    # ---------------------------------------------------- headline: C2
-    case = make_case("c2")
-    ms_step, kms = device_rate(torch, ctx, case.bound, case.wire_bytes, case.out_bytes,
-                               args.steps, args.warmup)
-    value = case.out_bytes / (ms_step * 1e-3) / 1e9
-    alg = case.wire_bytes + case.out_bytes
-    achieved = alg / (ms_step * 1e-3) / 1e9
-    p50, p95, rep = e2e_rate(torch, ctx, case, args.e2e_samples, pinned=False)
-    q50, q95, prep = e2e_rate(torch, ctx, case, args.e2e_samples, pinned=True)
-    f50, f95, frep = e2e_rate(torch, ctx, case, args.e2e_samples, pinned=False, host_stages=0)
-    first_ms = first_call_ms(torch, P, case)
-    # the size-matched copy ceiling: a 16-byte vector copy moving the same
-    # number of bytes (half read, half written)
-    copy_gbs = P.measure_copy(0, alg // 2, 200, 3)
-    cpu = cpu_all = None
-    if not args.no_cpu:
-        cpu = cpu_baseline(case, args.cpu_seconds, 8)
-        cores = len(os.sched_getaffinity(0))
-        cpu_all = cpu_baseline(case, args.cpu_seconds, cores) if cores != 8 else cpu
-    line = {
-        "metric": METRIC,
-        "value": round(value, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 6),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic (seed 20260710, N(0,1) fp32)",
-        "config": {"workload": case.workload, "kernel": "interleave", "result_dtype": "f16",
-                   "output_bytes": case.out_bytes, "wire_bytes_per_step": case.wire_bytes,
-                   "value_definition": "output bytes / step time, wire resident in HBM"},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_for("c2"), "kernel_ms": round(ms_step, 5),
-                     "kernel_ms_per_launch_events": round(kms, 5),
-                     "algorithmic_bytes": alg,
-                     "copy_ceiling": {"GBps": round(copy_gbs, 1), "bytes": alg,
-                                      "kernel": "16-byte vector copy of the same bytes",
-                                      "frac": round(achieved / copy_gbs, 4)}},
-        "e2e": {"pinned_h2d_ceiling_GBps": round(h2d_ceiling, 2),
-                "first_call_ms": first_ms,
-                "pageable": {"p50_ms": round(p50 * 1e3, 3), "p95_ms": round(p95 * 1e3, 3),
-                             "effective_GBps": round(case.out_bytes / p50 / 1e9, 2),
-                             "wire_bytes": rep["wire_bytes"], "implementation": rep["implementation"],
-                             "pcie_frac": round(rep["wire_bytes"] / p50 / 1e9 / h2d_ceiling, 4)},
-                "pageable_f32_wire": {"p50_ms": round(f50 * 1e3, 3),
-                                      "effective_GBps": round(case.out_bytes / f50 / 1e9, 2),
-                                      "wire_bytes": frep["wire_bytes"],
-                                      "pcie_frac": round(frep["wire_bytes"] / f50 / 1e9 / h2d_ceiling, 4)},
-                "pinned": {"p50_ms": round(q50 * 1e3, 3), "p95_ms": round(q95 * 1e3, 3),
-                           "effective_GBps": round(case.out_bytes / q50 / 1e9, 2),
-                           "wire_bytes": prep["wire_bytes"], "implementation": prep["implementation"],
-                           "pcie_frac": round(prep["wire_bytes"] / q50 / 1e9 / h2d_ceiling, 4)}},
-        "cpu_baseline": cpu,
-        "cpu_baseline_all_cores": cpu_all,
-        "host": host_info(),
-    }
+    line = headline(torch, P, args, h2d_ceiling)
     ctx.close()
     print(json.dumps(line), flush=True)
 

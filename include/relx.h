@@ -342,6 +342,22 @@ int relx_verify_launches(const relx_bound *bound, int wire_boundary, int64_t chu
  * launches selected a channel outside its parameters. */
 int relx_ctx_synchronize(relx_ctx *ctx, relx_err *err);
 
+/* Kernel timing of a context's blocking uploads (relx_execute_h2d and
+ * relx_execute_group_h2d without no_wait): when enabled, each chunk's
+ * relayout launches are bracketed by timing events on the copy stream they
+ * run on (the first completes when the chunk's copy has landed), and the
+ * elapsed times are summed when the call completes. Enabling resets the
+ * sums. The device-side counterpart of the reference's trace ranges
+ * (libreloc/src/Trace.h:15-39); no other counterpart. */
+typedef struct relx_kernel_times {
+  int64_t calls;    /* timed calls */
+  int64_t chunks;   /* timed chunks (one event pair each) */
+  int64_t launches; /* kernel launches inside them */
+  double ms;        /* summed elapsed milliseconds */
+} relx_kernel_times;
+int relx_ctx_time_kernels(relx_ctx *ctx, int enable, relx_err *err);
+int relx_ctx_kernel_times(relx_ctx *ctx, relx_kernel_times *out, relx_err *err);
+
 /* Pinned host memory helpers (hipHostMalloc / hipHostFree). */
 int relx_host_alloc(size_t bytes, void **out, relx_err *err);
 int relx_host_free(void *p);

@@ -150,3 +150,75 @@ class IndexedRef(TypedRef):
         if not self.h:
             raise RuntimeError(err.value.decode())
         self.result_bytes = L.ref_typed_result_bytes(self.h)
+
+
+HIP_LIB_PATH = os.path.join(HERE, "_ref", "libreloc_ref_hip.so")
+_hip = None
+
+
+def hip_available():
+    return os.path.exists(HIP_LIB_PATH)
+
+
+def hip_lib():
+    """libreloc_ref_hip.so: the reference's cpu_reference H2D row (CPU
+    transform into pinned ring slots, then hipMemcpyAsync of each slot) on a
+    HIP CopyBackend. Loads torch first so one HIP runtime serves both."""
+    global _hip
+    if _hip is None:
+        import torch  # noqa: F401
+        lib()  # libreloc_ref.so, which the HIP driver links against
+        L = ctypes.CDLL(HIP_LIB_PATH)
+        vp, cp, sz = ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t
+        L.ref_cpu_h2d_prepare.restype = vp
+        L.ref_cpu_h2d_prepare.argtypes = [cp, sz, ctypes.POINTER(cp), ctypes.POINTER(ctypes.c_int64),
+                                          ctypes.c_int, ctypes.POINTER(cp), ctypes.POINTER(ctypes.c_int),
+                                          ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int64),
+                                          ctypes.POINTER(vp), ctypes.POINTER(sz), ctypes.c_int,
+                                          ctypes.c_uint, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                          cp, sz]
+        L.ref_cpu_h2d_result_bytes.restype = ctypes.c_int64
+        L.ref_cpu_h2d_result_bytes.argtypes = [vp]
+        L.ref_cpu_h2d_execute.restype = ctypes.c_int
+        L.ref_cpu_h2d_execute.argtypes = [vp, vp, sz, vp, sz, cp, sz]
+        L.ref_cpu_h2d_free.argtypes = [vp]
+        _hip = L
+    return _hip
+
+
+class CpuH2dRef:
+    """The reference's CPU H2D path end to end: a typed plan through the
+    cpu_reference dispatch row (transform on `threads` workers into
+    `buffers` pinned slots, each slot's H2D on `queues` streams), a layout
+    plan through executeTransfer; `execute` blocks until the result is in
+    device memory."""
+
+    def __init__(self, blob, symbols, params=None, threads=8, buffers=2, queues=1, device=0):
+        L = hip_lib()
+        sn, sv, ns = _syms(symbols)
+        params = params or {}
+        names = list(params)
+        np_ = max(1, len(names))
+        pn = (ctypes.c_char_p * np_)(*[n.encode() for n in names])
+        pk = (ctypes.c_int * np_)(*[KINDS[params[n][0]][0] for n in names])
+        pb = (ctypes.c_int * np_)(*[KINDS[params[n][0]][1] for n in names])
+        pl = (ctypes.c_int64 * np_)(*[(params[n][1][0] if params[n][1] else -1) for n in names])
+        self._keep = [ctypes.create_string_buffer(params[n][2], len(params[n][2])) for n in names]
+        pd = (ctypes.c_void_p * np_)(*[ctypes.addressof(b) for b in self._keep])
+        psz = (ctypes.c_size_t * np_)(*[len(params[n][2]) for n in names])
+        err = ctypes.create_string_buffer(512)
+        self.h = L.ref_cpu_h2d_prepare(blob, len(blob), sn, sv, ns, pn, pk, pb, pl, pd, psz,
+                                       len(names), threads, buffers, queues, device, err, 512)
+        if not self.h:
+            raise RuntimeError(err.value.decode())
+        self.result_bytes = L.ref_cpu_h2d_result_bytes(self.h)
+
+    def execute(self, src_ptr, src_bytes, dst_ptr, dst_bytes):
+        err = ctypes.create_string_buffer(512)
+        if hip_lib().ref_cpu_h2d_execute(self.h, src_ptr, src_bytes, dst_ptr, dst_bytes, err, 512):
+            raise RuntimeError(err.value.decode())
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            hip_lib().ref_cpu_h2d_free(self.h)
+            self.h = None

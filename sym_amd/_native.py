@@ -75,6 +75,11 @@ class relx_report(ctypes.Structure):
                 for f, _ in self._fields_}
 
 
+class relx_kernel_times(ctypes.Structure):
+    _fields_ = [("calls", ctypes.c_int64), ("chunks", ctypes.c_int64),
+                ("launches", ctypes.c_int64), ("ms", ctypes.c_double)]
+
+
 # every entry point include/relx.h declares, with its ctypes signature
 _VP, _SZ, _I, _I64, _U64 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int64, ctypes.c_uint64
 _E = ctypes.POINTER(relx_err)
@@ -118,6 +123,8 @@ SIGNATURES = {
     "relx_host_stage": (_I, [_VP, _I, _VP, _VP, _I, _E]),
     "relx_verify_launches": (_I, [_VP, _I, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64), _E]),
     "relx_ctx_synchronize": (_I, [_VP, _E]),
+    "relx_ctx_time_kernels": (_I, [_VP, _I, _E]),
+    "relx_ctx_kernel_times": (_I, [_VP, ctypes.POINTER(relx_kernel_times), _E]),
     "relx_host_alloc": (_I, [_SZ, ctypes.POINTER(_VP), _E]),
     "relx_host_free": (_I, [_VP]),
     "relx_measure_h2d": (ctypes.c_double, [_I, _SZ, _I, _I]),

@@ -550,6 +550,29 @@ int relx_ctx_synchronize(relx_ctx *ctx, relx_err *err) {
   });
 }
 
+int relx_ctx_time_kernels(relx_ctx *ctx, int enable, relx_err *err) {
+  return guarded(err, [&] {
+    if (!ctx)
+      throw relx::Error("invalid_argument", "null context");
+    std::lock_guard<std::mutex> g(ctx->ctx->mu);
+    ctx->ctx->time_kernels = enable != 0;
+    ctx->ctx->kt = relx::KernelTimes{};
+  });
+}
+
+int relx_ctx_kernel_times(relx_ctx *ctx, relx_kernel_times *out, relx_err *err) {
+  return guarded(err, [&] {
+    if (!ctx || !out)
+      throw relx::Error("invalid_argument", "null argument");
+    std::lock_guard<std::mutex> g(ctx->ctx->mu);
+    const relx::KernelTimes &k = ctx->ctx->kt;
+    out->calls = k.calls;
+    out->chunks = k.chunks;
+    out->launches = k.launches;
+    out->ms = k.ms;
+  });
+}
+
 int relx_host_alloc(size_t bytes, void **out, relx_err *err) {
   return guarded(err, [&] {
     if (!out)

@@ -16,10 +16,12 @@
 // A page-locked source skips the ring and is DMA'd in place.
 #include "runtime.h"
 
+#include <dlfcn.h>
 #include <immintrin.h>
 
 #include <algorithm>
 #include <chrono>
+#include <cstdlib>
 #include <cstring>
 
 #include "../../include/relx.h"
@@ -111,6 +113,53 @@ void host_transform(const Prepared &p, uint32_t k, uint32_t src_width, const voi
   }
 }
 
+// ------------------------------------------------------------ tracing
+
+namespace {
+
+struct Roctx {
+  int (*push)(const char *) = nullptr;
+  int (*pop)() = nullptr;
+};
+
+// The ROCTX entry points when RELX_TRACE=1 and the library opens; else none.
+const Roctx &roctx() {
+  static const Roctx r = [] {
+    Roctx t;
+    const char *env = std::getenv("RELX_TRACE");
+    if (!env || std::strcmp(env, "1") != 0)
+      return t;
+    void *h = dlopen("librocprofiler-sdk-roctx.so.1", RTLD_NOW | RTLD_GLOBAL);
+    if (!h)
+      h = dlopen("/opt/rocm/lib/librocprofiler-sdk-roctx.so.1", RTLD_NOW | RTLD_GLOBAL);
+    if (!h)
+      return t;
+    t.push = reinterpret_cast<int (*)(const char *)>(dlsym(h, "roctxRangePushA"));
+    t.pop = reinterpret_cast<int (*)()>(dlsym(h, "roctxRangePop"));
+    if (!t.push || !t.pop)
+      t = Roctx{};
+    return t;
+  }();
+  return r;
+}
+
+} // namespace
+
+TraceRange::TraceRange(const char *name, int64_t chunk) {
+  const Roctx &r = roctx();
+  if (!r.push)
+    return;
+  char buf[96];
+  std::snprintf(buf, sizeof(buf), "%s chunk=%lld", name, static_cast<long long>(chunk));
+  r.push(buf);
+  open_ = true;
+}
+
+TraceRange::~TraceRange() {
+  if (open_)
+    roctx().pop();
+}
+
 // ------------------------------------------------------------ handles
 
 const DeviceProgram &BoundHandle::program(uint32_t k) {
@@ -196,6 +245,16 @@ void join_copy_streams(Context &ctx, hipStream_t s, int64_t used) {
     HIPCHECK(hipEventRecord(ctx.join_ev[i], ctx.copies[i]));
     HIPCHECK(hipStreamWaitEvent(s, ctx.join_ev[i], 0));
   }
+}
+
+// The i-th pair of kernel timing events (created on first use, kept).
+hipEvent_t *timing_pair(Context &ctx, size_t i) {
+  while (ctx.time_ev.size() < 2 * (i + 1)) {
+    hipEvent_t e;
+    HIPCHECK(hipEventCreate(&e));
+    ctx.time_ev.push_back(e);
+  }
+  return &ctx.time_ev[2 * i];
 }
 
 // Every copy stream waits for `ev`.
@@ -425,6 +484,9 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
   int slot = 0;
   int64_t nchunk = 0; // chunks of every member so far: picks the copy stream
   relx_report sum{};
+  // Kernel timing covers blocking calls, whose events are read at the end.
+  const bool timing = ctx.time_kernels && !comp && !opt.no_wait;
+  size_t tpairs = 0;
   for (size_t mi = 0; mi < ms.size(); ++mi) {
     Member &m = ms[mi];
     const DeviceProgram &dp = *m.dp;
@@ -464,16 +526,24 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
       launches = index_select_device(ctx, *m.h, wire, static_cast<size_t>(bd.table_bytes), m.dst,
                                      m.dst_bytes, cs);
     }
+    const KernelBatches kb = kernel_batches(p);
+    int64_t kb0 = 0; // first unit of the kernel batch being gathered
     for (int64_t v0 = 0; v0 < (m.table ? 0 : p.units); v0 += p.per_chunk) {
       const int64_t v1 = std::min(p.units, v0 + p.per_chunk);
       const int64_t woff = v0 * p.unit_wire, wbytes = (v1 - v0) * p.unit_wire;
+      const int64_t chunk_no = nchunk;
       hipStream_t cs = ctx.copy_stream(nchunk++);
       if (m.direct) {
+        TraceRange tr("relx.h2d.submit", chunk_no);
         HIPCHECK(hipMemcpyAsync(wire + woff, m.src + woff, static_cast<size_t>(wbytes),
                                 hipMemcpyHostToDevice, cs));
       } else {
         uint8_t *s = static_cast<uint8_t *>(ctx.slots[static_cast<size_t>(slot)]);
-        HIPCHECK(hipEventSynchronize(ctx.slot_ev[static_cast<size_t>(slot)]));
+        {
+          TraceRange tr("relx.h2d.slot_wait", chunk_no);
+          HIPCHECK(hipEventSynchronize(ctx.slot_ev[static_cast<size_t>(slot)]));
+        }
+        TraceRange tr("relx.h2d.stage", chunk_no);
         const int64_t e0 = v0 * (p.unit_src / sw), e1 = v1 * (p.unit_src / sw);
         const int64_t ne = e1 - e0;
         const uint8_t *src_base = m.src + e0 * sw;
@@ -496,9 +566,26 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
         HIPCHECK(hipEventRecord(ctx.slot_ev[static_cast<size_t>(slot)], cs));
         slot = (slot + 1) % static_cast<int>(ctx.slots.size());
       }
-      launches += launch_program(dp, v0, v1, v0 == 0, v1 == p.units, wire, m.dst, par.pf, par.pi,
-                                 status, cs);
       ++chunks;
+      if (v1 < kb.end(kb0))
+        continue; // the kernel batch takes more chunks
+      // The batch's launches follow this chunk's copy on its stream, and the
+      // other copy stream's copies of the batch through an event.
+      if (kb0 < v0 && two_streams)
+        join_copy_streams(ctx, cs, nchunk);
+      // Timing events bracket the batch's launches on the stream they run
+      // on; the first completes when the batch's copies have landed.
+      hipEvent_t *tev = timing ? timing_pair(ctx, tpairs++) : nullptr;
+      if (tev)
+        HIPCHECK(hipEventRecord(tev[0], cs));
+      const int64_t nl = launch_program(dp, kb0, v1, kb0 == 0, v1 == p.units, wire, m.dst,
+                                        par.pf, par.pi, status, cs);
+      if (tev) {
+        HIPCHECK(hipEventRecord(tev[1], cs));
+        ctx.kt.launches += nl;
+      }
+      launches += nl;
+      kb0 = v1;
     }
     if (m.report) {
       relx_report &r = *m.report;
@@ -550,6 +637,15 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
   }
   HIPCHECK(hipEventSynchronize(ctx.done_ev));
   ctx.unsynced = false;
+  if (timing) {
+    for (size_t i = 0; i < tpairs; ++i) {
+      float ms = 0.0f;
+      HIPCHECK(hipEventElapsedTime(&ms, ctx.time_ev[2 * i], ctx.time_ev[2 * i + 1]));
+      ctx.kt.ms += ms;
+    }
+    ctx.kt.chunks += static_cast<int64_t>(tpairs);
+    ++ctx.kt.calls;
+  }
   if (any_generic) {
     if (read_status(status))
       throw Error("channel_out_of_range", "a stage selected a channel outside its parameters");
@@ -673,6 +769,7 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
   std::vector<Pending> pending; // copies issued, not yet copied out of their slot
   size_t next = 0;
   auto consume = [&](const Pending &p) {
+    TraceRange tr("relx.d2h.copy_out", p.off / std::max<int64_t>(1, per * row));
     HIPCHECK(hipEventSynchronize(ctx.slot_ev[static_cast<size_t>(p.slot)]));
     const uint8_t *from = static_cast<const uint8_t *>(ctx.slots[static_cast<size_t>(p.slot)]);
     ctx.workers->parallel_for(p.bytes, int64_t{1} << 20, [&](int64_t x, int64_t y) {
@@ -694,6 +791,7 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
    }
    for (int64_t u0 = 0; u0 < units; u0 += per) {
     const int64_t u1 = std::min(units, u0 + per);
+    TraceRange tr("relx.d2h.submit", chunks);
     if (axis >= 0 || u0 == 0) {
       launches += launch_all(dp, prefix_launches(dp, fixed, axis, u0, u1), src, result, par.pf,
                              par.pi, status, ctx.compute);
@@ -826,6 +924,9 @@ void destroy_context(Context &ctx) {
       (void)hipEventDestroy(e);
       e = nullptr;
     }
+  for (hipEvent_t e : ctx.time_ev)
+    (void)hipEventDestroy(e);
+  ctx.time_ev.clear();
   if (ctx.wire)
     (void)hipFree(ctx.wire);
   ctx.wire = nullptr;
@@ -871,6 +972,13 @@ ChunkPlan chunk_plan(const DeviceProgram &dp, uint32_t src_width, int64_t chunk_
   return p;
 }
 
+KernelBatches kernel_batches(const ChunkPlan &p) {
+  const int64_t chunks = (p.units + p.per_chunk - 1) / p.per_chunk;
+  int64_t n = kKernelBatchBytes / std::max<int64_t>(1, p.per_chunk * p.unit_wire);
+  n = std::max<int64_t>(1, std::min(n, chunks / 4));
+  return {p.units, n * p.per_chunk};
+}
+
 int64_t verify_launches(BoundHandle &h, uint32_t k, int64_t chunk_bytes) {
   const DeviceProgram &dp = h.program(k);
   int64_t n = 0;
@@ -898,8 +1006,11 @@ int64_t verify_launches(BoundHandle &h, uint32_t k, int64_t chunk_bytes) {
   };
   for (int direct = 0; direct < (chunk_bytes > 0 ? 1 : 2); ++direct) {
     const ChunkPlan p = chunk_plan(dp, source_width(*h.bound), chunk_bytes, direct != 0);
-    for (int64_t v0 = 0; v0 < p.units; v0 += p.per_chunk) {
-      const int64_t v1 = std::min(p.units, v0 + p.per_chunk);
+    const KernelBatches kb = kernel_batches(p);
+    for (int64_t v0 = 0; v0 < p.units; v0 = kb.end(v0)) {
+      const int64_t v1 = kb.end(v0);
+      if (v0 % p.per_chunk || (v1 % p.per_chunk && v1 != p.units))
+        throw Error("internal_launch_check", "a kernel batch does not end on a chunk boundary");
       for (const KArgs &a : box_launches(dp, v0, v1, v0 == 0, v1 == p.units))
         check(a);
     }

@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <condition_variable>
 #include <cstdint>
@@ -114,6 +115,20 @@ int64_t default_chunk_bytes(int64_t total, bool h2d, bool direct);
 uint32_t source_width(const Bound &b);
 ChunkPlan chunk_plan(const DeviceProgram &dp, uint32_t src_width, int64_t chunk_bytes, bool direct);
 
+// The kernel launches of an upload each cover a batch of landed chunks. A
+// launch streams at the HBM rate only from a few hundred MB up (C5's
+// permute: 50 MB per launch at 51% of peak, 400 MB at 70%), while a chunk's
+// copy takes far longer than its share of the kernel, so a batch takes
+// chunks until it holds kKernelBatchBytes of wire. A member keeps at least
+// four batches, so that the last one, which runs after the last copy,
+// stays short.
+constexpr int64_t kKernelBatchBytes = int64_t{256} << 20;
+struct KernelBatches {
+  int64_t units, per; // chunk-axis units, units per batch (whole chunks)
+  int64_t end(int64_t k0) const { return std::min(units, k0 + per); }
+};
+KernelBatches kernel_batches(const ChunkPlan &p);
+
 // Host staging transform: source elements [e0, e1) at boundary 0 -> wire
 // elements at boundary `k` (leading per-tensor stages applied elementwise).
 void host_transform(const Prepared &p, uint32_t k, uint32_t src_width, const void *src, void *dst,
@@ -210,6 +225,29 @@ uint32_t auto_host_stages(const BoundHandle &h);
 // launch of the device-resident path; returns the count.
 int64_t verify_launches(BoundHandle &h, uint32_t k, int64_t chunk_bytes);
 
+// A ROCTX range on the calling thread around one host phase of the pipeline
+// (the reference's TraceRange, libreloc/src/Trace.h:15-39, which its NVTX
+// builds emit at libreloc/src/Pipeline.cpp:204,213). Enabled at run time by
+// the environment variable RELX_TRACE=1, which opens the ROCTX library on
+// first use; otherwise a range costs one branch. The name carries the chunk.
+class TraceRange {
+public:
+  TraceRange(const char *name, int64_t chunk);
+  ~TraceRange();
+  TraceRange(const TraceRange &) = delete;
+  TraceRange &operator=(const TraceRange &) = delete;
+
+private:
+  bool open_ = false;
+};
+
+// Kernel timing of blocking uploads (relx_ctx_time_kernels): per chunk, the
+// elapsed time between events recorded before and after its launches.
+struct KernelTimes {
+  int64_t calls = 0, chunks = 0, launches = 0;
+  double ms = 0.0;
+};
+
 #ifndef RELX_COPY_STREAMS
 #define RELX_COPY_STREAMS 2
 #endif
@@ -246,6 +284,9 @@ struct Context {
   bool check_pending[64] = {};
   uint32_t check_next = 0;
   bool channel_error = false; // a resolved check found its flag set
+  bool time_kernels = false;
+  KernelTimes kt;
+  std::vector<hipEvent_t> time_ev; // timing event pairs, reused call to call
   std::unique_ptr<Workers> workers;
   unsigned worker_threads = 0;
   int64_t max_retained = 0;

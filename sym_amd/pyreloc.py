@@ -481,6 +481,21 @@ class Context:
         if N.lib().relx_ctx_synchronize(self._h, ctypes.byref(err)):
             _raise(err)
 
+    def time_kernels(self, enable=True):
+        """Bracket each chunk's relayout launches of later blocking uploads
+        with timing events (resets the sums)."""
+        err = N.relx_err()
+        if N.lib().relx_ctx_time_kernels(self._h, 1 if enable else 0, ctypes.byref(err)):
+            _raise(err)
+
+    def kernel_times(self):
+        """{calls, chunks, launches, ms} summed over the timed uploads."""
+        t = N.relx_kernel_times()
+        err = N.relx_err()
+        if N.lib().relx_ctx_kernel_times(self._h, ctypes.byref(t), ctypes.byref(err)):
+            _raise(err)
+        return {f: getattr(t, f) for f, _ in t._fields_}
+
     def stats(self):
         s = N.relx_ctx_stats()
         N.lib().relx_ctx_stats_get(self._h, ctypes.byref(s))

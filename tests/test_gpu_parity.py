@@ -323,8 +323,9 @@ def _c5_expected(x, s, b_idx=None):
 
 @pytest.mark.parametrize("B,S", W.C5_SHAPES)
 def test_c5_activation_quant(ctx, B, S):
-    """One plan bound per (B, S). Whole-output check up to E = 32M elements;
-    beyond that every element of two sampled batch entries."""
+    """One plan bound per (B, S); every output element is checked against the
+    oracle (by groups of batch entries past E = 32M elements, to bound the
+    oracle's memory)."""
     plan = W.c5_plan()
     x, s = W.c5_input(B, S, seed=B * 10007 + S)
     out, rep, b = run_h2d(ctx, plan.blob, {"B": B, "S": S}, W.param("scale", s), x,
@@ -335,8 +336,10 @@ def test_c5_activation_quant(ctx, B, S):
     if E <= 33554432:
         assert np.array_equal(got, _c5_expected(x, s))
     else:
-        picks = sorted({0, B - 1, B // 2})
-        assert np.array_equal(got[picks], _c5_expected(x, s, picks))
+        step = max(1, 33554432 // (S * 4096))
+        for b0 in range(0, B, step):
+            picks = list(range(b0, min(B, b0 + step)))
+            assert np.array_equal(got[picks], _c5_expected(x, s, picks)), picks
 
 
 # -------------------------------------------------------- value sweeps
