@@ -235,6 +235,24 @@ int relx_execute_h2d(relx_ctx *ctx, const relx_bound *bound, const void *src, si
                      void *dst, size_t dst_bytes, const relx_options *opt, relx_report *report,
                      relx_err *err);
 
+/* The upload of relx_execute_h2d with no allocation: the call allocates no
+ * device or pinned host memory (no hipMalloc, hipFree, hipHostMalloc or
+ * allocating library routine). No counterpart in the reference; it is for
+ * callers that cannot allocate: code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation. The wire is staged in the
+ * library's static device scratch, a file-scope array of 64 MiB that each
+ * GPU the library runs on holds until the process ends (63 MiB of wire, and
+ * parameter tables of up to 512 KiB of floats and 512 KiB of ints), and the
+ * source must be page-locked: it crosses by direct DMA, with no host stages.
+ * Errors: "insufficient_capacity" for a wire or parameter tables beyond
+ * those limits, "invalid_options" for a pageable source or host stages,
+ * "plan_mismatch" for an indexed plan, else as relx_execute_h2d. Every call
+ * on a GPU shares that GPU's scratch and leaves its contents behind: calls
+ * that overlap on one GPU (from several contexts or threads) race. */
+int relx_execute_h2d_static(relx_ctx *ctx, const relx_bound *bound, const void *src,
+                            size_t src_bytes, void *dst, size_t dst_bytes, const relx_options *opt,
+                            relx_report *report, relx_err *err);
+
 /* A group of bound plans as one schedule: all members' wire bytes through
  * one ring and one event barrier (reference group_detail::executeGroup,
  * libreloc/src/Dispatch.cpp:1833-1981; pyreloc.execute_dispatch_group).

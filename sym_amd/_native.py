@@ -104,6 +104,8 @@ SIGNATURES = {
     "relx_ctx_stats_get": (_I, [_VP, ctypes.POINTER(relx_ctx_stats)]),
     "relx_execute_h2d": (_I, [_VP, _VP, _VP, _SZ, _VP, _SZ, ctypes.POINTER(relx_options),
                               ctypes.POINTER(relx_report), _E]),
+    "relx_execute_h2d_static": (_I, [_VP, _VP, _VP, _SZ, _VP, _SZ, ctypes.POINTER(relx_options),
+                                     ctypes.POINTER(relx_report), _E]),
     "relx_execute_group_h2d": (_I, [_VP, _I, ctypes.POINTER(_VP), ctypes.POINTER(_VP),
                                     ctypes.POINTER(_SZ), ctypes.POINTER(_VP), ctypes.POINTER(_SZ),
                                     ctypes.POINTER(relx_options), ctypes.POINTER(relx_report),

@@ -26,7 +26,7 @@ DEVICE = ["--offload-arch=" + ARCH, "-mcode-object-version=5", "-fno-gpu-flush-d
 SOURCES = ["plan.cpp", "program.cpp", "runtime.cpp", "workers.cpp", "indexed.cpp", "capi.cpp",
            "kernels.hip",
            "k_stream_fast.hip", "k_stream_generic.hip", "k_transpose.hip", "k_interleave.hip",
-           "k_interleave_generic.hip", "k_permute.hip", "k_gather.hip", "k_copy.hip"]
+           "k_interleave_generic.hip", "k_permute.hip", "k_gather.hip", "k_copy.hip", "noalloc.hip"]
 
 
 # The one-level interleave takes its hot arguments as leading scalars that

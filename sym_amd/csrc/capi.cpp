@@ -20,6 +20,8 @@ void destroy_context(Context &ctx);
 void relayout_device(Context &ctx, BoundHandle &h, uint32_t k, const void *wire, void *dst,
                      hipStream_t stream);
 void resolve_checks(Context &ctx);
+void execute_static(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes, void *dst,
+                    size_t dst_bytes, const relx_options &opt, relx_report *report);
 double measure_h2d(int device, size_t bytes, int iters, int rounds);
 double measure_copy(int device, size_t bytes, int iters, int rounds, bool d2h);
 } // namespace relx
@@ -450,6 +452,42 @@ int relx_execute_d2h(relx_ctx *ctx, const relx_bound *bound, const void *src, si
       throw relx::Error("invalid_options", "device-to-host runs every stage on the device");
     relx::execute_d2h(c, const_cast<relx::BoundHandle &>(bound->h), src, src_bytes, dst,
                       dst_bytes, o, report);
+  });
+  if (rc != RELX_OK) {
+    ++c.failures;
+    const bool complete = relx::drain(c);
+    if (err)
+      err->completion = complete ? RELX_COMPLETE : RELX_UNKNOWN;
+    if (!complete)
+      c.quarantined = true;
+  }
+  return rc;
+}
+
+int relx_execute_h2d_static(relx_ctx *ctx, const relx_bound *bound, const void *src,
+                            size_t src_bytes, void *dst, size_t dst_bytes, const relx_options *opt,
+                            relx_report *report, relx_err *err) {
+  if (!ctx) {
+    set_err(err, "invalid_argument", "null context");
+    return RELX_ERROR;
+  }
+  relx::Context &c = *ctx->ctx;
+  std::lock_guard<std::mutex> g(c.mu);
+  if (c.closed || c.quarantined) {
+    set_err(err, "resources_closed", "context is closed or quarantined");
+    return RELX_ERROR;
+  }
+  relx_options o{};
+  o.host_stages = -1;
+  o.source_pinned = -1;
+  if (opt)
+    o = *opt;
+  ++c.calls;
+  const int rc = guarded(err, [&] {
+    if (!bound)
+      throw relx::Error("invalid_argument", "null bound plan");
+    relx::execute_static(c, const_cast<relx::BoundHandle &>(bound->h), src, src_bytes, dst,
+                         dst_bytes, o, report);
   });
   if (rc != RELX_OK) {
     ++c.failures;

@@ -352,10 +352,22 @@ struct Member {
   int64_t arena_bytes; // wire arena bytes of this member
 };
 
+// The device memory an allocation-free call uses in place of the context's
+// wire arena and the bound plan's parameter tables: regions of the
+// library's static scratch array, and the host tables uploaded into it.
+struct StaticScratch {
+  uint8_t *wire;
+  size_t wire_cap;
+  float *pf;
+  int32_t *pi;
+  const std::vector<float> *host_pf;
+  const std::vector<int32_t> *host_pi;
+};
+
 } // namespace
 
 void execute(Context &ctx, std::vector<Member> &members, const relx_options &opt,
-             relx_report *total, Completion *comp);
+             relx_report *total, Completion *comp, const StaticScratch *sc = nullptr);
 
 } // namespace relx
 
@@ -418,12 +430,70 @@ void execute_members(Context &ctx, int n, BoundHandle *const *bounds, const void
   execute(ctx, ms, opt, total, comp);
 }
 
+// The allocation-free upload: the pipeline above with the wire staged in the
+// library's static device scratch and the parameter tables uploaded into it,
+// from a page-locked source by direct DMA (no ring), with no worker pool and
+// no timing events. It allocates no device or pinned host memory.
+void execute_static(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes, void *dst,
+                    size_t dst_bytes, const relx_options &opt, relx_report *report) {
+  DeviceGuard guard(ctx.device);
+  if (!ctx.scratch || !ctx.param_stage)
+    throw Error("backend_failure", "the static scratch is not mapped on this context's device");
+  const Bound &b = *h.bound;
+  if (b.indexed)
+    throw Error("plan_mismatch", "the allocation-free upload takes layout and typed plans; "
+                                 "indexed plans gather host rows through the staging ring");
+  if (opt.host_stages > 0)
+    throw Error("invalid_options", "the allocation-free upload applies no host stages: "
+                                   "the source crosses as it is");
+  if (!src || !dst)
+    throw Error("invalid_view", "null source or destination");
+  const bool pinned = opt.source_pinned > 0 || (opt.source_pinned < 0 && probe_pinned(src));
+  if (!pinned)
+    throw Error("invalid_options", "the allocation-free upload needs a page-locked source: "
+                                   "it has no staging ring to allocate");
+  const DeviceProgram &dp = h.program(0);
+  const int64_t need_src = b.typed ? b.source_bytes : dp.wire_elems * b.layout.element_size;
+  if (static_cast<int64_t>(src_bytes) < need_src)
+    throw Error("insufficient_capacity", "source holds " + std::to_string(src_bytes) +
+                                             " bytes, the plan reads " + std::to_string(need_src));
+  const int64_t need_dst = dp.dst_elems * dp.base.wout;
+  if (static_cast<int64_t>(dst_bytes) < need_dst)
+    throw Error("insufficient_capacity", "destination holds " + std::to_string(dst_bytes) +
+                                             " bytes, the plan writes " + std::to_string(need_dst));
+  if (static_cast<size_t>(dp.wire_bytes) > kScratchWireBytes)
+    throw Error("insufficient_capacity",
+                "the plan's wire is " + std::to_string(dp.wire_bytes) +
+                    " bytes; the allocation-free upload stages at most " +
+                    std::to_string(kScratchWireBytes) + " bytes");
+  if (dp.pf.size() * sizeof(float) > kParamStageHalf ||
+      dp.pi.size() * sizeof(int32_t) > kParamStageHalf)
+    throw Error("insufficient_capacity", "the plan's parameter tables exceed the static scratch's " +
+                                             std::to_string(kParamStageHalf) + "-byte tables");
+  if (ctx.unsynced) { // an earlier call may still read the pinned parameter staging
+    HIPCHECK(hipEventSynchronize(ctx.done_ev));
+    ctx.unsynced = false;
+  }
+  std::vector<Member> ms{Member{&h, static_cast<const uint8_t *>(src), src_bytes,
+                                static_cast<uint8_t *>(dst), dst_bytes, report, 0, &dp, true, 0,
+                                false, dp.wire_bytes}};
+  uint8_t *tables = ctx.scratch + kScratchWireBytes;
+  const StaticScratch sc{ctx.scratch, kScratchWireBytes, reinterpret_cast<float *>(tables),
+                         reinterpret_cast<int32_t *>(tables + kParamStageHalf), &dp.pf, &dp.pi};
+  execute(ctx, ms, opt, nullptr, nullptr, &sc);
+}
+
 void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
-             relx_report *total, Completion *comp) {
+             relx_report *total, Completion *comp, const StaticScratch *sc) {
   size_t wire_total = 0;
   for (const Member &m : ms)
     wire_total = std::max(wire_total, m.wire_off + static_cast<size_t>(m.arena_bytes));
-  ensure_wire(ctx, wire_total);
+  if (!sc)
+    ensure_wire(ctx, wire_total);
+  else if (wire_total > sc->wire_cap)
+    throw Error("insufficient_capacity", "the wire needs " + std::to_string(wire_total) +
+                                             " bytes; the static scratch holds " +
+                                             std::to_string(sc->wire_cap));
 
   // Chunk plan per member: units of the chunk axis per chunk (a table upload:
   // byte ranges of the table, multiples of 256 bytes).
@@ -451,10 +521,12 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
     total_chunks += (p.units + p.per_chunk - 1) / p.per_chunk;
   const bool two_streams = total_chunks > 1; // else one copy stream does everything
   const int nslots = opt.n_buffers > 0 ? opt.n_buffers : 3;
+  if (max_slot && sc)
+    throw Error("invalid_options", "an allocation-free call has no staging ring");
   if (max_slot)
     ensure_ring(ctx, nslots, max_slot);
   const unsigned threads = opt.gather_threads > 0 ? static_cast<unsigned>(opt.gather_threads) : 8u;
-  if (!ctx.workers || ctx.worker_threads != threads) {
+  if (!sc && (!ctx.workers || ctx.worker_threads != threads)) {
     ctx.workers = std::make_unique<Workers>(threads);
     ctx.worker_threads = threads;
   }
@@ -480,21 +552,35 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
   int32_t *status = ctx.status + (ctx.status_next++ % kStatusSlots);
   if (any_generic)
     clear_status(status);
+  if (sc) {
+    // The parameter tables go to the scratch through the context's pinned
+    // staging (a DMA, no runtime staging), ahead of every chunk's kernel.
+    const size_t fb = sc->host_pf->size() * sizeof(float), ib = sc->host_pi->size() * sizeof(int32_t);
+    std::memcpy(ctx.param_stage, sc->host_pf->data(), fb);
+    std::memcpy(ctx.param_stage + kParamStageHalf, sc->host_pi->data(), ib);
+    HIPCHECK(hipMemcpyAsync(sc->pf, ctx.param_stage, fb, hipMemcpyHostToDevice, ctx.copies[0]));
+    HIPCHECK(hipMemcpyAsync(sc->pi, ctx.param_stage + kParamStageHalf, ib, hipMemcpyHostToDevice,
+                            ctx.copies[0]));
+    HIPCHECK(hipEventRecord(ctx.join_ev[0], ctx.copies[0]));
+    for (int i = 1; i < kCopyStreams; ++i)
+      HIPCHECK(hipStreamWaitEvent(ctx.copies[i], ctx.join_ev[0], 0));
+  }
 
   int slot = 0;
   int64_t nchunk = 0; // chunks of every member so far: picks the copy stream
   relx_report sum{};
   // Kernel timing covers blocking calls, whose events are read at the end.
-  const bool timing = ctx.time_kernels && !comp && !opt.no_wait;
+  const bool timing = ctx.time_kernels && !comp && !opt.no_wait && !sc;
   size_t tpairs = 0;
   for (size_t mi = 0; mi < ms.size(); ++mi) {
     Member &m = ms[mi];
     const DeviceProgram &dp = *m.dp;
     const ChunkPlan &p = plans[mi];
-    const BoundHandle::DevParams par = m.h->device_params(ctx.device, m.k);
+    const BoundHandle::DevParams par =
+        sc ? BoundHandle::DevParams{sc->pf, sc->pi} : m.h->device_params(ctx.device, m.k);
     const uint32_t sw = m.h->bound->typed ? m.h->bound->source_type.width()
                                           : m.h->bound->layout.element_size;
-    uint8_t *wire = ctx.wire + m.wire_off;
+    uint8_t *wire = (sc ? sc->wire : ctx.wire) + m.wire_off;
     int64_t chunks = 0, launches = 0;
     if (m.table) {
       // The table crosses as it is (byte chunks); the gather reads rows from
@@ -874,6 +960,11 @@ std::unique_ptr<Context> make_context(int device, int64_t max_retained) {
   std::memset(ctx->status, 0, flags);
   for (uint32_t i = 0; i < kDeviceChecks; ++i)
     HIPCHECK(hipEventCreateWithFlags(&ctx->check_ev[i], hipEventDisableTiming));
+  // set-up of the allocation-free upload: this device's scratch address and
+  // the pinned staging of its parameter tables
+  ctx->scratch = scratch_address(device);
+  HIPCHECK(hipHostMalloc(reinterpret_cast<void **>(&ctx->param_stage), kScratchParamBytes,
+                         hipHostMallocDefault));
   return ctx;
 }
 
@@ -927,6 +1018,9 @@ void destroy_context(Context &ctx) {
   for (hipEvent_t e : ctx.time_ev)
     (void)hipEventDestroy(e);
   ctx.time_ev.clear();
+  if (ctx.param_stage)
+    (void)hipHostFree(ctx.param_stage);
+  ctx.param_stage = nullptr;
   if (ctx.wire)
     (void)hipFree(ctx.wire);
   ctx.wire = nullptr;

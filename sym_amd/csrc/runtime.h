@@ -287,6 +287,11 @@ struct Context {
   bool time_kernels = false;
   KernelTimes kt;
   std::vector<hipEvent_t> time_ev; // timing event pairs, reused call to call
+  // The allocation-free upload: this device's copy of the static scratch
+  // (its address from hipGetSymbolAddress) and pinned staging for the
+  // parameter tables it uploads (kScratchParamBytes, allocated here).
+  uint8_t *scratch = nullptr;
+  uint8_t *param_stage = nullptr;
   std::unique_ptr<Workers> workers;
   unsigned worker_threads = 0;
   int64_t max_retained = 0;
@@ -300,6 +305,19 @@ struct Context {
   bool closed = false;
   ~Context(); // frees the status flags (the rest goes in destroy_context)
 };
+
+// The allocation-free upload's device scratch (noalloc.hip): one file-scope
+// array of kScratchBytes on each GPU the library runs on, held until the
+// process ends. The wire is staged in its first kScratchWireBytes; the
+// parameter tables (floats, then ints) take the two halves of the last
+// kScratchParamBytes.
+constexpr size_t kScratchBytes = size_t{64} << 20;
+constexpr size_t kScratchParamBytes = size_t{1} << 20;
+constexpr size_t kScratchWireBytes = kScratchBytes - kScratchParamBytes;
+constexpr size_t kParamStageHalf = kScratchParamBytes / 2;
+// The device address of `device`'s copy of the scratch, found once per
+// device with hipGetSymbolAddress; call with `device` current.
+uint8_t *scratch_address(int device);
 
 constexpr uint32_t kStatusSlots = 1024;
 constexpr uint32_t kDeviceChecks = 64; // size of Context::check_ev

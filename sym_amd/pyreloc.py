@@ -409,6 +409,18 @@ class Context:
             _raise(err)
         return rep.as_dict()
 
+    def execute_h2d_static(self, bound, src_ptr, src_nbytes, dst_ptr, dst_nbytes, **options):
+        """The allocation-free upload (relx_execute_h2d_static): a page-locked
+        source, the wire staged in the library's static device scratch."""
+        rep = N.relx_report()
+        err = N.relx_err()
+        opt = _options(**options)
+        if N.lib().relx_execute_h2d_static(self._h, bound._h, src_ptr, src_nbytes, dst_ptr,
+                                           dst_nbytes, ctypes.byref(opt), ctypes.byref(rep),
+                                           ctypes.byref(err)):
+            _raise(err)
+        return rep.as_dict()
+
     def execute_group_h2d(self, bounds, srcs, dsts, **options):
         """srcs/dsts: lists of (pointer, nbytes). Returns (reports, total)."""
         n = len(bounds)
