@@ -253,6 +253,76 @@ int relx_execute_h2d_static(relx_ctx *ctx, const relx_bound *bound, const void *
                             size_t src_bytes, void *dst, size_t dst_bytes, const relx_options *opt,
                             relx_report *report, relx_err *err);
 
+/* ------------------------------------------------- layout transfers */
+
+/* A framework buffer as the caller declares it (reference BufferView,
+ * libreloc/include/reloc/Transfer.h:47-56): the allocation (base, capacity
+ * in bytes from base), the byte offset of logical element 0, extents,
+ * element strides, element size, memory kind and device ordinal (-1 for
+ * host memory). */
+#define RELX_MAX_VIEW_RANK 16
+#define RELX_KIND_HOST 0
+#define RELX_KIND_DEVICE 1
+#define RELX_H2D 0
+#define RELX_D2H 1
+typedef struct relx_view {
+  uint64_t base;
+  uint64_t capacity_bytes;
+  uint64_t offset_bytes;
+  int rank;
+  int64_t extents[RELX_MAX_VIEW_RANK];
+  int64_t strides[RELX_MAX_VIEW_RANK];
+  uint32_t element_size;
+  int kind;
+  int device;
+} relx_view;
+
+/* Bytes from element 0 the view can address, after rejecting empty,
+ * negative-stride, broadcast and overlapping views, every step
+ * overflow-checked; `role` names the view in messages. Replaces
+ * reloc::viewSpanBytes (libreloc/src/Transfer.cpp:65-113) and
+ * pyreloc.BufferView.span_bytes (libreloc/python/PyTransfer.cpp:327-330).
+ * Errors: "invalid_view", "unsupported_layout", "integer_overflow",
+ * "insufficient_capacity". */
+int relx_view_span_bytes(const relx_view *view, const char *role, uint64_t *span, relx_err *err);
+
+/* Preflight: the layout plan's source reads fit `source` and the view is
+ * admissible for `direction` (RELX_H2D / RELX_D2H); `*span` receives the
+ * source span. Allocates and launches nothing. Replaces
+ * reloc::validateTransferSource (libreloc/src/Transfer.cpp:233-244) and
+ * pyreloc.validate_transfer_source (libreloc/python/PyTransfer.cpp:91-99).
+ * Errors: the view's, "direction_mismatch", "typed_unsupported",
+ * "plan_mismatch", "integer_overflow". */
+int relx_validate_transfer_source(const relx_bound *bound, const relx_view *source,
+                                  int direction, uint64_t *span, relx_err *err);
+
+/* Full validation with the destination: dense, exactly the plan's
+ * footprint, every padded write inside. Replaces reloc::validateTransfer
+ * (libreloc/src/Transfer.cpp:246-268) and pyreloc.make_transfer
+ * (libreloc/python/PyTransfer.cpp:109-118). */
+int relx_validate_transfer(const relx_bound *bound, const relx_view *source,
+                           const relx_view *destination, int direction, uint64_t *source_span,
+                           uint64_t *destination_bytes, relx_err *err);
+
+/* Validate, then run the layout plan's forward transfer on the context's
+ * device: host -> device through the upload pipeline (the source view's
+ * span is uploaded from its element 0), device -> host through the download
+ * pipeline. Blocks like relx_execute_h2d / relx_execute_d2h. Replaces
+ * reloc::executeTransfer (libreloc/src/Transfer.cpp:493-544) and
+ * pyreloc.execute_transfer (libreloc/python/PyTransfer.cpp:120-219).
+ * Errors: the validators', "device_mismatch" (the device view is not on the
+ * context's device), "backend_mismatch" (both views in host memory), and
+ * those of the pipelines. */
+int relx_execute_transfer(relx_ctx *ctx, const relx_bound *bound, const relx_view *source,
+                          const relx_view *destination, int direction, const relx_options *opt,
+                          relx_report *report, relx_err *err);
+
+/* The device ordinal owning a device pointer (hipPointerGetAttributes).
+ * Replaces reloc::cudaPointerDevice and pyreloc.cuda_pointer_device
+ * (libreloc/python/PyTransfer.cpp:291-306). Errors: "invalid_view" for
+ * host or unknown memory. */
+int relx_pointer_device(const void *pointer, int *device, relx_err *err);
+
 /* A group of bound plans as one schedule: all members' wire bytes through
  * one ring and one event barrier (reference group_detail::executeGroup,
  * libreloc/src/Dispatch.cpp:1833-1981; pyreloc.execute_dispatch_group).

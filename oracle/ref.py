@@ -222,3 +222,41 @@ class CpuH2dRef:
         if getattr(self, "h", None):
             hip_lib().ref_cpu_h2d_free(self.h)
             self.h = None
+
+
+def validate_transfer(blob, symbols, src, dst, direction, source_only=False):
+    """The reference's validateTransfer / validateTransferSource on a layout
+    plan. Views are (base, capacity, offset, extents, strides, element size,
+    kind 'host'|'cuda', device) tuples. Returns ('ok', source span),
+    ('error', '<code>: <message>') or ('plan', None) when the plan does not
+    decode or bind."""
+    L = lib()
+    if not hasattr(L, "_vt"):
+        f = L.ref_validate_transfer
+        i64p = ctypes.POINTER(ctypes.c_int64)
+        u64p = ctypes.POINTER(ctypes.c_uint64)
+        f.restype = ctypes.c_int
+        f.argtypes = ([ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_char_p), i64p,
+                       ctypes.c_int] +
+                      [u64p, ctypes.c_int, i64p, i64p, ctypes.c_uint32, ctypes.c_int, ctypes.c_int] * 2 +
+                      [ctypes.c_int, ctypes.c_int, u64p, ctypes.c_char_p, ctypes.c_size_t])
+        L._vt = f
+    sn, sv, ns = _syms(symbols)
+
+    def parts(v):
+        base, cap, off, ext, strides, es, kind, dev = v
+        words = (ctypes.c_uint64 * 3)(base, cap, off)
+        e = (ctypes.c_int64 * max(1, len(ext)))(*ext)
+        s = (ctypes.c_int64 * max(1, len(strides)))(*strides)
+        return [words, len(ext), e, s, es, 1 if kind == "cuda" else 0, dev]
+
+    span = ctypes.c_uint64(0)
+    err = ctypes.create_string_buffer(512)
+    d = dst if dst is not None else src
+    rc = L._vt(blob, len(blob), sn, sv, ns, *parts(src), *parts(d), 1 if direction == "d2h" else 0,
+               1 if source_only else 0, ctypes.byref(span), err, 512)
+    if rc == 0:
+        return "ok", span.value
+    if rc == 1:
+        return "error", err.value.decode()
+    return "plan", None

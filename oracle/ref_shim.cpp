@@ -17,6 +17,7 @@
 #include "reloc/Decode.h"
 #include "reloc/Execute.h"
 #include "reloc/GatherPool.h"
+#include "reloc/Transfer.h"
 #include "reloc/TypedExecute.h"
 
 #include <cstring>
@@ -192,6 +193,61 @@ void *ref_indexed_prepare(const uint8_t *blob, size_t n, const char **symNames,
   if (threads > 1)
     h->pool = std::make_unique<reloc::GatherPool>(threads);
   return h;
+}
+
+// validateTransferSource (sourceOnly) or validateTransfer on a decoded and
+// bound layout plan (libreloc/src/Transfer.cpp:233-268). A view is given as
+// (base, capacity, offset) words, rank, extents, strides, element size,
+// kind (0 host, 1 cuda) and device. Returns 0 with the source span, 1 with
+// "<code>: <message>", 2 when the plan does not decode or bind.
+int ref_validate_transfer(const uint8_t *blob, size_t n, const char **symNames,
+                          const int64_t *symVals, int nsym, const uint64_t *sw, int srank,
+                          const int64_t *sext, const int64_t *sstr, uint32_t ses, int skind,
+                          int sdev, const uint64_t *dw, int drank, const int64_t *dext,
+                          const int64_t *dstr, uint32_t des, int dkind, int ddev, int direction,
+                          int sourceOnly, uint64_t *span, char *err, size_t cap) {
+  auto decoded = reloc::decodePlan(blob, n);
+  if (std::holds_alternative<reloc::DecodeError>(decoded))
+    return 2;
+  reloc::SymbolMap symbols;
+  for (int i = 0; i < nsym; ++i)
+    symbols[symNames[i]] = symVals[i];
+  auto bound = reloc::bind(std::get<reloc::RelocationPlan>(decoded), symbols);
+  if (std::holds_alternative<reloc::BindError>(bound))
+    return 2;
+  auto view = [](const uint64_t *w, int rank, const int64_t *ext, const int64_t *str, uint32_t es,
+                 int kind, int dev) {
+    reloc::BufferView v;
+    v.base = static_cast<uintptr_t>(w[0]);
+    v.capacityBytes = static_cast<size_t>(w[1]);
+    v.offsetBytes = static_cast<size_t>(w[2]);
+    v.extents.assign(ext, ext + rank);
+    v.strides.assign(str, str + rank);
+    v.elementSize = es;
+    v.kind = kind ? reloc::MemoryKind::Cuda : reloc::MemoryKind::Host;
+    v.device = dev;
+    return v;
+  };
+  const auto dir = direction ? reloc::TransferDirection::DeviceToHost
+                             : reloc::TransferDirection::HostToDevice;
+  const reloc::BufferView src = view(sw, srank, sext, sstr, ses, skind, sdev);
+  const auto &b = std::get<reloc::BoundPlan>(bound);
+  if (sourceOnly) {
+    auto r = reloc::validateTransferSource(b, src, dir);
+    if (auto *e = std::get_if<reloc::TransferError>(&r)) {
+      setErr(err, cap, e->code + ": " + e->message);
+      return 1;
+    }
+    *span = std::get<size_t>(r);
+    return 0;
+  }
+  auto r = reloc::validateTransfer(b, src, view(dw, drank, dext, dstr, des, dkind, ddev), dir);
+  if (auto *e = std::get_if<reloc::TransferError>(&r)) {
+    setErr(err, cap, e->code + ": " + e->message);
+    return 1;
+  }
+  *span = std::get<reloc::TransferRequest>(r).sourceSpanBytes;
+  return 0;
 }
 
 } // extern "C"

@@ -75,6 +75,17 @@ class relx_report(ctypes.Structure):
                 for f, _ in self._fields_}
 
 
+RELX_MAX_VIEW_RANK = 16
+_I64V = ctypes.c_int64 * RELX_MAX_VIEW_RANK
+
+
+class relx_view(ctypes.Structure):
+    _fields_ = [("base", ctypes.c_uint64), ("capacity_bytes", ctypes.c_uint64),
+                ("offset_bytes", ctypes.c_uint64), ("rank", ctypes.c_int),
+                ("extents", _I64V), ("strides", _I64V), ("element_size", ctypes.c_uint32),
+                ("kind", ctypes.c_int), ("device", ctypes.c_int)]
+
+
 class relx_kernel_times(ctypes.Structure):
     _fields_ = [("calls", ctypes.c_int64), ("chunks", ctypes.c_int64),
                 ("launches", ctypes.c_int64), ("ms", ctypes.c_double)]
@@ -106,6 +117,16 @@ SIGNATURES = {
                               ctypes.POINTER(relx_report), _E]),
     "relx_execute_h2d_static": (_I, [_VP, _VP, _VP, _SZ, _VP, _SZ, ctypes.POINTER(relx_options),
                                      ctypes.POINTER(relx_report), _E]),
+    "relx_view_span_bytes": (_I, [ctypes.POINTER(relx_view), ctypes.c_char_p,
+                                  ctypes.POINTER(_U64), _E]),
+    "relx_validate_transfer_source": (_I, [_VP, ctypes.POINTER(relx_view), _I,
+                                           ctypes.POINTER(_U64), _E]),
+    "relx_validate_transfer": (_I, [_VP, ctypes.POINTER(relx_view), ctypes.POINTER(relx_view), _I,
+                                    ctypes.POINTER(_U64), ctypes.POINTER(_U64), _E]),
+    "relx_execute_transfer": (_I, [_VP, _VP, ctypes.POINTER(relx_view), ctypes.POINTER(relx_view),
+                                   _I, ctypes.POINTER(relx_options), ctypes.POINTER(relx_report),
+                                   _E]),
+    "relx_pointer_device": (_I, [_VP, ctypes.POINTER(_I), _E]),
     "relx_execute_group_h2d": (_I, [_VP, _I, ctypes.POINTER(_VP), ctypes.POINTER(_VP),
                                     ctypes.POINTER(_SZ), ctypes.POINTER(_VP), ctypes.POINTER(_SZ),
                                     ctypes.POINTER(relx_options), ctypes.POINTER(relx_report),

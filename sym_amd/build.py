@@ -23,7 +23,8 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "
           "-Wno-unused-command-line-argument"]
 DEVICE = ["--offload-arch=" + ARCH, "-mcode-object-version=5", "-fno-gpu-flush-denormals-to-zero",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
-SOURCES = ["plan.cpp", "program.cpp", "runtime.cpp", "workers.cpp", "indexed.cpp", "capi.cpp",
+SOURCES = ["plan.cpp", "program.cpp", "runtime.cpp", "workers.cpp", "indexed.cpp", "transfer.cpp",
+           "capi.cpp",
            "kernels.hip",
            "k_stream_fast.hip", "k_stream_generic.hip", "k_transpose.hip", "k_interleave.hip",
            "k_interleave_generic.hip", "k_permute.hip", "k_gather.hip", "k_copy.hip", "noalloc.hip"]

@@ -22,6 +22,13 @@ void relayout_device(Context &ctx, BoundHandle &h, uint32_t k, const void *wire,
 void resolve_checks(Context &ctx);
 void execute_static(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes, void *dst,
                     size_t dst_bytes, const relx_options &opt, relx_report *report);
+uint64_t view_span_bytes(const relx_view &v, const std::string &role);
+uint64_t validate_transfer_source(const BoundHandle &h, const relx_view &src, int direction);
+void validate_transfer(const BoundHandle &h, const relx_view &src, const relx_view &dst,
+                       int direction, uint64_t &src_span, uint64_t &dst_bytes);
+void execute_transfer(Context &ctx, BoundHandle &h, const relx_view &src, const relx_view &dst,
+                      int direction, const relx_options &opt, relx_report *report);
+int pointer_device(const void *p);
 double measure_h2d(int device, size_t bytes, int iters, int rounds);
 double measure_copy(int device, size_t bytes, int iters, int rounds, bool d2h);
 } // namespace relx
@@ -498,6 +505,88 @@ int relx_execute_h2d_static(relx_ctx *ctx, const relx_bound *bound, const void *
       c.quarantined = true;
   }
   return rc;
+}
+
+int relx_view_span_bytes(const relx_view *view, const char *role, uint64_t *span, relx_err *err) {
+  return guarded(err, [&] {
+    if (!view || !span)
+      throw relx::Error("invalid_argument", "null view or output");
+    *span = relx::view_span_bytes(*view, role ? role : "view");
+  });
+}
+
+int relx_validate_transfer_source(const relx_bound *bound, const relx_view *source,
+                                  int direction, uint64_t *span, relx_err *err) {
+  return guarded(err, [&] {
+    if (!bound || !source)
+      throw relx::Error("invalid_argument", "null bound plan or view");
+    if (direction != RELX_H2D && direction != RELX_D2H)
+      throw relx::Error("invalid_options", "direction must be host-to-device or device-to-host");
+    const uint64_t s = relx::validate_transfer_source(bound->h, *source, direction);
+    if (span)
+      *span = s;
+  });
+}
+
+int relx_validate_transfer(const relx_bound *bound, const relx_view *source,
+                           const relx_view *destination, int direction, uint64_t *source_span,
+                           uint64_t *destination_bytes, relx_err *err) {
+  return guarded(err, [&] {
+    if (!bound || !source || !destination)
+      throw relx::Error("invalid_argument", "null bound plan or view");
+    uint64_t s = 0, d = 0;
+    relx::validate_transfer(bound->h, *source, *destination, direction, s, d);
+    if (source_span)
+      *source_span = s;
+    if (destination_bytes)
+      *destination_bytes = d;
+  });
+}
+
+int relx_execute_transfer(relx_ctx *ctx, const relx_bound *bound, const relx_view *source,
+                          const relx_view *destination, int direction, const relx_options *opt,
+                          relx_report *report, relx_err *err) {
+  if (!ctx) {
+    set_err(err, "invalid_argument", "null context");
+    return RELX_ERROR;
+  }
+  relx::Context &c = *ctx->ctx;
+  std::lock_guard<std::mutex> g(c.mu);
+  if (c.closed || c.quarantined) {
+    set_err(err, "resources_closed", "context is closed or quarantined");
+    return RELX_ERROR;
+  }
+  relx_options o{};
+  o.host_stages = -1;
+  o.source_pinned = -1;
+  if (opt)
+    o = *opt;
+  ++c.calls;
+  const int rc = guarded(err, [&] {
+    if (!bound || !source || !destination)
+      throw relx::Error("invalid_argument", "null bound plan or view");
+    relx::execute_transfer(c, const_cast<relx::BoundHandle &>(bound->h), *source, *destination,
+                           direction, o, report);
+  });
+  if (rc != RELX_OK) {
+    ++c.failures;
+    const bool complete = relx::drain(c);
+    if (err)
+      err->completion = complete ? RELX_COMPLETE : RELX_UNKNOWN;
+    if (!complete)
+      c.quarantined = true;
+  }
+  return rc;
+}
+
+int relx_pointer_device(const void *pointer, int *device, relx_err *err) {
+  return guarded(err, [&] {
+    if (!device)
+      throw relx::Error("invalid_argument", "null output");
+    if (!pointer)
+      throw relx::Error("invalid_view", "pointer is null");
+    *device = relx::pointer_device(pointer);
+  });
 }
 
 int relx_relayout_device(relx_ctx *ctx, const relx_bound *bound, int wire_boundary,

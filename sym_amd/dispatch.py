@@ -32,56 +32,9 @@ import threading
 
 from . import pyreloc as P
 from .pyreloc import TransferError
+from .transfer import BufferView, DispatchResources, context_for  # noqa: F401
 
 POLICIES = ("auto", "original_cpu")
-_KINDS = {"host": "host", "cuda": "cuda", "device": "cuda"}
-
-
-class BufferView:
-    """Memory seen as a strided tensor (reference pyreloc.BufferView,
-    libreloc/python/PyTransfer.cpp:62-76,312-330): base address, capacity
-    in bytes from the base, byte offset of element 0, extents, strides in
-    elements, element size in bytes, kind "host" or "cuda", device ordinal."""
-
-    def __init__(self, base, capacity_bytes, offset_bytes, extents, strides, element_size,
-                 kind, device=-1):
-        if kind not in _KINDS:
-            raise ValueError("kind must be 'host' or 'cuda', got %r" % (kind,))
-        extents, strides = [int(e) for e in extents], [int(s) for s in strides]
-        if len(extents) != len(strides):
-            raise ValueError("extents and strides differ in rank")
-        self.base = int(base)
-        self.capacity_bytes = int(capacity_bytes)
-        self.offset_bytes = int(offset_bytes)
-        self.extents = extents
-        self.strides = strides
-        self.element_size = int(element_size)
-        self.kind = _KINDS[kind]
-        self.device = int(device)
-
-    @property
-    def address(self):
-        return self.base + self.offset_bytes
-
-    def is_dense(self):
-        """Row-major dense (the only layout typed dispatch accepts)."""
-        running = 1
-        for e, s in zip(reversed(self.extents), reversed(self.strides)):
-            if e != 1 and s != running:
-                return False
-            running *= e
-        return True
-
-    def span_bytes(self):
-        """Bytes from the base the view can reach (offset included)."""
-        if any(e == 0 for e in self.extents):
-            return self.offset_bytes
-        last = sum((e - 1) * s for e, s in zip(self.extents, self.strides))
-        return self.offset_bytes + (last + 1) * self.element_size
-
-    def __repr__(self):
-        return "BufferView(%s, extents=%s, strides=%s, element_size=%d)" % (
-            self.kind, self.extents, self.strides, self.element_size)
 
 
 def _label(k):
@@ -108,9 +61,7 @@ def _check_table_view(bound, view):
     (libreloc/src/Dispatch.cpp:161-201)."""
     if view.kind == "cuda":
         raise TransferError("direction_mismatch", "host-to-device source must be host memory")
-    if view.span_bytes() > view.capacity_bytes:
-        raise TransferError("insufficient_capacity", "source view reaches %d bytes of %d"
-                            % (view.span_bytes(), view.capacity_bytes))
+    view.span_bytes  # noqa: B018 - the checked span raises for a bad view
     if view.element_size != bound.info.source_width:
         raise TransferError("plan_mismatch", "source element size differs from the typed "
                             "program's source type")
@@ -227,27 +178,52 @@ def prepare_dispatch_template(bound, direction, device="cuda", *, policy="auto",
     return DispatchTemplate(bound, direction, capability, selection, int(threads))
 
 
-def _check_views(bound, source, destination, direction):
+def _check_view(bound, view, is_source, direction):
+    """checkView (libreloc/src/Dispatch.cpp:162-219): a CUDA view on the
+    device end of its direction, the checked span, the program's element
+    size, dense row-major, and exactly the program's bytes (an indexed
+    source: the prepared host row shape)."""
     info = bound.info
-    want = ("host", "cuda") if direction == "h2d" else ("cuda", "host")
-    if (source.kind, destination.kind) != want:
-        raise TransferError("direction_mismatch", "%s moves %s -> %s, got %s -> %s"
-                            % (direction, want[0], want[1], source.kind, destination.kind))
-    if bound.indexed:
-        _check_table_view(bound, source)
-    for name, view, extents, width in (
-            ("source", source, bound.source_extents if bound.indexed else
-             list(info.source_extents[:info.source_rank]), info.source_width),
-            ("destination", destination, list(info.result_extents[:info.result_rank]),
-             info.result_width)):
-        if view.extents != extents or view.element_size != width:
-            raise TransferError("plan_mismatch", "%s view is %s x %d B, the plan needs %s x %d B"
-                                % (name, view.extents, view.element_size, extents, width))
-        if not view.is_dense():
-            raise TransferError("invalid_view", "%s view is not dense row-major" % name)
-        if view.span_bytes() > view.capacity_bytes:
-            raise TransferError("insufficient_capacity", "%s view reaches %d bytes of %d"
-                                % (name, view.span_bytes(), view.capacity_bytes))
+    what = "source" if is_source else "destination"
+    if direction == "h2d" and is_source and view.kind == "cuda":
+        raise TransferError("direction_mismatch", "host-to-device source must be host memory")
+    if direction == "d2h" and not is_source and view.kind == "cuda":
+        raise TransferError("direction_mismatch", "device-to-host destination must be host memory")
+    span = view.span_bytes
+    if view.element_size != (info.source_width if is_source else info.result_width):
+        raise TransferError("plan_mismatch", "%s element size differs from the typed program's "
+                            "%s type" % (what, "source" if is_source else "result"))
+    if not view.is_dense():
+        raise TransferError("unsupported_layout", "%s view must be dense row-major" % what)
+    if is_source and bound.indexed:
+        if direction != "h2d" or view.extents != bound.source_extents:
+            raise TransferError("plan_mismatch", "indexed source requires the prepared host row shape")
+        return
+    # the source layout's bytes at boundary 0 (pads enter later), the result's
+    expected = info.wire_bytes_at[0] if is_source else bound.destination_bytes
+    if span != expected:
+        raise TransferError("plan_mismatch", "%s view spans %d bytes but the typed program needs %d"
+                            % (what, span, expected))
+    if is_source:
+        elements = 1
+        for e in view.extents:
+            elements *= e
+        want = 1
+        for e in info.source_extents[:info.source_rank]:
+            want *= e
+        if elements != want:
+            raise TransferError("plan_mismatch", "source view element count differs from the "
+                                "program's source descriptor")
+
+
+def _check_views(bound, source, destination, direction):
+    _check_view(bound, source, True, direction)
+    _check_view(bound, destination, False, direction)
+    # this library's rows move data between host and device memory only
+    device_end = destination if direction == "h2d" else source
+    if device_end.kind != "cuda":
+        raise TransferError("backend_mismatch", "%s rows need the %s in device memory"
+                            % (direction, "destination" if direction == "h2d" else "source"))
 
 
 def prepare_dispatch_from_template(template, source, destination):
@@ -265,21 +241,14 @@ def prepare_dispatch(bound, source, destination, direction, *, policy="auto", ca
 
 
 class Resources(P.Context):
-    """Retained streams, pinned ring and device wire scratch reused across
-    requests (reference dispatch::Resources,
-    libreloc/src/DispatchResources.cpp:44,552-686)."""
+    """Retained streams, pinned ring and device wire scratch of one device,
+    reused across requests (reference dispatch::Resources,
+    libreloc/src/DispatchResources.cpp:44,552-686). `DispatchResources` is
+    the per-device cache of them that the reference's constructor builds."""
 
 
-_default = {}
-_default_lock = threading.Lock()
-
-
-def _resources_for(device):
-    with _default_lock:
-        ctx = _default.get(device)
-        if ctx is None:
-            ctx = _default[device] = Resources(device)
-        return ctx
+def _resources_for(resources, device):
+    return context_for(resources, max(0, device))
 
 
 def _pinning(pinning):
@@ -329,7 +298,7 @@ def execute_dispatch(request, *, caller_stream=None, n_buffers=2, n_streams=2, g
         src, dst = request.source, request.destination
         d2h = request.template.direction == "d2h"
         device = src.device if d2h else dst.device
-        ctx = resources if resources is not None else _resources_for(max(0, device))
+        ctx = _resources_for(resources, device)
         run = ctx.execute_d2h if d2h else ctx.execute_h2d
         rep = run(request.template.bound, src.address, src.capacity_bytes - src.offset_bytes,
                   dst.address, dst.capacity_bytes - dst.offset_bytes,
@@ -387,7 +356,7 @@ def execute_dispatch_group(group, *, caller_stream=None, gather_threads=1, gathe
     group.executing = True
     try:
         dev = max(0, group.items[0].destination.device)
-        ctx = resources if resources is not None else _resources_for(dev)
+        ctx = _resources_for(resources, dev)
         bounds = [r.template.bound for r in group.items]
         srcs = [(r.source.address, r.source.capacity_bytes - r.source.offset_bytes) for r in group.items]
         dsts = [(r.destination.address, r.destination.capacity_bytes - r.destination.offset_bytes)
@@ -477,7 +446,7 @@ def submit_dispatch_group(group, *, caller_stream=None, gather_threads=8, gather
         raise ValueError("gather_threads and max_scratch_bytes must be positive")
     _pinning(pinning)
     dev = max(0, group.items[0].destination.device)
-    ctx = resources if resources is not None else _resources_for(dev)
+    ctx = _resources_for(resources, dev)
     bounds = [r.template.bound for r in group.items]
     srcs = [(r.source.address, r.source.capacity_bytes - r.source.offset_bytes) for r in group.items]
     dsts = [(r.destination.address, r.destination.capacity_bytes - r.destination.offset_bytes)

@@ -611,9 +611,13 @@ def measure_d2h(device=0, nbytes=256 << 20, iters=20, rounds=3):
     return N.lib().relx_measure_d2h(int(device), int(nbytes), int(iters), int(rounds))
 
 
-# The typed dispatch API (prepare_dispatch / execute_dispatch / groups) lives
-# in sym_amd.dispatch and is re-exported here under pyreloc's names.
-from .dispatch import (BufferView, DispatchCompletion, DispatchRequest,  # noqa: E402,F401
+# The layout transfer API (sym_amd.transfer) and the typed dispatch API
+# (prepare_dispatch / execute_dispatch / groups, sym_amd.dispatch) are
+# re-exported here under pyreloc's names.
+from .transfer import (BufferView, DispatchResources, TransferRequest,  # noqa: E402,F401
+                       TransferResourceCache, cuda_enabled, cuda_pointer_device, execute_transfer,
+                       make_transfer, validate_transfer_source)
+from .dispatch import (DispatchCompletion, DispatchRequest,  # noqa: E402,F401
                        DispatchTemplate, GroupRequest, IndexSelectProgram, Resources,
                        execute_dispatch, execute_dispatch_group, prepare_dispatch,
                        prepare_dispatch_from_template, prepare_dispatch_group,

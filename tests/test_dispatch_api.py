@@ -32,9 +32,9 @@ def c2_bound():
 def test_buffer_view_geometry():
     a = np.zeros((3, 4), np.float32)
     v = host_view(a)
-    assert v.is_dense() and v.span_bytes() == 48 and v.address == a.ctypes.data
+    assert v.is_dense() and v.span_bytes == 48 and v.address == a.ctypes.data
     t = host_view(a.T)
-    assert not t.is_dense() and t.span_bytes() == 48
+    assert not t.is_dense() and t.span_bytes == 48
     with pytest.raises(ValueError):
         P.BufferView(0, 0, 0, [1], [1], 1, "disk")
 
@@ -105,17 +105,22 @@ def test_view_validation_codes():
     assert code(host_view(src), fake_device_view([2, 224, 224, 4], 4)) == "plan_mismatch"
     assert code(host_view(src[:1]), good) == "plan_mismatch"
     assert code(host_view(np.zeros((2, 3, 224, 224), np.float16)), good) == "plan_mismatch"
-    assert code(host_view(np.asfortranarray(src)), good) == "invalid_view"
+    assert code(host_view(np.asfortranarray(src)), good) == "unsupported_layout"
     assert code(host_view(src), fake_device_view([2, 224, 224, 4], 2, capacity=100)) == \
         "insufficient_capacity"
     host_dst = host_view(np.zeros((2, 224, 224, 4), np.float16))
-    assert code(host_view(src), host_dst) == "direction_mismatch"
+    # host views are admitted on either end (reference checkView); this
+    # library's rows need the device end in device memory
+    assert code(host_view(src), host_dst) == "backend_mismatch"
     # device-to-host: a cuda source into a host destination
     dev_src = fake_device_view([2, 3, 224, 224], 4)
     req = P.prepare_dispatch(b, dev_src, host_dst, "d2h")
     assert req.template.direction == "d2h"
     with pytest.raises(P.TransferError) as e:
         P.prepare_dispatch(b, host_view(src), host_dst, "d2h")
+    assert e.value.code == "backend_mismatch"
+    with pytest.raises(P.TransferError) as e:
+        P.prepare_dispatch(b, host_view(src), fake_device_view([2, 224, 224, 4], 2), "d2h")
     assert e.value.code == "direction_mismatch"
 
 
