@@ -69,6 +69,30 @@ const char *relx_plan_symbol(const relx_plan *plan, int i);
 
 void relx_plan_free(relx_plan *plan);
 
+/* Decoded value stages of a typed (v1) plan (reference TypedPlanHandle
+ * .stages / .fills / .parameters, libreloc/python/PyReloc.cpp:241-288,
+ * 803-840). Types are (kind 0 float, 1 bfloat, 2 integer; bits);
+ * signedness 0 signless, 1 signed, 2 unsigned; parameter kinds 0 none,
+ * 1 inline, 2 binding. */
+typedef struct relx_plan_stage_info {
+  int transform; /* 0 cast, 1 quantize, 2 dequantize */
+  int policy;    /* 0 ieee_rne, 1 exact, 2 symmetric_rne, 3 affine */
+  int in_kind, in_bits, in_signedness;
+  int out_kind, out_bits, out_signedness;
+  int rank;
+  int64_t axis; /* -1 for a per-tensor stage */
+  int has_channel;
+  int scale_kind, zero_point_kind;
+} relx_plan_stage_info;
+int relx_plan_stage_count(const relx_plan *plan);
+int relx_plan_stage(const relx_plan *plan, int i, relx_plan_stage_info *out);
+int relx_plan_fill_count(const relx_plan *plan);
+/* Runtime parameter declarations in first-declaration order, one per name:
+ * name (owned by the plan), type, rank, first stage and role (0 scale,
+ * 1 zero point). Returns the count, or fills entry i when 0 <= i < count. */
+int relx_plan_parameter(const relx_plan *plan, int i, const char **name, int *kind, int *bits,
+                        int *rank, int *stage, int *role);
+
 /* A runtime parameter value by declared name (reference ParameterValue,
  * libreloc/include/reloc/Bind.h:125-133): element type (kind 0 float,
  * 1 bfloat, 2 integer; bitwidth), rank 0 or 1 with its length, and the

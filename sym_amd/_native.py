@@ -31,6 +31,15 @@ class relx_param(ctypes.Structure):
 _I64R = ctypes.c_int64 * RELX_MAX_RANK
 
 
+class relx_plan_stage_info(ctypes.Structure):
+    _fields_ = [("transform", ctypes.c_int), ("policy", ctypes.c_int), ("in_kind", ctypes.c_int),
+                ("in_bits", ctypes.c_int), ("in_signedness", ctypes.c_int),
+                ("out_kind", ctypes.c_int), ("out_bits", ctypes.c_int),
+                ("out_signedness", ctypes.c_int), ("rank", ctypes.c_int),
+                ("axis", ctypes.c_int64), ("has_channel", ctypes.c_int),
+                ("scale_kind", ctypes.c_int), ("zero_point_kind", ctypes.c_int)]
+
+
 class relx_bound_info(ctypes.Structure):
     _fields_ = [("typed", ctypes.c_int), ("rank", ctypes.c_int), ("extents", _I64R),
                 ("src_strides", _I64R), ("dst_strides", _I64R), ("pad_lo", _I64R),
@@ -103,6 +112,12 @@ SIGNATURES = {
     "relx_plan_symbol_count": (_I, [_VP]),
     "relx_plan_symbol": (ctypes.c_char_p, [_VP, _I]),
     "relx_plan_free": (None, [_VP]),
+    "relx_plan_stage_count": (_I, [_VP]),
+    "relx_plan_stage": (_I, [_VP, _I, ctypes.POINTER(relx_plan_stage_info)]),
+    "relx_plan_fill_count": (_I, [_VP]),
+    "relx_plan_parameter": (_I, [_VP, _I, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_I),
+                                 ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I),
+                                 ctypes.POINTER(_I)]),
     "relx_bind": (_I, [_VP, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_I64), _I,
                        ctypes.POINTER(relx_param), _I, ctypes.POINTER(_VP), _E]),
     "relx_bind_indexed": (_I, [_VP, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_I64), _I,

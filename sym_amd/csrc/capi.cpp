@@ -121,6 +121,73 @@ const char *relx_plan_symbol(const relx_plan *plan, int i) {
 
 void relx_plan_free(relx_plan *plan) { delete plan; }
 
+int relx_plan_stage_count(const relx_plan *plan) {
+  return plan ? static_cast<int>(plan->plan->stages.size()) : 0;
+}
+
+int relx_plan_stage(const relx_plan *plan, int i, relx_plan_stage_info *out) {
+  if (!plan || !out || i < 0 || i >= static_cast<int>(plan->plan->stages.size()))
+    return RELX_ERROR;
+  const relx::PlanStage &s = plan->plan->stages[static_cast<size_t>(i)];
+  out->transform = s.transform;
+  out->policy = s.policy;
+  out->in_kind = s.in.kind;
+  out->in_bits = static_cast<int>(s.in.bits);
+  out->in_signedness = s.in_sign;
+  out->out_kind = s.out.kind;
+  out->out_bits = static_cast<int>(s.out.bits);
+  out->out_signedness = s.out_sign;
+  out->rank = static_cast<int>(s.shape.size());
+  out->axis = s.axis;
+  out->has_channel = s.has_channel ? 1 : 0;
+  out->scale_kind = s.scale.kind;
+  out->zero_point_kind = s.zero_point.kind;
+  return RELX_OK;
+}
+
+int relx_plan_fill_count(const relx_plan *plan) {
+  return plan ? static_cast<int>(plan->plan->fills.size()) : 0;
+}
+
+int relx_plan_parameter(const relx_plan *plan, int i, const char **name, int *kind, int *bits,
+                        int *rank, int *stage, int *role) {
+  if (!plan)
+    return 0;
+  int n = 0;
+  std::vector<const std::string *> seen;
+  const auto &stages = plan->plan->stages;
+  for (size_t k = 0; k < stages.size(); ++k) {
+    const relx::StageParam *params[2] = {&stages[k].scale, &stages[k].zero_point};
+    for (int r = 0; r < 2; ++r) {
+      const relx::StageParam &p = *params[r];
+      if (p.kind != relx::kParamBinding)
+        continue;
+      bool dup = false;
+      for (const std::string *s : seen)
+        dup = dup || *s == p.name;
+      if (dup)
+        continue;
+      seen.push_back(&p.name);
+      if (n == i) {
+        if (name)
+          *name = p.name.c_str();
+        if (kind)
+          *kind = p.type.kind;
+        if (bits)
+          *bits = static_cast<int>(p.type.bits);
+        if (rank)
+          *rank = p.rank;
+        if (stage)
+          *stage = static_cast<int>(k);
+        if (role)
+          *role = r;
+      }
+      ++n;
+    }
+  }
+  return n;
+}
+
 int relx_bind(const relx_plan *plan, const char *const *sym_names, const int64_t *sym_values,
               int nsym, const relx_param *params, int nparam, relx_bound **out,
               relx_err *err) {

@@ -309,6 +309,11 @@ class Plan:
     result_dtype: str
     divisibility: List[Tuple[E, int]] = field(default_factory=list)
     parameters: List[Tuple[str, str, List[E]]] = field(default_factory=list)
+    # typed plans: the value stages as written (shape, parameters, channel map
+    # over result coordinates) and the pad fills (destination axis of the
+    # plan, entry stage, dtype, bits), for an artifact's manifest
+    stages: List["_Stage"] = field(default_factory=list)
+    fills: List[Tuple[int, int, str, int]] = field(default_factory=list)
 
 
 def encode(source_shape: Sequence, source_dtype: str, ops: Sequence, *, force_typed=False) -> Plan:
@@ -799,8 +804,10 @@ def _finalize(source_shape, source_dtype, axes, pads, stages, divisibility, dtyp
             w.u64(p.original_bits)
     elif pads and len({p.bits for p in pads}) > 1:
         raise EncodeError("layout plans carry a single fill value")
+    fills = [(k, new_pads[k].stage, new_pads[k].original_dtype, new_pads[k].original_bits)
+             for k in sorted(new_pads)] if typed else []
     return Plan(bytes(w.out), symbols, typed, list(source_shape), list(result_shape), source_dtype,
-                dtype, list(divisibility), params)
+                dtype, list(divisibility), params, list(stages) if typed else [], fills)
 
 
 # ------------------------------------------------------------ indexed (v2)

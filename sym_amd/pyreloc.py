@@ -85,6 +85,52 @@ class Plan:
         L = N.lib()
         return [L.relx_plan_symbol(self._h, i).decode() for i in range(L.relx_plan_symbol_count(self._h))]
 
+    @property
+    def num_stages(self):
+        return N.lib().relx_plan_stage_count(self._h)
+
+    @property
+    def stages(self):
+        """Decoded value stages (reference TypedPlanHandle.stages,
+        libreloc/python/PyReloc.cpp:241-259): transform, policy, input and
+        output dtypes with signedness, rank, axis and channel presence."""
+        out = []
+        for i in range(self.num_stages):
+            s = N.relx_plan_stage_info()
+            N.lib().relx_plan_stage(self._h, i, ctypes.byref(s))
+            out.append({"transform": _TRANSFORM_NAMES[s.transform],
+                        "policy": _POLICY_NAMES.get(s.policy, "unknown"),
+                        "input": _DTYPE_NAMES.get((s.in_kind, s.in_bits), "unknown"),
+                        "input_signedness": _SIGNEDNESS[s.in_signedness],
+                        "output": _DTYPE_NAMES.get((s.out_kind, s.out_bits), "unknown"),
+                        "output_signedness": _SIGNEDNESS[s.out_signedness],
+                        "rank": s.rank, "axis": s.axis, "has_channel": bool(s.has_channel),
+                        "scale": _PARAM_KINDS[s.scale_kind],
+                        "zero_point": _PARAM_KINDS[s.zero_point_kind]})
+        return out
+
+    @property
+    def fills(self):
+        return N.lib().relx_plan_fill_count(self._h)
+
+    @property
+    def parameters(self):
+        """Runtime parameter declarations in first-declaration order
+        (reference TypedPlanHandle.parameters, PyReloc.cpp:263-288)."""
+        L = N.lib()
+        out = []
+        for i in range(L.relx_plan_parameter(self._h, -1, None, None, None, None, None, None)):
+            name = ctypes.c_char_p()
+            kind, bits, rank, stage, role = (ctypes.c_int() for _ in range(5))
+            L.relx_plan_parameter(self._h, i, ctypes.byref(name), ctypes.byref(kind),
+                                  ctypes.byref(bits), ctypes.byref(rank), ctypes.byref(stage),
+                                  ctypes.byref(role))
+            out.append({"name": name.value.decode(),
+                        "dtype": _DTYPE_NAMES.get((kind.value, bits.value), "unknown"),
+                        "rank": rank.value, "stage": stage.value,
+                        "role": "scale" if role.value == 0 else "zero_point"})
+        return out
+
     def __del__(self):
         h = getattr(self, "_h", None)
         if h:
@@ -119,6 +165,9 @@ def load_indexed_plan(blob):
 _DTYPE_NAMES = {(0, 32): "float32", (0, 16): "float16", (0, 64): "float64", (1, 16): "bfloat16",
                 (2, 8): "int8", (2, 16): "int16", (2, 32): "int32", (2, 64): "int64"}
 _POLICY_NAMES = {0: "ieee_rne", 1: "exact", 2: "symmetric_rne", 3: "affine"}
+_TRANSFORM_NAMES = {0: "cast", 1: "quantize", 2: "dequantize"}
+_SIGNEDNESS = {0: "signless", 1: "signed", 2: "unsigned"}
+_PARAM_KINDS = {0: None, 1: "inline", 2: "binding"}
 
 
 def _indexed_metadata(blob):
