@@ -1,0 +1,330 @@
+"""librelx's pipeline on the CPU, over a stand-in for the HIP runtime.
+
+tests/native/pipeline_driver links the library's host sources (plan,
+program, runtime, workers, indexed, transfer, capi) against
+tests/native/hip_fake.cpp, under ThreadSanitizer, and runs C-ABI scenarios
+over cases written here (plan bytes, bindings, source, the oracle's result).
+The stand-in runs streams as worker threads, events as stream markers, and
+every relayout launch with the element-wise kernel's semantics; it checks
+each access to device memory, page-locked memory and registered host
+buffers against the ordering HIP guarantees (stream order, events, host
+synchronization), so a missing wait is reported whatever the timing.
+
+Covered here, the way the reference's host backend and fault shim cover
+its transfer engine (libreloc/include/reloc/HostBackend.h:27-75,
+libreloc/test/TransferTestSupport.h:83-164):
+  * ring and event ordering: every chunk size, ring depth, worker count,
+    host-stage boundary, pageable and pinned sources, no_wait calls,
+    caller streams (none, the null stream, a stream of their own), groups,
+    submitted groups in flight together, device-to-host, device-resident
+    relayouts, the allocation-free upload; results equal the oracle's and
+    no access is unordered, with delays and jitter on every operation;
+  * faults: allocation failures, copies, launches, event records and
+    stream waits refused when submitted, copies and kernels that fault on
+    their stream (a sticky device error), a synchronize that fails, and a
+    device whose completion cannot be proven: the error code and the
+    completion the C ABI reports, whether the context is quarantined, and
+    what the next call and the close do;
+  * the checker itself: a device-to-host call told of no producer stream
+    reads a source still being written, which the checker reports.
+"""
+import json
+import os
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+from oracle import relx_oracle as O
+from sym_amd import encoder as EN
+from sym_amd import workloads as W
+from tests import fuzz_plans as F
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+NATIVE = os.path.join(HERE, "native")
+DRIVER = os.path.join(NATIVE, "_build", "pipeline_driver")
+
+
+@pytest.fixture(scope="module")
+def driver():
+    if shutil.which("g++") is None or not os.path.isdir("/opt/rocm/include/hip"):
+        pytest.skip("g++ or the HIP headers are missing")
+    r = subprocess.run(["make", "-s", "-j8", "-C", NATIVE], capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    return DRIVER
+
+
+def run(driver, lines, timeout=240):
+    """Run scenario lines; returns the parsed results (ThreadSanitizer
+    findings fail the test)."""
+    env = dict(os.environ, TSAN_OPTIONS="halt_on_error=0 exitcode=66 report_signal_unsafe=0")
+    r = subprocess.run([driver], input="\n".join(lines) + "\n", capture_output=True, text=True,
+                       timeout=timeout, env=env)
+    assert "ThreadSanitizer" not in r.stderr, r.stderr[-6000:]
+    assert r.returncode == 0, (r.returncode, r.stderr[-3000:])
+    out = [json.loads(l) for l in r.stdout.splitlines() if l.startswith("{")]
+    assert len(out) == len(lines), r.stdout[-2000:]
+    return out
+
+
+# ------------------------------------------------------------------ cases
+
+def write_case(root, name, blob, src, want=None, syms=None, params=None, index=None):
+    """params: {name: (kind, bits, array)}; index: (bits, array)."""
+    d = os.path.join(str(root), name)
+    os.makedirs(d, exist_ok=True)
+    with open(os.path.join(d, "plan.bin"), "wb") as f:
+        f.write(blob)
+    lines = ["sym %s %d" % (k, v) for k, v in (syms or {}).items()]
+    for i, (pname, (kind, bits, arr)) in enumerate((params or {}).items()):
+        fn = "param%d.bin" % i
+        arr = np.ascontiguousarray(arr)
+        with open(os.path.join(d, fn), "wb") as f:
+            f.write(arr.tobytes())
+        lines.append("param %s %d %d %d %d %s" % (pname, kind, bits, arr.ndim, arr.size, fn))
+    if index is not None:
+        bits, arr = index
+        with open(os.path.join(d, "index.bin"), "wb") as f:
+            f.write(np.ascontiguousarray(arr).tobytes())
+        lines.append("index 2 %d 1 %d index.bin" % (bits, len(arr)))
+    with open(os.path.join(d, "bind.txt"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+    with open(os.path.join(d, "src.bin"), "wb") as f:
+        f.write(np.ascontiguousarray(src).tobytes())
+    if want is not None:
+        with open(os.path.join(d, "want.bin"), "wb") as f:
+            f.write(bytes(want))
+    return d
+
+
+@pytest.fixture(scope="module")
+def cases(tmp_path_factory):
+    root = tmp_path_factory.mktemp("fake_cases")
+    c = {}
+    # C1 (layout only): 2^18 f32, transpose [4096, 64] -> [64, 4096]
+    n = 1 << 18
+    x = W.c1_input(n)
+    blob = W.c1_plan().blob
+    want = O.execute_layout(O.bind(O.decode_plan(blob), {"s0": n}), x.tobytes())
+    c["c1"] = write_case(root, "c1", blob, x, want, {"s0": n})
+    # C2 (typed, one per-tensor cast): the host applies it at boundary 1
+    shape = (2, 3, 32, 48)
+    x = W.c2_input(*shape)
+    blob = W.c2_plan(*shape).blob
+    c["c2"] = write_case(root, "c2", blob, x, O.run_typed(blob, {}, {}, x).tobytes())
+    # C5 (a per-head quantize on the device: results not emulated)
+    b, s = 2, 64
+    x, scale = W.c5_input(b, s)
+    c["c5"] = write_case(root, "c5", W.c5_plan().blob, x, None, {"B": b, "S": s},
+                         {"scale": (0, 32, scale)})
+    # indexed: rows of an f32 table (copy gather)
+    rng = np.random.default_rng(5)
+    table = rng.standard_normal((4096, 64)).astype(np.float32)
+    idx = rng.integers(0, 4096, 3000).astype(np.int64)
+    iplan = EN.encode_index_select(["N", "D"], "float32", "M", "int64", "float32")
+    syms = {"N": 4096, "D": 64, "M": len(idx)}
+    c["ix"] = write_case(root, "ix", iplan, table, table[idx].tobytes(), syms, index=(64, idx))
+    # random layout plans (pads, transposes, reshapes) from the fuzz set
+    k = 0
+    for seed in range(0, 200):
+        r = F.make_plan(seed)
+        if r is None or r[0].typed:
+            continue
+        plan, src, _ = r
+        try:
+            want = O.execute_layout(O.bind(O.decode_plan(plan.blob), {}), src.tobytes())
+        except (O.BindError, O.ExecutionError):
+            continue
+        c["fz%d" % k] = write_case(root, "fz%d" % seed, plan.blob, src, want)
+        k += 1
+        if k == 6:
+            break
+    return c
+
+
+def ok(res):
+    """Every call succeeded, results matched, no unordered access."""
+    assert not res["setup_error"], res
+    assert all(cl["rc"] == 0 for cl in res["calls"]), res["calls"]
+    assert res["close"]["rc"] == 0, res["close"]
+    assert res["mismatches"] == 0, res["notes"]
+    assert not res["violations"], res["violations"][:5]
+    assert not res["quarantined"]
+
+
+# ------------------------------------------------------------ ordering
+
+DELAYS = "delay_copy=300 delay_kernel=300 jitter=1"
+
+
+def test_upload_orders_and_results(driver, cases):
+    lines = []
+    for name in ("c1", "fz0", "fz1", "fz2", "fz3", "fz4", "fz5"):
+        for pinned in (0, 1):
+            for chunk, nbuf in ((0, 0), (65536, 2), (16384, 3)):
+                lines.append("h2d %s pinned=%d chunk=%d nbuf=%d threads=3 seed=%d %s"
+                             % (cases[name], pinned, chunk, nbuf, len(lines), DELAYS))
+    res = run(driver, lines)
+    for r in res:
+        ok(r)
+        assert r["checked"] == 2
+    chunked = [r for r in res if "chunk=16384" in lines[res.index(r)]]
+    assert max(r["report"]["chunks"] for r in chunked) >= 8
+
+
+def test_host_stages_and_device_stages(driver, cases):
+    lines = ["h2d %s hs=1 chunk=%d nbuf=2 threads=4 seed=%d %s" % (cases["c2"], ch, i, DELAYS)
+             for i, ch in enumerate((0, 8192, 65536))]
+    # device value stages: ordering only (the stand-in does not run stages)
+    lines += ["h2d %s chunk=%d check=0 seed=%d %s" % (cases["c5"], ch, i, DELAYS)
+              for i, ch in enumerate((0, 32768))]
+    lines += ["h2d %s hs=0 check=0 chunk=8192 %s" % (cases["c2"], DELAYS)]
+    res = run(driver, lines)
+    for r in res:
+        ok(r)
+    assert all(r["report"]["wire_boundary"] == 1 and r["checked"] == 2 for r in res[:3])
+    assert all(r["counts"]["unemulated"] > 0 for r in res[3:])
+
+
+@pytest.mark.parametrize("caller", ["none", "null", "stream"])
+def test_no_wait_and_caller_streams(driver, cases, caller):
+    lines = ["h2d %s caller=%s nowait=%d chunk=32768 nbuf=2 repeat=3 seed=%d %s"
+             % (cases[n], caller, nw, i, DELAYS)
+             for i, (n, nw) in enumerate(((n, nw) for n in ("c1", "fz2") for nw in (0, 1)))]
+    for r in run(driver, lines):
+        ok(r)
+
+
+@pytest.mark.parametrize("caller", ["none", "stream"])
+def test_no_wait_calls_back_to_back(driver, cases, caller):
+    """Calls in flight together: each call's copies overwrite the wire arena
+    the call before may still be reading, and its kernels the destination
+    that call writes."""
+    lines = ["h2d %s caller=%s nowait=1 burst=1 pinned=%d chunk=%d nbuf=2 repeat=4 seed=%d %s"
+             % (cases[n], caller, pinned, chunk, i, DELAYS)
+             for i, (n, pinned, chunk) in enumerate(
+                 (n, p, ch) for n in ("c1", "fz2") for p in (0, 1) for ch in (0, 16384, 65536))]
+    res = run(driver, lines)
+    for r in res:
+        ok(r)
+        assert r["checked"] == 1
+
+
+def test_groups_and_submissions(driver, cases):
+    lines = ["group %s members=3 chunk=32768 nbuf=2 %s" % (cases["c1"], DELAYS),
+             "group %s members=4 hs=1 chunk=8192 nbuf=3 %s" % (cases["c2"], DELAYS),
+             "submit %s members=2 chunk=32768 %s" % (cases["c1"], DELAYS),
+             "submit %s members=2 chunk=16384 nbuf=2 twice=1 %s" % (cases["fz1"], DELAYS),
+             "submit %s members=2 pinned=1 twice=1 %s" % (cases["c1"], DELAYS)]
+    res = run(driver, lines)
+    for r in res:
+        ok(r)
+    assert res[0]["checked"] == 3 and res[3]["checked"] == 4
+
+
+def test_indexed_uploads(driver, cases):
+    lines = ["h2d %s chunk=%d nbuf=2 seed=%d %s" % (cases["ix"], ch, i, DELAYS)
+             for i, ch in enumerate((0, 65536, 4096))]
+    lines.append("h2d %s pinned=1 %s" % (cases["ix"], DELAYS))
+    res = run(driver, lines)
+    for r in res:
+        ok(r)
+    assert {r["report"]["implementation"] for r in res} >= {"hip_table_gather"} or \
+        all(r["report"]["implementation"].startswith("hip_relayout") for r in res)
+
+
+def test_device_to_host_and_device_resident(driver, cases):
+    lines = []
+    for name in ("c1", "fz0", "fz3"):
+        for pinned in (0, 1):
+            for chunk in (0, 16384):
+                lines.append("d2h %s pinned=%d chunk=%d nbuf=2 caller=stream %s"
+                             % (cases[name], pinned, chunk, DELAYS))
+        for caller in ("null", "stream"):
+            lines.append("device %s caller=%s %s" % (cases[name], caller, DELAYS))
+    lines.append("d2h %s caller=null %s" % (cases["c1"], DELAYS))
+    for r in run(driver, lines):
+        ok(r)
+
+
+def test_allocation_free_upload(driver, cases):
+    lines = ["static %s %s" % (cases["c1"], DELAYS), "static %s %s" % (cases["fz2"], DELAYS)]
+    for r in run(driver, lines):
+        ok(r)
+
+
+def test_checker_reports_a_missing_wait(driver, cases):
+    """The device source is written on the caller's stream, but the call is
+    told of no producer stream: the relayout reads it unordered."""
+    res = run(driver, ["d2h %s caller=stream_untold %s" % (cases["c1"], DELAYS)])[0]
+    assert any("relayout kernel" in v and "unordered" in v for v in res["violations"]), res
+
+
+# --------------------------------------------------------------- faults
+
+def fault(driver, case, knob, extra=""):
+    return run(driver, ["h2d %s chunk=32768 nbuf=2 repeat=2 %s %s" % (case, knob, extra)])[0]
+
+
+def test_faults_when_submitted(driver, cases):
+    """A call refused when submitted fails with backend_failure; the
+    context drains (completion known), stays usable, and closes."""
+    for knob in ("fail_copy_at=3", "fail_launch_at=2", "fail_record_at=4", "fail_wait_at=2"):
+        r = fault(driver, cases["c1"], knob, DELAYS)
+        first = r["calls"][0]
+        assert first["rc"] == 1 and first["code"] == "backend_failure", (knob, r)
+        assert first["completion"] == 1, (knob, first)  # drained: complete
+        assert not r["quarantined"] and r["close"]["rc"] == 0, (knob, r)
+        assert not r["violations"], (knob, r["violations"][:3])
+        # the next call on the same context succeeds and is right
+        assert r["calls"][1]["rc"] == 0 and r["checked"] == 1 and r["mismatches"] == 0, (knob, r)
+
+
+def test_allocation_failures(driver, cases):
+    # the wire arena (first device allocation of the call) cannot be made
+    r = fault(driver, cases["c1"], "fail_malloc_at=1")
+    assert r["calls"][0]["code"] == "backend_failure" and "OutOfMemory" in r["calls"][0]["message"]
+    assert r["calls"][0]["completion"] == 1 and not r["quarantined"] and r["close"]["rc"] == 0
+    # the pinned ring cannot be made (pageable source)
+    r = fault(driver, cases["c1"], "fail_host_malloc_at=1")
+    assert r["calls"][0]["code"] == "backend_failure" and "OutOfMemory" in r["calls"][0]["message"]
+    assert not r["quarantined"]
+    # the context itself cannot be made
+    r = run(driver, ["h2d %s fail_host_malloc_at=1 knobs_first=1" % cases["c1"]])[0]
+    assert r["create"]["rc"] == 1 and r["create"]["code"] == "backend_failure"
+
+
+def test_faults_on_the_stream_quarantine(driver, cases):
+    """A copy or kernel that faults on its stream leaves a sticky device
+    error: the call fails, the drain cannot prove completion, the context
+    is quarantined and refuses later calls; closing reports the unknown
+    completion."""
+    for knob in ("fail_copy_async_at=2", "fail_kernel_async_at=1"):
+        r = fault(driver, cases["c1"], knob, DELAYS)
+        first = r["calls"][0]
+        assert first["rc"] == 1 and first["code"] == "backend_failure", (knob, r)
+        assert first["completion"] == 2, (knob, first)  # unknown
+        assert r["quarantined"] == 1
+        assert r["close"]["rc"] == 1 and r["close"]["code"] == "completion_unknown"
+
+
+def test_unknown_completion_quarantines(driver, cases):
+    """Every synchronize fails (the reference's quiesce returning Unknown):
+    the call fails with an unknown completion, the context is quarantined,
+    and close keeps its memory."""
+    r = fault(driver, cases["c1"], "sync_unknown=1", DELAYS)
+    first = r["calls"][0]
+    assert first["code"] == "backend_failure" and first["completion"] == 2
+    assert r["quarantined"] == 1 and r["close"]["code"] == "completion_unknown"
+    assert not [v for v in r["violations"] if "hipFree" in v or "hipHostFree" in v]
+
+
+def test_a_failed_synchronize_once(driver, cases):
+    """One synchronize fails, the rest work: the call reports the failure,
+    the drain succeeds, the context stays usable and closes cleanly."""
+    r = fault(driver, cases["c1"], "fail_sync_at=1", DELAYS)
+    first = r["calls"][0]
+    assert first["rc"] == 1 and first["code"] == "backend_failure"
+    assert first["completion"] == 1 and not r["quarantined"]
+    assert r["close"]["rc"] == 0
