@@ -372,11 +372,17 @@ int relx_submit_group_h2d(relx_ctx *ctx, int n, const relx_bound *const *bounds,
                           const size_t *dst_bytes, const relx_options *opt, relx_report *reports,
                           relx_report *total, relx_completion **out, relx_err *err);
 
-/* Completion::query: *done = 1 once every kernel of the call finished. */
+/* Completion::query: *done = 1 once every kernel of the call finished.
+ * When the device reports a failure for the group, the context is drained:
+ * "backend_failure" with a complete completion, or, when completion cannot
+ * be proven, "completion_unknown" with RELX_UNKNOWN and the context
+ * quarantined (reference Completion, libreloc/src/DispatchResources.cpp:
+ * 325-361). The outcome is kept: later queries and waits report it. */
 int relx_completion_query(relx_completion *c, int *done, relx_err *err);
 
 /* Completion::wait: block until done; reports a channel outside the
- * parameters (`channel_out_of_range`) like the blocking call would. */
+ * parameters (`channel_out_of_range`) like the blocking call would, and a
+ * device failure as relx_completion_query does. */
 int relx_completion_wait(relx_completion *c, relx_err *err);
 
 /* Completion::waitStream: order `stream` after the call without blocking

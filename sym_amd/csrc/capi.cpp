@@ -13,7 +13,6 @@ void execute_members(Context &ctx, int n, BoundHandle *const *bounds, const void
                      const size_t *src_bytes, void *const *dsts, const size_t *dst_bytes,
                      const relx_options &opt, relx_report *reports, relx_report *total,
                      Completion *comp);
-void completion_wait(Completion &c);
 std::unique_ptr<Context> make_context(int device, int64_t max_retained);
 bool drain(Context &ctx);
 void destroy_context(Context &ctx);
@@ -45,6 +44,11 @@ struct relx_ctx {
 
 struct relx_completion {
   relx::Completion c;
+  // The outcome of a group the device failed, kept for later queries and
+  // waits (reference Completion's stored TransferOutcome).
+  bool failed = false;
+  std::string code, message;
+  int completion = 0;
 };
 
 namespace {
@@ -80,6 +84,40 @@ template <class F> int guarded(relx_err *err, F &&fn) {
     set_err(err, "internal_error", e.what());
   }
   return RELX_ERROR;
+}
+
+// Errors raised before a call enqueues any work.
+bool before_launch(const char *code) {
+  static const char *const codes[] = {"invalid_argument", "invalid_options", "insufficient_capacity",
+                                      "invalid_view",     "plan_mismatch",   "resources_closed",
+                                      "unsupported_layout", "device_mismatch", "backend_mismatch",
+                                      "invalid_boundary"};
+  for (const char *c : codes)
+    if (std::strcmp(code, c) == 0)
+      return true;
+  return false;
+}
+
+// After a failed call: drain what was enqueued. When completion cannot be
+// proven the context is quarantined and the error becomes
+// "completion_unknown" with an unknown completion (reference
+// libreloc/src/DispatchResources.cpp:652-666); otherwise the call's own
+// error stands, with a known completion (complete, or not launched for
+// errors raised before any work was enqueued).
+void after_failure(relx::Context &c, relx_err *err) {
+  ++c.failures;
+  if (!relx::drain(c)) {
+    c.quarantined = true;
+    if (err) {
+      const std::string cause = std::string(err->code) + ": " + err->message;
+      set_err(err, "completion_unknown",
+              "the call failed (" + cause + ") and its context could not be drained; quarantined",
+              -1, RELX_UNKNOWN);
+    }
+    return;
+  }
+  if (err)
+    err->completion = before_launch(err->code) ? RELX_NOT_LAUNCHED : RELX_COMPLETE;
 }
 
 } // namespace
@@ -400,15 +438,8 @@ static int run_group(relx_ctx *ctx, int n, const relx_bound *const *bounds,
     relx::execute_members(c, n, hs.data(), srcs, src_bytes, dsts, dst_bytes, o, reports, total,
                           comp ? &comp->c : nullptr);
   });
-  if (rc != RELX_OK) {
-    ++c.failures;
-    // Drain what was enqueued; unknown completion quarantines the context.
-    const bool complete = relx::drain(c);
-    if (err)
-      err->completion = complete ? RELX_COMPLETE : RELX_UNKNOWN;
-    if (!complete)
-      c.quarantined = true;
-  }
+  if (rc != RELX_OK)
+    after_failure(c, err);
   return rc;
 }
 
@@ -454,29 +485,78 @@ int relx_submit_group_h2d(relx_ctx *ctx, int n, const relx_bound *const *bounds,
   return RELX_OK;
 }
 
+namespace {
+
+// A submitted group the device failed: drain the context; when completion
+// cannot be proven the context is quarantined and the outcome is
+// "completion_unknown", else the device's error with a known completion
+// (reference Completion, libreloc/src/DispatchResources.cpp:325-361). The
+// outcome is kept for every later query and wait.
+int fail_completion(relx_completion *c, const char *what, hipError_t e, relx_err *err) {
+  if (!c->failed) {
+    relx::Context &ctx = *c->c.ctx;
+    std::lock_guard<std::mutex> g(ctx.mu);
+    ++ctx.failures;
+    c->failed = true;
+    if (relx::drain(ctx)) {
+      c->code = "backend_failure";
+      c->message = std::string(what) + ": " + hipGetErrorString(e);
+      c->completion = RELX_COMPLETE;
+    } else {
+      ctx.quarantined = true;
+      c->code = "completion_unknown";
+      c->message = std::string("asynchronous group failed (") + what + ": " + hipGetErrorString(e) +
+                   ") and the context could not be drained; quarantined";
+      c->completion = RELX_UNKNOWN;
+    }
+  }
+  set_err(err, c->code, c->message, -1, c->completion);
+  return RELX_ERROR;
+}
+
+} // namespace
+
 int relx_completion_query(relx_completion *c, int *done, relx_err *err) {
-  return guarded(err, [&] {
+  if (c && c->failed)
+    return fail_completion(c, "", hipSuccess, err);
+  hipError_t failed = hipSuccess;
+  const int rc = guarded(err, [&] {
     if (!c || !done)
       throw relx::Error("invalid_argument", "null argument");
     relx::DeviceScope scope(c->c.ctx->device);
     const hipError_t e = hipEventQuery(c->c.ev);
-    if (e != hipSuccess && e != hipErrorNotReady)
-      throw relx::Error("backend_failure", std::string("hipEventQuery: ") + hipGetErrorString(e));
+    if (e != hipSuccess && e != hipErrorNotReady) {
+      failed = e;
+      return;
+    }
     *done = e == hipSuccess ? 1 : 0;
     if (*done)
-      relx::completion_wait(c->c); // reports a channel error once complete
+      relx::completion_check(c->c); // reports a channel error once complete
   });
+  return failed != hipSuccess ? fail_completion(c, "hipEventQuery", failed, err) : rc;
 }
 
 int relx_completion_wait(relx_completion *c, relx_err *err) {
-  return guarded(err, [&] {
+  if (c && c->failed)
+    return fail_completion(c, "", hipSuccess, err);
+  hipError_t failed = hipSuccess;
+  const int rc = guarded(err, [&] {
     if (!c)
       throw relx::Error("invalid_argument", "null completion");
-    relx::completion_wait(c->c);
+    relx::DeviceScope scope(c->c.ctx->device);
+    const hipError_t e = hipEventSynchronize(c->c.ev);
+    if (e != hipSuccess) {
+      failed = e;
+      return;
+    }
+    relx::completion_check(c->c);
   });
+  return failed != hipSuccess ? fail_completion(c, "hipEventSynchronize", failed, err) : rc;
 }
 
 int relx_completion_wait_stream(relx_completion *c, uint64_t stream, relx_err *err) {
+  if (c && c->failed)
+    return fail_completion(c, "", hipSuccess, err);
   return guarded(err, [&] {
     if (!c)
       throw relx::Error("invalid_argument", "null completion");
@@ -527,14 +607,8 @@ int relx_execute_d2h(relx_ctx *ctx, const relx_bound *bound, const void *src, si
     relx::execute_d2h(c, const_cast<relx::BoundHandle &>(bound->h), src, src_bytes, dst,
                       dst_bytes, o, report);
   });
-  if (rc != RELX_OK) {
-    ++c.failures;
-    const bool complete = relx::drain(c);
-    if (err)
-      err->completion = complete ? RELX_COMPLETE : RELX_UNKNOWN;
-    if (!complete)
-      c.quarantined = true;
-  }
+  if (rc != RELX_OK)
+    after_failure(c, err);
   return rc;
 }
 
@@ -563,14 +637,8 @@ int relx_execute_h2d_static(relx_ctx *ctx, const relx_bound *bound, const void *
     relx::execute_static(c, const_cast<relx::BoundHandle &>(bound->h), src, src_bytes, dst,
                          dst_bytes, o, report);
   });
-  if (rc != RELX_OK) {
-    ++c.failures;
-    const bool complete = relx::drain(c);
-    if (err)
-      err->completion = complete ? RELX_COMPLETE : RELX_UNKNOWN;
-    if (!complete)
-      c.quarantined = true;
-  }
+  if (rc != RELX_OK)
+    after_failure(c, err);
   return rc;
 }
 
@@ -635,14 +703,8 @@ int relx_execute_transfer(relx_ctx *ctx, const relx_bound *bound, const relx_vie
     relx::execute_transfer(c, const_cast<relx::BoundHandle &>(bound->h), *source, *destination,
                            direction, o, report);
   });
-  if (rc != RELX_OK) {
-    ++c.failures;
-    const bool complete = relx::drain(c);
-    if (err)
-      err->completion = complete ? RELX_COMPLETE : RELX_UNKNOWN;
-    if (!complete)
-      c.quarantined = true;
-  }
+  if (rc != RELX_OK)
+    after_failure(c, err);
   return rc;
 }
 
@@ -678,6 +740,9 @@ int relx_index_select_device(relx_ctx *ctx, const relx_bound *bound, const void 
   return guarded(err, [&] {
     if (!ctx || !bound)
       throw relx::Error("invalid_argument", "null argument");
+    std::lock_guard<std::mutex> g(ctx->ctx->mu);
+    if (ctx->ctx->closed || ctx->ctx->quarantined)
+      throw relx::Error("resources_closed", "context is closed or quarantined");
     relx::index_select_device(*ctx->ctx, const_cast<relx::BoundHandle &>(bound->h), table,
                               table_bytes, dst, dst_bytes, reinterpret_cast<hipStream_t>(stream));
   });

@@ -741,6 +741,11 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
 void completion_wait(Completion &c) {
   DeviceGuard guard(c.ctx->device);
   HIPCHECK(hipEventSynchronize(c.ev));
+  completion_check(c);
+}
+
+// Once the completion's event has completed: the call's status flag.
+void completion_check(Completion &c) {
   if (c.generic && !c.checked) {
     c.checked = true;
     if (read_status(c.status))

@@ -333,4 +333,9 @@ struct Completion {
   bool checked = false;
 };
 
+// Wait for a completion, then check its status flag ("channel_out_of_range").
+void completion_wait(Completion &c);
+// The status check alone, once the completion's event has completed.
+void completion_check(Completion &c);
+
 } // namespace relx

@@ -253,6 +253,12 @@ struct Caller {
 fake_knobs g_armed{};
 void arm() { fake_configure(&g_armed); }
 
+bool quarantined(relx_ctx *ctx) {
+  relx_ctx_stats st{};
+  relx_ctx_stats_get(ctx, &st);
+  return st.quarantined != 0;
+}
+
 void run_h2d(const Case &c, const Opts &o, Result &r, relx_ctx *ctx) {
   const size_t out = static_cast<size_t>(c.info.destination_bytes);
   const bool pinned = o.get("pinned", 0) == 1;
@@ -290,6 +296,15 @@ void run_h2d(const Case &c, const Opts &o, Result &r, relx_ctx *ctx) {
       relx_ctx_stats st{};
       relx_ctx_stats_get(ctx, &st);
       failed = st.quarantined != 0; // a drained context takes the next call
+      // persist: call a quarantined context again (it must refuse at once)
+      if (failed && o.get("persist", 0)) {
+        for (++i; i < repeat; ++i) {
+          relx_err e3{};
+          relx_options o3 = options_of(o);
+          r.calls.push_back(call_of(
+              relx_execute_h2d(ctx, c.bound, src, c.src.size(), dst, out, &o3, nullptr, &e3), e3));
+        }
+      }
       continue;
     }
     if (burst && i + 1 < repeat)
@@ -420,9 +435,10 @@ void run_d2h(const Case &c, const Opts &o, Result &r, relx_ctx *ctx) {
     relx_err e{};
     const int rc = relx_execute_d2h(ctx, c.bound, src, c.src.size(), dst, out, &opt, &r.report, &e);
     r.calls.push_back(call_of(rc, e));
-    ok = rc == RELX_OK;
-    if (ok)
+    if (rc == RELX_OK)
       check(r, c, dst, out, o.get("check", 1) != 0);
+    else
+      ok = !quarantined(ctx); // a drained context takes the next call
   }
   if (!pinned)
     fake_unregister_host(dst);
@@ -450,13 +466,14 @@ void run_device(const Case &c, const Opts &o, Result &r, relx_ctx *ctx) {
     const int rc = relx_relayout_device(ctx, c.bound, static_cast<int>(o.get("hs", 0)), wire, dst,
                                         reinterpret_cast<uint64_t>(caller.s), &e);
     r.calls.push_back(call_of(rc, e));
-    ok = rc == RELX_OK;
-    if (!ok)
-      break;
-    (void)hipStreamSynchronize(caller.s);
+    const hipError_t se = hipStreamSynchronize(caller.s);
     relx_err e2{};
     const int rc2 = relx_ctx_synchronize(ctx, &e2);
     r.calls.push_back(call_of(rc2, e2));
+    if (rc != RELX_OK || rc2 != RELX_OK || se != hipSuccess) {
+      ok = se == hipSuccess; // a device fault leaves the buffers to the device
+      continue;
+    }
     fake_host_read(dst, out, "host reads the result");
     (void)hipMemcpy(host.data(), dst, out, hipMemcpyDeviceToHost);
     check(r, c, host.data(), out, o.get("check", 1) != 0);
@@ -485,9 +502,10 @@ void run_static(const Case &c, const Opts &o, Result &r, relx_ctx *ctx) {
     relx_err e{};
     const int rc = relx_execute_h2d_static(ctx, c.bound, src, c.src.size(), dst, out, &opt, &r.report, &e);
     r.calls.push_back(call_of(rc, e));
-    ok = rc == RELX_OK;
-    if (!ok)
-      break;
+    if (rc != RELX_OK) {
+      ok = !quarantined(ctx); // a drained context takes the next call
+      continue;
+    }
     fake_host_read(dst, out, "host reads the result");
     (void)hipMemcpy(host.data(), dst, out, hipMemcpyDeviceToHost);
     check(r, c, host.data(), out, o.get("check", 1) != 0);

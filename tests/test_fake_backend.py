@@ -303,7 +303,8 @@ def test_faults_on_the_stream_quarantine(driver, cases):
     for knob in ("fail_copy_async_at=2", "fail_kernel_async_at=1"):
         r = fault(driver, cases["c1"], knob, DELAYS)
         first = r["calls"][0]
-        assert first["rc"] == 1 and first["code"] == "backend_failure", (knob, r)
+        assert first["rc"] == 1 and first["code"] == "completion_unknown", (knob, r)
+        assert "backend_failure" in first["message"] and "quarantined" in first["message"]
         assert first["completion"] == 2, (knob, first)  # unknown
         assert r["quarantined"] == 1
         assert r["close"]["rc"] == 1 and r["close"]["code"] == "completion_unknown"
@@ -315,7 +316,7 @@ def test_unknown_completion_quarantines(driver, cases):
     and close keeps its memory."""
     r = fault(driver, cases["c1"], "sync_unknown=1", DELAYS)
     first = r["calls"][0]
-    assert first["code"] == "backend_failure" and first["completion"] == 2
+    assert first["code"] == "completion_unknown" and first["completion"] == 2
     assert r["quarantined"] == 1 and r["close"]["code"] == "completion_unknown"
     assert not [v for v in r["violations"] if "hipFree" in v or "hipHostFree" in v]
 
@@ -328,3 +329,62 @@ def test_a_failed_synchronize_once(driver, cases):
     assert first["rc"] == 1 and first["code"] == "backend_failure"
     assert first["completion"] == 1 and not r["quarantined"]
     assert r["close"]["rc"] == 0
+
+
+def test_submitted_group_failures(driver, cases):
+    """A submitted group the device fails: the completion's query or wait
+    reports it; a sticky fault cannot be drained (completion_unknown, the
+    context quarantined), a failed wait on a healthy device can
+    (backend_failure, complete); the outcome is kept."""
+    line = "submit %s members=2 chunk=32768 pinned=1 %s"
+    r = run(driver, [line % (cases["c1"], "fail_kernel_async_at=1 " + DELAYS)])[0]
+    codes = [cl["code"] for cl in r["calls"] if cl["rc"]]
+    assert codes and codes[-1] == "completion_unknown", r["calls"]
+    assert [cl for cl in r["calls"] if cl["rc"]][-1]["completion"] == 2
+    assert r["quarantined"] == 1 and r["close"]["code"] == "completion_unknown"
+    r = run(driver, [line % (cases["c1"], "fail_sync_at=1")])[0]
+    bad = [cl for cl in r["calls"] if cl["rc"]]
+    assert [cl["code"] for cl in bad] == ["backend_failure"], r["calls"]
+    assert bad[0]["completion"] == 1 and "hipEventSynchronize" in bad[0]["message"]
+    assert not r["quarantined"] and r["close"]["rc"] == 0
+
+
+def test_device_to_host_failures(driver, cases):
+    line = "d2h %s chunk=16384 nbuf=2 pinned=%d repeat=2 %s"
+    # refused launch: drained, the next call works
+    r = run(driver, [line % (cases["c1"], 0, "fail_launch_at=1 " + DELAYS)])[0]
+    assert r["calls"][0]["code"] == "backend_failure" and r["calls"][0]["completion"] == 1
+    assert r["calls"][1]["rc"] == 0 and r["checked"] == 1 and r["mismatches"] == 0
+    assert not r["quarantined"] and r["close"]["rc"] == 0 and not r["violations"]
+    # a copy that faults on its stream: quarantined
+    r = run(driver, [line % (cases["c1"], 1, "fail_copy_async_at=3 " + DELAYS)])[0]
+    assert r["calls"][0]["code"] == "completion_unknown" and r["calls"][0]["completion"] == 2
+    assert r["quarantined"] == 1 and len(r["calls"]) == 1
+    assert r["close"]["code"] == "completion_unknown"
+
+
+def test_device_resident_and_static_failures(driver, cases):
+    # a refused relayout launch is reported; the context stays usable
+    r = run(driver, ["device %s caller=stream repeat=2 fail_launch_at=1 %s" % (cases["c1"], DELAYS)])[0]
+    assert r["calls"][0]["code"] == "backend_failure"
+    assert all(cl["rc"] == 0 for cl in r["calls"][1:]) and r["checked"] == 1
+    assert not r["violations"] and r["close"]["rc"] == 0
+    # the allocation-free upload: a refused copy drains; a faulting one quarantines
+    r = run(driver, ["static %s repeat=2 fail_copy_at=1 %s" % (cases["c1"], DELAYS)])[0]
+    assert r["calls"][0]["code"] == "backend_failure" and r["calls"][0]["completion"] == 1
+    assert r["calls"][1]["rc"] == 0 and r["checked"] == 1 and r["mismatches"] == 0
+    r = run(driver, ["static %s repeat=2 fail_copy_async_at=1 %s" % (cases["c1"], DELAYS)])[0]
+    assert r["calls"][0]["code"] == "completion_unknown" and r["calls"][0]["completion"] == 2
+    assert r["quarantined"] == 1 and r["close"]["code"] == "completion_unknown"
+
+
+def test_quarantined_context_refuses_calls(driver, cases):
+    """After a quarantine every call is refused with resources_closed."""
+    r = run(driver, ["h2d %s chunk=32768 repeat=3 persist=1 fail_copy_async_at=1 %s"
+                     % (cases["c1"], DELAYS)])[0]
+    assert r["quarantined"] == 1 and len(r["calls"]) == 3
+    assert [cl["code"] for cl in r["calls"]] == ["completion_unknown"] + ["resources_closed"] * 2
+    assert [cl["completion"] for cl in r["calls"]] == [2, 0, 0]
+    r = run(driver, ["group %s members=2 chunk=32768 fail_kernel_async_at=1 %s" % (cases["c1"], DELAYS)])[0]
+    assert r["calls"][0]["code"] == "completion_unknown" and r["calls"][0]["completion"] == 2
+    assert r["quarantined"] == 1
