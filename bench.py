@@ -61,7 +61,11 @@ def parse():
                     help="turn two rocprofv3 --pmc runs of --traffic-probe into profiles/traffic.json")
     ap.add_argument("--summarize-trace", metavar="TRACE_DIR",
                     help="per-call copy/kernel/staging timeline of a rocprofv3 marker + memory-copy "
-                         "+ kernel trace of the headline (RELX_TRACE=1)")
+                         "+ kernel trace of the headline (RELX_TRACE=1), or of a --trace-configs run "
+                         "(its output line saved as TRACE_DIR/plan.json)")
+    ap.add_argument("--trace-configs", metavar="CONFIGS",
+                    help="end-to-end uploads of these configs only, pageable then pinned (8 warm-up "
+                         "calls and 6 timed calls each), for a rocprofv3 trace; prints the call plan")
     return ap.parse_args()
 
 
@@ -517,6 +521,79 @@ def _union(intervals):
     return total + (cur_e - cur_s if cur_e is not None else 0)
 
 
+TRACE_WARMUP, TRACE_SAMPLES = 8, 6
+
+
+def trace_configs(torch, ctx, names, h2d_ceiling):
+    """The end-to-end calls a --trace-configs trace covers, in call order."""
+    entries = []
+    for name in names:
+        case = make_case(name)
+        for pinned in (False, True):
+            _, _, rep = e2e_rate(torch, ctx, case, TRACE_SAMPLES, pinned=pinned)
+            entries.append({"config": name, "source": "pinned" if pinned else "pageable",
+                            "warmup": TRACE_WARMUP, "samples": TRACE_SAMPLES,
+                            "wire_bytes": rep["wire_bytes"], "chunks": rep["chunks"],
+                            "implementation": rep["implementation"]})
+    return {"pinned_h2d_ceiling_GBps": round(h2d_ceiling, 2), "entries": entries}
+
+
+def _median(v):
+    v = sorted(v)
+    return v[len(v) // 2] if v else float("nan")
+
+
+def summarize_calls(d, plan):
+    """Where each end-to-end call's time goes, from the library's
+    `relx.h2d.call` ranges (host entry to return) of a --trace-configs run:
+    per config and source, medians over the timed calls of the wall time,
+    its ideal at the PCIe ceiling (wire bytes / pinned ceiling), the time
+    before the first copy starts (staging of the first chunk, call set-up),
+    the DMA engines' busy time and the gaps between copies, and the tail
+    after the last copy lands (last kernels and the host's wake-up)."""
+    marks = _csv_rows(d, "marker_api_trace.csv")
+    calls = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"]))
+                   for r in marks if r["Function"].startswith("relx.h2d.call"))
+    copies = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"]))
+                    for r in _csv_rows(d, "memory_copy_trace.csv")
+                    if r["Direction"] == "MEMORY_COPY_HOST_TO_DEVICE")
+    kernels = [(int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"])
+               for r in _csv_rows(d, "kernel_trace.csv") if "relx::" in r["Kernel_Name"]]
+    stage = [(int(r["Start_Timestamp"]), int(r["End_Timestamp"]))
+             for r in marks if r["Function"].startswith("relx.h2d.stage")]
+    ceiling = plan["pinned_h2d_ceiling_GBps"]
+    lines = ["| config | source | chunks | wall us | ideal us | PCIe frac | before first copy us | "
+             "DMA busy us | gaps between copies us | tail after last copy us | host staging us | kernels |",
+             "|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    i = 0
+    for e in plan["entries"]:
+        rows = []
+        for j in range(e["warmup"] + e["samples"]):
+            if i >= len(calls):
+                break
+            t0, t1 = calls[i]
+            i += 1
+            if j < e["warmup"]:
+                continue
+            cs = [c for c in copies if t0 <= c[0] < t1]
+            ks = [k for k in kernels if t0 <= k[0] < t1]
+            if not cs:
+                continue
+            busy = _union(cs)
+            first, last = min(c[0] for c in cs), max(c[1] for c in cs)
+            rows.append({"wall": (t1 - t0) / 1e3, "before": (first - t0) / 1e3, "busy": busy / 1e3,
+                         "gaps": (last - first - busy) / 1e3, "tail": (t1 - last) / 1e3,
+                         "stage": sum(b - a for a, b in stage if t0 <= a < t1) / 1e3, "kernels": len(ks)})
+        if not rows:
+            continue
+        m = {k: _median([r[k] for r in rows]) for k in rows[0]}
+        ideal = e["wire_bytes"] / ceiling / 1e3
+        lines.append("| %s | %s | %d | %.1f | %.1f | %.3f | %.1f | %.1f | %.1f | %.1f | %.1f | %d |" % (
+            e["config"], e["source"], e["chunks"], m["wall"], ideal, ideal / m["wall"], m["before"],
+            m["busy"], m["gaps"], m["tail"], m["stage"], m["kernels"]))
+    print("\n".join(lines))
+
+
 def summarize_trace(d):
     """Per-call timeline of the headline upload from a rocprofv3
     --kernel-trace --memory-copy-trace --marker-trace run with RELX_TRACE=1:
@@ -903,7 +980,12 @@ def headline(torch, P, args, h2d_ceiling):
 def main():
     args = parse()
     if args.summarize_trace:
-        summarize_trace(args.summarize_trace)
+        plan_path = os.path.join(args.summarize_trace, "plan.json")
+        if os.path.exists(plan_path):
+            with open(plan_path) as f:
+                summarize_calls(args.summarize_trace, json.loads(f.read().strip().splitlines()[-1]))
+        else:
+            summarize_trace(args.summarize_trace)
         return
     if args.summarize_pmc:
         probe = None
@@ -933,6 +1015,11 @@ def main():
     from sym_amd import pyreloc as P
     ctx = P.Context(0)
     h2d_ceiling = P.measure_h2d(0, 256 << 20, 20, 3)
+
+    if args.trace_configs:
+        print(json.dumps(trace_configs(torch, ctx, args.trace_configs.split(","), h2d_ceiling)), flush=True)
+        ctx.close()
+        return
 
     if args.traffic_probe:
         traffic_probe(torch, ctx, args.configs.split(","))

@@ -145,12 +145,12 @@ const Roctx &roctx() {
 
 } // namespace
 
-TraceRange::TraceRange(const char *name, int64_t chunk) {
+TraceRange::TraceRange(const char *name, int64_t index, const char *key) {
   const Roctx &r = roctx();
   if (!r.push)
     return;
   char buf[96];
-  std::snprintf(buf, sizeof(buf), "%s chunk=%lld", name, static_cast<long long>(chunk));
+  std::snprintf(buf, sizeof(buf), "%s %s=%lld", name, key, static_cast<long long>(index));
   r.push(buf);
   open_ = true;
 }
@@ -378,6 +378,7 @@ void execute_members(Context &ctx, int n, BoundHandle *const *bounds, const void
                      const size_t *src_bytes, void *const *dsts, const size_t *dst_bytes,
                      const relx_options &opt, relx_report *reports, relx_report *total,
                      Completion *comp) {
+  TraceRange call_range("relx.h2d.call", ctx.calls, "call");
   DeviceGuard guard(ctx.device);
   std::vector<Member> ms;
   size_t wire_total = 0;
@@ -803,6 +804,7 @@ D2hPlan d2h_plan(const DeviceProgram &dp, int64_t chunk_bytes, bool pinned) {
 // ring and the worker threads copy each slot out as soon as its copy lands.
 void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes, void *dst,
                  size_t dst_bytes, const relx_options &opt, relx_report *report) {
+  TraceRange call_range("relx.d2h.call", ctx.calls, "call");
   DeviceGuard guard(ctx.device);
   if (h.bound->indexed) // libreloc/src/Dispatch.cpp:196-201: indexed sources are host rows
     throw Error("plan_mismatch", "indexed source requires the prepared host row shape");

@@ -232,7 +232,8 @@ int64_t verify_launches(BoundHandle &h, uint32_t k, int64_t chunk_bytes);
 // first use; otherwise a range costs one branch. The name carries the chunk.
 class TraceRange {
 public:
-  TraceRange(const char *name, int64_t chunk);
+  // "<name> <key>=<index>", e.g. "relx.h2d.stage chunk=3", "relx.h2d.call call=7"
+  TraceRange(const char *name, int64_t index, const char *key = "chunk");
   ~TraceRange();
   TraceRange(const TraceRange &) = delete;
   TraceRange &operator=(const TraceRange &) = delete;
