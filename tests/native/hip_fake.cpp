@@ -120,6 +120,7 @@ struct Access {
 };
 std::vector<Access> g_acc;
 std::vector<std::string> g_violations;
+std::vector<VClock> g_tokens; // host hand-off snapshots
 
 fake_knobs g_knobs{};
 fake_counts g_counts{};
@@ -926,6 +927,20 @@ void fake_mark_user_pinned(const void *p) {
   auto it = g_allocs.find(reinterpret_cast<uintptr_t>(p));
   if (it != g_allocs.end())
     it->second.user = true;
+}
+
+int fake_host_handoff(void) {
+  std::lock_guard<std::mutex> g(g_mu);
+  g_tokens.push_back(host_tick().vc);
+  return static_cast<int>(g_tokens.size()) - 1;
+}
+
+void fake_host_adopt(int token) {
+  std::lock_guard<std::mutex> g(g_mu);
+  if (token < 0 || static_cast<size_t>(token) >= g_tokens.size())
+    return;
+  HostAgent &h = host_tick();
+  vjoin(h.vc, g_tokens[static_cast<size_t>(token)]);
 }
 
 void fake_shutdown(void) {

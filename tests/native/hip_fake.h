@@ -74,6 +74,12 @@ void fake_unregister_host(const void *p);
 // from them does not count as a host write made just before it.
 void fake_mark_user_pinned(const void *p);
 
+// Ordering between host threads (thread start and join, or any hand-off):
+// the thread that hands over takes a token of everything it has done so
+// far; the thread that takes over adopts it.
+int fake_host_handoff(void);
+void fake_host_adopt(int token);
+
 // Stop every stream's worker (streams of quarantined contexts included).
 void fake_shutdown(void);
 }

@@ -23,6 +23,8 @@
 //   device   relx_relayout_device on the caller stream after the wire was
 //            written on it
 //   static   relx_execute_h2d_static from a page-locked source
+//   threads  several host threads uploading at once, through one context
+//            (`shared=1`) or one context each
 // Options: pinned, chunk, nbuf, threads, hs (host stages), caller (none,
 // null, stream), nowait, repeat, members, twice, check, the fault knobs and
 // delays of fake_knobs, and devices / device (device count, context device).
@@ -484,6 +486,75 @@ void run_device(const Case &c, const Opts &o, Result &r, relx_ctx *ctx) {
   }
 }
 
+// Several host threads upload at once, each with its own buffers: through
+// the one context (`shared=1`, whose calls the library serializes) or one
+// context each, all sharing the bound plan and its device caches.
+void run_threads(const Case &c, const Opts &o, Result &r, relx_ctx *ctx) {
+  const int nt = static_cast<int>(o.get("threads_n", 4));
+  const bool shared = o.get("shared", 1) != 0;
+  const int repeat = static_cast<int>(o.get("repeat", 3));
+  const size_t out = static_cast<size_t>(c.info.destination_bytes);
+  std::vector<relx_ctx *> ctxs(static_cast<size_t>(nt), ctx);
+  for (int t = 0; t < nt && !shared; ++t) {
+    relx_err e{};
+    if (relx_ctx_create(0, 0, &ctxs[static_cast<size_t>(t)], &e) != RELX_OK) {
+      r.notes.push_back(std::string("context: ") + e.code);
+      return;
+    }
+  }
+  std::vector<std::vector<uint8_t>> srcs(static_cast<size_t>(nt));
+  std::vector<void *> dsts(static_cast<size_t>(nt));
+  for (int t = 0; t < nt; ++t) {
+    srcs[static_cast<size_t>(t)].assign(c.src.begin(), c.src.end());
+    fake_register_host(srcs[static_cast<size_t>(t)].data(), c.src.size());
+    dsts[static_cast<size_t>(t)] = device_buffer(out, 0xA5);
+  }
+  arm();
+  std::vector<std::vector<Call>> calls(static_cast<size_t>(nt));
+  std::vector<int64_t> bad(static_cast<size_t>(nt), 0), seen(static_cast<size_t>(nt), 0);
+  std::vector<std::thread> pool;
+  std::vector<int> done(static_cast<size_t>(nt), -1);
+  const int start = fake_host_handoff(); // the threads follow the set-up
+  for (int t = 0; t < nt; ++t)
+    pool.emplace_back([&, t] {
+      const size_t i = static_cast<size_t>(t);
+      fake_host_adopt(start);
+      std::vector<uint8_t> host(out);
+      for (int k = 0; k < repeat; ++k) {
+        relx_options opt = options_of(o);
+        relx_err e{};
+        const int rc = relx_execute_h2d(ctxs[i], c.bound, srcs[i].data(), c.src.size(), dsts[i], out,
+                                        &opt, nullptr, &e);
+        calls[i].push_back(call_of(rc, e));
+        if (rc != RELX_OK)
+          continue;
+        fake_host_read(dsts[i], out, "a thread reads its result");
+        (void)hipMemcpy(host.data(), dsts[i], out, hipMemcpyDeviceToHost);
+        ++seen[i];
+        if (!c.want.empty() && std::memcmp(host.data(), c.want.data(), out) != 0)
+          ++bad[i];
+      }
+      done[i] = fake_host_handoff();
+    });
+  for (std::thread &th : pool)
+    th.join();
+  for (int token : done) // the main thread follows every thread's work
+    fake_host_adopt(token);
+  for (int t = 0; t < nt; ++t) {
+    const size_t i = static_cast<size_t>(t);
+    r.calls.insert(r.calls.end(), calls[i].begin(), calls[i].end());
+    r.checked += c.want.empty() ? 0 : seen[i];
+    r.mismatches += bad[i];
+    fake_unregister_host(srcs[i].data());
+    (void)hipFree(dsts[i]);
+    if (!shared) {
+      relx_err e{};
+      if (relx_ctx_close(ctxs[i], &e) != RELX_OK)
+        r.notes.push_back(std::string("close: ") + e.code);
+    }
+  }
+}
+
 void run_static(const Case &c, const Opts &o, Result &r, relx_ctx *ctx) {
   const size_t out = static_cast<size_t>(c.info.destination_bytes);
   void *src = nullptr;
@@ -595,6 +666,8 @@ int main() {
           run_device(c, o, r, ctx);
         else if (scenario == "static")
           run_static(c, o, r, ctx);
+        else if (scenario == "threads")
+          run_threads(c, o, r, ctx);
         else
           setup_error = "unknown scenario " + scenario;
         relx_ctx_stats st{};

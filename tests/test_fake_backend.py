@@ -388,3 +388,16 @@ def test_quarantined_context_refuses_calls(driver, cases):
     r = run(driver, ["group %s members=2 chunk=32768 fail_kernel_async_at=1 %s" % (cases["c1"], DELAYS)])[0]
     assert r["calls"][0]["code"] == "completion_unknown" and r["calls"][0]["completion"] == 2
     assert r["quarantined"] == 1
+
+
+@pytest.mark.parametrize("shared", [1, 0])
+def test_threads_upload_at_once(driver, cases, shared):
+    """Host threads upload at once through one context (the library
+    serializes its calls) or one context each, all sharing the bound
+    plans and their device caches; results right, nothing unordered, no
+    data race."""
+    lines = ["threads %s threads_n=4 shared=%d repeat=3 chunk=%d nbuf=2 threads=2 %s"
+             % (cases[n], shared, ch, DELAYS) for n, ch in (("c1", 32768), ("fz2", 16384), ("c2", 8192))]
+    for r in run(driver, lines):
+        ok(r)
+        assert r["checked"] == 12 and len(r["calls"]) == 12
