@@ -20,7 +20,8 @@
 //            waited (`twice=1`: two submissions in flight)
 //   d2h      relx_execute_d2h from a device source written on the caller
 //            stream just before
-//   device   relx_relayout_device on the caller stream after the wire was
+//   device   relx_relayout_device (an indexed plan: relx_index_select_device)
+//            on the caller stream after the wire (table) was
 //            written on it
 //   static   relx_execute_h2d_static from a page-locked source
 //   threads  several host threads uploading at once, through one context
@@ -465,8 +466,12 @@ void run_device(const Case &c, const Opts &o, Result &r, relx_ctx *ctx) {
   for (int i = 0; i < repeat && ok; ++i) {
     caller.produce(wire, c.src.data(), c.src.size());
     relx_err e{};
-    const int rc = relx_relayout_device(ctx, c.bound, static_cast<int>(o.get("hs", 0)), wire, dst,
-                                        reinterpret_cast<uint64_t>(caller.s), &e);
+    // an indexed plan gathers its rows from the device-resident table
+    const int rc = c.info.indexed
+                       ? relx_index_select_device(ctx, c.bound, wire, c.src.size(), dst, out,
+                                                  reinterpret_cast<uint64_t>(caller.s), &e)
+                       : relx_relayout_device(ctx, c.bound, static_cast<int>(o.get("hs", 0)), wire,
+                                              dst, reinterpret_cast<uint64_t>(caller.s), &e);
     r.calls.push_back(call_of(rc, e));
     const hipError_t se = hipStreamSynchronize(caller.s);
     relx_err e2{};

@@ -244,8 +244,12 @@ def test_device_to_host_and_device_resident(driver, cases):
         for caller in ("null", "stream"):
             lines.append("device %s caller=%s %s" % (cases[name], caller, DELAYS))
     lines.append("d2h %s caller=null %s" % (cases["c1"], DELAYS))
-    for r in run(driver, lines):
+    # an indexed plan's rows gathered from a device-resident table
+    lines += ["device %s caller=%s %s" % (cases["ix"], caller, DELAYS) for caller in ("null", "stream")]
+    res = run(driver, lines)
+    for r in res:
         ok(r)
+    assert all(r["checked"] == 2 for r in res)
 
 
 def test_allocation_free_upload(driver, cases):
