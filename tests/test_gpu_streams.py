@@ -188,3 +188,59 @@ def test_index_select_on_the_null_stream(ctx, ballast):
     ctx.index_select_device(b, t.data_ptr(), x.nbytes, out.data_ptr(), want.size, stream=0)
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy(), want.view(np.uint8).reshape(-1))
+
+
+@pytest.mark.parametrize("pinned", [False, True])
+def test_no_wait_calls_back_to_back(ctx, pinned):
+    """Uploads in flight together: each call's copies overwrite the wire
+    arena the call before may still be reading. Different sources into
+    different destinations, one synchronization at the end."""
+    n = 6
+    cases = [c2_case(2, 32, 32 + 16 * i) for i in range(n)]
+    outs = [torch.empty(w.size, dtype=torch.uint8, device="cuda") for _, _, w in cases]
+    torch.cuda.synchronize()
+    srcs = [torch.from_numpy(x.copy()).pin_memory() if pinned else x for x, _, _ in cases]
+    for i, ((x, b, _), out, s) in enumerate(zip(cases, outs, srcs)):
+        say("no_wait burst", i, "pinned" if pinned else "pageable")
+        ptr = s.data_ptr() if pinned else s.ctypes.data
+        ctx.execute_h2d(b, ptr, x.nbytes, out.data_ptr(), out.numel(), no_wait=True,
+                        chunk_bytes=16384, source_pinned=1 if pinned else 0)
+    ctx.synchronize()
+    for (_, _, want), out in zip(cases, outs):
+        assert np.array_equal(out.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("shared", [True, False])
+def test_threads_upload_at_once(shared):
+    """Host threads upload at once through one context (its calls are
+    serialized) or one context each, sharing the bound plan and its device
+    caches; each thread's result equals the oracle's."""
+    import threading
+    x, b, want = c2_case(4, 64, 64)
+    n, rounds = 4, 5
+    ctxs = [P.Context(0)] * n if shared else [P.Context(0) for _ in range(n)]
+    outs = [torch.empty(want.size, dtype=torch.uint8, device="cuda") for _ in range(n)]
+    torch.cuda.synchronize()
+    errors = []
+
+    def work(i):
+        try:
+            for _ in range(rounds):
+                ctxs[i].execute_h2d(b, x.ctypes.data, x.nbytes, outs[i].data_ptr(), outs[i].numel(),
+                                    chunk_bytes=32768, gather_threads=2)
+                got = outs[i].cpu().numpy()
+                if not np.array_equal(got, want):
+                    errors.append((i, int(np.argmax(got != want))))
+        except Exception as e:  # reported by the main thread
+            errors.append((i, repr(e)))
+
+    say("threads", n, "shared" if shared else "one context each")
+    ts = [threading.Thread(target=work, args=(i,)) for i in range(n)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join(timeout=60)
+    assert not any(t.is_alive() for t in ts)
+    for c in set(ctxs):
+        c.close()
+    assert not errors, errors
