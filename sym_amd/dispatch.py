@@ -28,13 +28,110 @@ Names, argument meaning and error codes follow the reference so that
 Requests whose policy asks for a CPU executor ("original_cpu") or a forced
 row this build lacks raise TransferError("implementation_unavailable").
 """
+import math
 import threading
 
 from . import pyreloc as P
 from .pyreloc import TransferError
-from .transfer import BufferView, DispatchResources, context_for  # noqa: F401
+from .transfer import (BufferView, DispatchResources, GatherPool,  # noqa: F401
+                       _gather_threads, context_for)
 
 POLICIES = ("auto", "original_cpu")
+
+
+class Calibration:
+    """A parsed cost-model calibration (reference pyreloc.Calibration,
+    libreloc/python/PyReloc.cpp:658-672; the file format of
+    libreloc/src/CostModel.cpp:29-76). The reference's `auto` policy uses it
+    to choose between CPU and device rows; this build has only device rows,
+    so a calibration is accepted wherever the reference takes one and
+    changes no selection."""
+
+    __slots__ = ("_machine", "_values")
+
+    def __init__(self, machine, values):
+        self._machine = machine
+        self._values = dict(values)
+
+    @property
+    def machine(self):
+        return self._machine
+
+    def value(self, key):
+        """The calibrated figure under `key`, or None."""
+        return self._values.get(key)
+
+    def __repr__(self):
+        return "Calibration(machine=%r, %d values)" % (self._machine, len(self._values))
+
+
+def _strtod(s):
+    """A whole-string C strtod: decimal and hexadecimal floats, inf and nan;
+    NaN for anything else (the caller rejects non-finite values)."""
+    if "_" in s:  # Python's float() takes digit separators, strtod does not
+        return math.nan
+    try:
+        return float(s)
+    except ValueError:
+        pass
+    body = s[1:] if s[:1] in "+-" else s
+    if body[:2] in ("0x", "0X"):
+        try:
+            return float.fromhex(s)
+        except ValueError:
+            pass
+    return math.nan
+
+
+def parse_calibration(text):
+    """Parse a "# costmodel calibration v0" file; ValueError names the
+    offending line, as the reference's CostModel::parse does."""
+    machine, values, saw_version = "", {}, False
+    for line_no, line in enumerate(text.split("\n"), 1):
+        raw = line.strip(" \t\r\n")
+        if not raw:
+            continue
+        if not saw_version:
+            if raw != "# costmodel calibration v0":
+                raise ValueError("calibration: first non-blank line must be the v0 version "
+                                 "header (line %d)" % line_no)
+            saw_version = True
+            continue
+        if raw.startswith("#"):
+            if raw.startswith("# machine:"):
+                machine = raw[len("# machine:"):].strip(" \t\r\n")
+            continue
+        fields = raw.split("#", 1)[0].split()
+        if len(fields) < 2:
+            raise ValueError("calibration: expected 'key value' at line %d" % line_no)
+        if len(fields) > 2:
+            raise ValueError("calibration: trailing junk at line %d" % line_no)
+        key, text_value = fields
+        v = _strtod(text_value)
+        if not math.isfinite(v):
+            raise ValueError("calibration: non-numeric value at line %d" % line_no)
+        if key in values:
+            raise ValueError("calibration: duplicate key '%s' at line %d" % (key, line_no))
+        values[key] = v
+    if not saw_version:
+        raise ValueError("calibration: empty file (no version header)")
+    return Calibration(machine, values)
+
+
+def load_calibration(path):
+    """Load a calibration file (reference pyreloc.load_calibration,
+    libreloc/python/PyReloc.cpp:662-672)."""
+    try:
+        with open(path) as f:
+            text = f.read()
+    except OSError:
+        raise ValueError("calibration: cannot read " + str(path)) from None
+    return parse_calibration(text)
+
+
+def _check_calibration(calibration):
+    if calibration is not None and not isinstance(calibration, Calibration):
+        raise TypeError("calibration must be pyreloc.Calibration or None")
 
 
 def _label(k):
@@ -172,10 +269,33 @@ def prepare_dispatch_template(bound, direction, device="cuda", *, policy="auto",
     and launches nothing (reference prepare_dispatch_template)."""
     if int(threads) < 1:
         raise ValueError("threads must be >= 1")
+    _check_calibration(calibration)
     bound = _unwrap(bound)
     capability = query_capability(bound, direction, device)
     selection = _select(bound, direction, capability, policy, implementation)
     return DispatchTemplate(bound, direction, capability, selection, int(threads))
+
+
+def select_dispatch(bound, direction, device="host", *, policy="auto", calibration=None, threads=8,
+                    implementation=""):
+    """The row the policy picks for this program, direction and device end,
+    without buffers: the row's fields plus 'policy' and 'placement_reason'
+    (reference select_dispatch, libreloc/python/PyDispatch.cpp:438-462,
+    845-864). A bridge fixes the row here and forces it in prepare_dispatch
+    once the destination exists."""
+    if device not in ("host", "cuda"):
+        raise ValueError("device must be 'host' or 'cuda', got '%s'" % device)
+    if int(threads) < 1:
+        raise ValueError("threads must be >= 1")
+    _check_calibration(calibration)
+    bound = _unwrap(bound)
+    capability = query_capability(bound, direction, device)
+    selection = _select(bound, direction, capability, policy, implementation)
+    row = next(r for r in capability["eligible"] if r["implementation"] == selection["implementation"])
+    out = dict(row)
+    out["policy"] = selection["policy"]
+    out["placement_reason"] = selection["placement_reason"]
+    return out
 
 
 def _check_view(bound, view, is_source, direction):
@@ -294,6 +414,7 @@ def execute_dispatch(request, *, caller_stream=None, n_buffers=2, n_streams=2, g
             raise ValueError("n_streams must be >= 1")
         if gather_threads < 0:
             raise ValueError("gather_threads must be >= 0 (0 = all cores)")
+        gather_threads = _gather_threads(gather_threads, gather_pool)
         request.executing = True
         src, dst = request.source, request.destination
         d2h = request.template.direction == "d2h"
@@ -352,6 +473,7 @@ def execute_dispatch_group(group, *, caller_stream=None, gather_threads=1, gathe
         raise TransferError("already_executed", "group is executing or already executed")
     if gather_threads < 1 or not max_scratch_bytes:
         raise ValueError("gather_threads and max_scratch_bytes must be positive")
+    gather_threads = _gather_threads(gather_threads, gather_pool)
     _pinning(pinning)
     group.executing = True
     try:
@@ -444,6 +566,7 @@ def submit_dispatch_group(group, *, caller_stream=None, gather_threads=8, gather
         raise ValueError("owners must be (source owners, destination owners[, extra owners])")
     if gather_threads < 1 or not max_scratch_bytes:
         raise ValueError("gather_threads and max_scratch_bytes must be positive")
+    gather_threads = _gather_threads(gather_threads, gather_pool)
     _pinning(pinning)
     dev = max(0, group.items[0].destination.device)
     ctx = _resources_for(resources, dev)

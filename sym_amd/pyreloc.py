@@ -666,9 +666,9 @@ def measure_d2h(device=0, nbytes=256 << 20, iters=20, rounds=3):
 from .transfer import (BufferView, DispatchResources, TransferRequest,  # noqa: E402,F401
                        TransferResourceCache, cuda_enabled, cuda_pointer_device, execute_transfer,
                        make_transfer, validate_transfer_source)
-from .dispatch import (DispatchCompletion, DispatchRequest,  # noqa: E402,F401
-                       DispatchTemplate, GroupRequest, IndexSelectProgram, Resources,
-                       execute_dispatch, execute_dispatch_group, prepare_dispatch,
-                       prepare_dispatch_from_template, prepare_dispatch_group,
+from .dispatch import (Calibration, DispatchCompletion, DispatchRequest,  # noqa: E402,F401
+                       DispatchTemplate, GatherPool, GroupRequest, IndexSelectProgram, Resources,
+                       execute_dispatch, execute_dispatch_group, load_calibration,
+                       prepare_dispatch, prepare_dispatch_from_template, prepare_dispatch_group,
                        prepare_dispatch_template, prepare_index_select_program, query_capability,
-                       submit_dispatch_group)
+                       select_dispatch, submit_dispatch_group)

@@ -348,6 +348,51 @@ def context_for(resources, device):
 
 # ------------------------------------------------------------ execution
 
+class GatherPool:
+    """A host worker pool handle (reference pyreloc.GatherPool,
+    libreloc/python/PyReloc.cpp:731-760): `threads` 0 means every core.
+    Passed as `gather_pool`, its thread count sets the staging workers of
+    the call (librelx keeps its worker threads inside each context). A
+    closed pool is refused with ValueError, as the reference does."""
+
+    def __init__(self, threads=0):
+        threads = int(threads)
+        if threads < 0:
+            raise ValueError("threads must be >= 0 (0 = all cores)")
+        self._threads = threads or (os.cpu_count() or 1)
+        self._closed = False
+
+    @property
+    def threads(self):
+        return self._threads
+
+    @property
+    def closed(self):
+        return self._closed
+
+    def close(self):
+        """Idempotent."""
+        self._closed = True
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+        return False
+
+
+def _gather_threads(gather_threads, gather_pool):
+    """The staging workers of a call: the pool's count when one is given."""
+    if gather_pool is None:
+        return gather_threads
+    if not isinstance(gather_pool, GatherPool):
+        raise TypeError("gather_pool must be pyreloc.GatherPool or None")
+    if gather_pool.closed:
+        raise ValueError("gather_pool is closed")
+    return gather_pool.threads
+
+
 def execute_transfer(request, *, caller_stream=None, n_buffers=4, n_streams=2, gather_threads=1,
                      gather_pool=None, resources=None, owners=None, pinning="auto",
                      min_pinned_bytes=None):
@@ -368,6 +413,7 @@ def execute_transfer(request, *, caller_stream=None, n_buffers=4, n_streams=2, g
             raise ValueError("n_streams must be >= 1")
         if gather_threads < 0:
             raise ValueError("gather_threads must be >= 0 (0 = all cores)")
+        gather_threads = _gather_threads(gather_threads, gather_pool)
         if pinning not in ("auto", "pinned", "pageable"):
             raise ValueError("pinning must be auto, pinned or pageable")
         if resources is not None or owners is not None:

@@ -16,6 +16,12 @@ def goldens():
         return json.load(f)
 
 
+def path(*parts):
+    """A fixture file under tests/golden (e.g. the reference's calibration
+    files in tests/golden/calibration)."""
+    return os.path.join(HERE, *parts)
+
+
 def typed_fixtures():
     out = []
     for jf in sorted(glob.glob(os.path.join(CORPUS, "typed", "*.json"))):

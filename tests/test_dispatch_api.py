@@ -131,3 +131,139 @@ def test_group_preparation():
     assert len(g.items) == 3 and not g.consumed
     with pytest.raises(P.TransferError):
         P.prepare_dispatch_group([])
+
+
+# ------------------------------------------------- calibration, pools, selection
+
+CAL = """# costmodel calibration v0
+# machine: testbox
+pcie.h2d_gbps 10
+cpu.t8.contiguous.contig_read_gbps 20
+hbm.bw_gbps 100
+overhead.a_ms 0.5  # a trailing comment
+"""
+
+
+def test_calibration_files_load(tmp_path):
+    """The reference's calibration format (libreloc/src/CostModel.cpp:29-76):
+    its test file, its two committed machine files (tests/golden/calibration,
+    copied from calibration/), and the parser's diagnostics."""
+    p = tmp_path / "test.cal"
+    p.write_text(CAL)
+    cal = P.load_calibration(str(p))
+    assert cal.machine == "testbox" and cal.value("overhead.a_ms") == 0.5
+    gen3 = P.load_calibration(G.path("calibration", "epyc7351-2080ti.cal"))
+    gen4 = P.load_calibration(G.path("calibration", "7800x3d-4070tis.cal"))
+    assert (gen3.machine, gen4.machine) == ("epyc7351-2080ti", "7800x3d-4070tis")
+    assert gen3.value("pcie.h2d_gbps") == 13.07
+    bad = {"no header\n": "first non-blank line must be the v0 version header (line 1)",
+           "": "empty file",
+           "# costmodel calibration v0\nkey\n": "expected 'key value' at line 2",
+           "# costmodel calibration v0\n\nk 1 2\n": "trailing junk at line 3",
+           "# costmodel calibration v0\nk one\n": "non-numeric value at line 2",
+           "# costmodel calibration v0\nk inf\n": "non-numeric value at line 2",
+           "# costmodel calibration v0\nk 1_0\n": "non-numeric value at line 2",
+           "# costmodel calibration v0\nk 1\nk 2\n": "duplicate key 'k' at line 3"}
+    for text, msg in bad.items():
+        p.write_text(text)
+        with pytest.raises(ValueError, match=msg.replace("(", r"\(").replace(")", r"\)")):
+            P.load_calibration(str(p))
+    p.write_text("# costmodel calibration v0\nk 0x10\n")
+    assert P.load_calibration(str(p)).value("k") == 16.0  # strtod reads hex floats
+    with pytest.raises(ValueError, match="cannot read"):
+        P.load_calibration(str(tmp_path / "missing.cal"))
+
+
+def test_calibration_is_accepted_and_changes_no_row(tmp_path):
+    p = tmp_path / "test.cal"
+    p.write_text(CAL)
+    cal = P.load_calibration(str(p))
+    b = c2_bound()
+    t = P.prepare_dispatch_template(b, "h2d", "cuda", calibration=cal)
+    assert t.selection == P.prepare_dispatch_template(b, "h2d", "cuda").selection
+    with pytest.raises(TypeError):
+        P.prepare_dispatch_template(b, "h2d", "cuda", calibration="gen3")
+
+
+def test_select_dispatch_rows():
+    """select_dispatch (PyDispatch.cpp:438-462): the selected row's fields
+    plus policy and placement reason, without buffers."""
+    b = c2_bound()
+    s = P.select_dispatch(b, "h2d", "cuda", threads=8)
+    assert s["implementation"] == "hip_relayout@1" and s["wire_boundary"] == 1
+    assert s["policy"] == "auto" and s["placement_reason"] == "device_relayout"
+    f = P.select_dispatch(b, "h2d", "cuda", implementation="hip_relayout")
+    assert f["wire_boundary"] == 0 and f["placement_reason"] == "forced"
+    assert P.select_dispatch(b, "d2h", "cuda")["implementation"] == "hip_relayout"
+    with pytest.raises(P.TransferError) as e:
+        P.select_dispatch(b, "h2d")  # the host device end: no CPU rows here
+    assert e.value.code == "implementation_unavailable"
+    with pytest.raises(ValueError):
+        P.select_dispatch(b, "h2d", "gpu")
+    with pytest.raises(ValueError):
+        P.select_dispatch(b, "h2d", "cuda", threads=0)
+
+
+def test_gather_pool_handle():
+    pool = P.GatherPool(3)
+    assert pool.threads == 3 and not pool.closed
+    assert P.GatherPool().threads >= 1  # 0: every core
+    with pytest.raises(ValueError):
+        P.GatherPool(-1)
+    with pool:
+        pass
+    assert pool.closed
+    pool.close()  # idempotent
+    b = c2_bound()
+    x = np.zeros((2, 3, 224, 224), np.float32)
+    req = P.prepare_dispatch(b, host_view(x), fake_device_view([2, 224, 224, 4], 2), "h2d")
+    with pytest.raises(ValueError, match="gather_pool is closed"):
+        P.execute_dispatch(req, gather_pool=pool)
+    with pytest.raises(TypeError):
+        P.execute_dispatch(req, gather_pool=4)
+    assert not req.consumed and not req.executing
+
+
+# How the in-scope callers call pyreloc: reloc_torch's dispatch, transport,
+# group, resources and index_select modules and the WeightFetcher workload
+# (libreloc/python/examples/workloads/common.py), as (positional arguments,
+# keyword names) per name, read from their call sites.
+CALLER_SURFACE = {
+    "BufferView": (0, ["base", "capacity_bytes", "device", "element_size", "extents", "kind",
+                       "offset_bytes", "strides"]),
+    "DispatchResources": (0, ["acquire_timeout_ms", "max_background_workers", "max_contexts",
+                              "max_contexts_per_device", "max_live_bytes", "max_retained_bytes",
+                              "max_streams"]),
+    "TransferResourceCache": (0, ["acquire_timeout_ms", "max_background_workers", "max_contexts",
+                                  "max_contexts_per_device", "max_live_staging_bytes",
+                                  "max_retained_bytes"]),
+    "bind_indexed": (3, []), "bind_typed": (3, []), "cuda_pointer_device": (1, []),
+    "execute_dispatch": (1, ["caller_stream", "chunk_size", "direct_dense_upload", "gather_pool",
+                             "gather_threads", "min_pinned_bytes", "n_buffers", "n_streams",
+                             "owners", "pinning", "pipeline", "resources"]),
+    "execute_transfer": (1, ["caller_stream", "gather_pool", "gather_threads", "min_pinned_bytes",
+                             "n_buffers", "n_streams", "owners", "pinning", "resources"]),
+    "load_calibration": (1, []), "make_transfer": (4, []),
+    "prepare_dispatch": (4, ["calibration", "implementation", "policy", "threads"]),
+    "prepare_dispatch_from_template": (3, []), "prepare_dispatch_group": (1, []),
+    "prepare_dispatch_template": (3, ["calibration", "implementation", "policy", "threads"]),
+    "prepare_index_select_program": (2, []), "query_capability": (3, []),
+    "select_dispatch": (3, ["threads"]), "validate_transfer_source": (3, []),
+    "execute_dispatch_group": (1, []), "submit_dispatch_group": (1, []),
+    "GatherPool": (1, []), "Calibration": None, "BindError": None, "DecodeError": None,
+    "TransferError": None, "cuda_enabled": None,
+}
+
+
+@pytest.mark.parametrize("name", sorted(CALLER_SURFACE))
+def test_callers_find_every_name_they_use(name):
+    import inspect
+    assert hasattr(P, name), name
+    shape = CALLER_SURFACE[name]
+    if shape is None:
+        return
+    n, kws = shape
+    obj = getattr(P, name)
+    sig = inspect.signature(obj.__init__ if inspect.isclass(obj) else obj)
+    args = [None] * (n + (1 if inspect.isclass(obj) else 0))  # self
+    sig.bind_partial(*args, **{k: None for k in kws})
