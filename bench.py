@@ -13,10 +13,12 @@ written.
 * `value`: output bytes x steps / wall time of the K steps.
 * `pcie`: the same steps in wire bytes against the measured pinned H2D
   ceiling, plus the pinned-source (direct DMA) rate.
-* `roofline`: the dominant kernel, the per-chunk k_permute launch inside the
-  timed steps, timed by event pairs on the copy stream it runs on;
-  algorithmic bytes per launch over its mean duration, against 8 TB/s.
-  `traffic` comes from the committed rocprofv3 PMC summary.
+* `roofline`: the dominant kernel, k_permute over one kernel batch of the
+  upload (8 batch entries), run back to back on one stream with an event
+  pair per launch; algorithmic bytes per launch over its mean duration,
+  against 8 TB/s. `in_pipeline` times the same launches inside the timed
+  steps. `traffic` comes from the committed rocprofv3 PMC summary
+  (profiles/traffic.json; PMC counters need a profiler run of their own).
 * `cpu_baseline`: the reference's own cpu_reference row (oracle/_ref: CPU
   transform into a 2-slot pinned ring, then H2D) on the same batch and host.
 
@@ -63,6 +65,9 @@ def parse():
                     help="per-call copy/kernel/staging timeline of a rocprofv3 marker + memory-copy "
                          "+ kernel trace of the headline (RELX_TRACE=1), or of a --trace-configs run "
                          "(its output line saved as TRACE_DIR/plan.json)")
+    ap.add_argument("--summarize-stats", metavar="TRACE_DIR",
+                    help="per-config kernel durations from a rocprofv3 --kernel-trace run of "
+                         "--traffic-probe (its output line saved as TRACE_DIR/probe.json)")
     ap.add_argument("--trace-configs", metavar="CONFIGS",
                     help="end-to-end uploads of these configs only, pageable then pinned (8 warm-up "
                          "calls and 6 timed calls each), for a rocprofv3 trace; prints the call plan")
@@ -644,6 +649,40 @@ def summarize_trace(d):
     print("\n".join(lines))
 
 
+def _kernel_pattern(info):
+    """The kernel names a probed config launches: the gather instance it
+    names, or its family at its element widths (the one-level interleave,
+    k_interleave1p, included)."""
+    import re
+    if info.get("pattern"):
+        return re.compile(re.escape(info["pattern"]))
+    return re.compile(r"k_%s(1p)?<%d, %d" % (info["family"], info["win"], info["wout"]))
+
+
+def summarize_stats(d, probe):
+    """Per-config kernel durations from a rocprofv3 --kernel-trace run of
+    --traffic-probe (its output line saved as d/probe.json): each config's
+    dispatches (matched by kernel name as in summarize_pmc), their mean and
+    median duration, and the algorithmic bytes over the mean as a fraction
+    of 8 TB/s. Prints a markdown table."""
+    rows = [(r["Kernel_Name"], (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+            for r in _csv_rows(d, "kernel_trace.csv")]
+    lines = ["| config | kernel | dispatches | mean us | median us | algorithmic bytes | "
+             "achieved GB/s | of 8 TB/s |", "|---|---|---:|---:|---:|---:|---:|---:|"]
+    for name, info in probe["kernels"].items():
+        pat = _kernel_pattern(info)
+        us = [t for k, t in rows if pat.search(k)]
+        if not us:
+            continue
+        kernel = next(k for k, _ in rows if pat.search(k)).replace("void relx::(anonymous namespace)::", "")
+        mean = float(np.mean(us))
+        alg = info["algorithmic_bytes"]
+        lines.append("| %s | `%s` | %d | %.2f | %.2f | %d | %.1f | %.3f |" % (
+            name, kernel.split("(")[0], len(us), mean, float(np.median(us)), alg, alg / mean / 1e3,
+            alg / mean / 1e3 / HBM_PEAK_GBS))
+    print("\n".join(lines))
+
+
 def summarize_pmc(fetch_dir, write_dir, probe):
     """Scale each kernel's FETCH_SIZE / WRITE_SIZE by what the counters read
     for the calibration copy and write profiles/traffic.json."""
@@ -657,11 +696,11 @@ def summarize_pmc(fetch_dir, write_dir, probe):
         factor = probe["calibration_bytes"] / float(np.median(cal))
         out[counter + "_calibration_factor"] = round(factor, 4)
         for name, info in probe["kernels"].items():
-            pat = info.get("pattern") or "k_%s<%d, %d" % (info["family"], info["win"], info["wout"])
-            vals = [v for k, v in rows if pat in k]
+            pat = _kernel_pattern(info)
+            vals = [v for k, v in rows if pat.search(k)]
             if vals:
                 med.setdefault(name, {})[counter] = float(np.median(vals)) * factor
-                med[name]["kernel"] = next(k for k, v in rows if pat in k)
+                med[name]["kernel"] = next(k for k, v in rows if pat.search(k))
                 med[name]["dispatches"] = len(vals)
     for name, m in med.items():
         if "FETCH_SIZE" in m and "WRITE_SIZE" in m:
@@ -979,6 +1018,10 @@ def headline(torch, P, args, h2d_ceiling):
 
 def main():
     args = parse()
+    if args.summarize_stats:
+        with open(os.path.join(args.summarize_stats, "probe.json")) as f:
+            summarize_stats(args.summarize_stats, json.loads(f.read().strip().splitlines()[-1]))
+        return
     if args.summarize_trace:
         plan_path = os.path.join(args.summarize_trace, "plan.json")
         if os.path.exists(plan_path):
