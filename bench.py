@@ -461,9 +461,11 @@ def traffic_probe(torch, ctx, names):
             out = torch.empty(x.size, dtype=torch.int8, device="cuda")
             for _ in range(3):
                 rep = ctx.execute_h2d(bound, x.ctypes.data, x.nbytes, out.data_ptr(), x.size)
+            # the typical launch (the median dispatch): a full batch of
+            # `units` batch entries (the last chunk is a launch of its own)
+            units = max(1, min((256 << 20) // (HEADLINE_S * 4096 * 2), HEADLINE_B // 4))
             kernels[name] = {"family": "permute", "win": 2, "wout": 1, "output_bytes": x.size,
-                             "algorithmic_bytes": (x.nbytes + x.size) // rep["kernel_launches"]
-                                                  + sc.nbytes,
+                             "algorithmic_bytes": units * HEADLINE_S * 4096 * 3 + sc.nbytes,
                              "launches_per_call": rep["kernel_launches"]}
             del out, x
             continue
@@ -924,17 +926,22 @@ def headline(torch, P, args, h2d_ceiling):
     p50, p95 = float(np.percentile(ts, 50)), float(np.percentile(ts, 95))
 
     # The dominant kernel: k_permute, one launch per kernel batch of the
-    # upload (whole batch entries). Its launches inside the steps are timed
-    # by event pairs on their copy stream, which also count the wait from
-    # the batch's last copy to the kernel's start; the roofline takes the
-    # same launch, the same box over B' = B / launches entries, back to back
-    # on one stream with an event pair per launch.
+    # upload. A batch takes whole batch entries (the chunks) up to 256 MiB of
+    # wire, at most a quarter of the call, and the last chunk is a batch of
+    # its own. The roofline takes the full batch's launch, the same box over
+    # B' entries, back to back on one stream with an event pair per launch.
+    # The launches inside the steps are timed by event pairs on their copy
+    # stream, which also count the wait from the batch's last copy to the
+    # kernel's start.
+    units = max(1, min((256 << 20) // (S * 4096 * 2), B // 4))
     launches_per_call = kt["launches"] // max(1, kt["calls"])
-    units = B // max(1, launches_per_call)
-    assert units * launches_per_call == B, (B, launches_per_call)
-    pipeline_ms = kt["ms"] / max(1, kt["chunks"])
+    expected = -(-(B - 1) // units) + 1 if units > 1 else B
+    assert launches_per_call == expected, (B, units, launches_per_call)
     unit_bytes = S * 4096 * 3  # one batch entry: 2 B of f16 read + 1 B of int8 written per element
     alg_per_launch = units * unit_bytes + sc.nbytes
+    # in the steps: every launch's bytes over every launch's time
+    pipeline_bytes = kt["calls"] * (B * unit_bytes + launches_per_call * sc.nbytes)
+    pipeline_gbs = pipeline_bytes / (kt["ms"] * 1e-3) / 1e9
     ub = P.bind_typed(plan, {"B": units, "S": S}, params)
     _, kernel_ms = device_rate(torch, res, ub, 2 * units * S * 4096, units * S * 4096,
                                max(100, 4 * args.steps), 10)
@@ -1005,8 +1012,9 @@ def headline(torch, P, args, h2d_ceiling):
                      "algorithmic_bytes_per_launch": alg_per_launch,
                      "algorithmic_bytes_per_unit": unit_bytes, "units_per_launch": units,
                      "in_pipeline": {"launches_timed": kt["launches"],
-                                     "ms_per_launch_events": round(pipeline_ms, 5),
-                                     "achieved": round(alg_per_launch / (pipeline_ms * 1e-3) / 1e9, 1)},
+                                     "launches_per_call": launches_per_call,
+                                     "kernel_ms_per_call_events": round(kt["ms"] / max(1, kt["calls"]), 4),
+                                     "achieved": round(pipeline_gbs, 1)},
                      "copy_ceiling": {"GBps": round(copy_gbs, 1), "bytes": alg_per_launch,
                                       "kernel": "16-byte vector copy of the same bytes",
                                       "frac": round(achieved / copy_gbs, 4)}},

@@ -1077,7 +1077,7 @@ KernelBatches kernel_batches(const ChunkPlan &p) {
   const int64_t chunks = (p.units + p.per_chunk - 1) / p.per_chunk;
   int64_t n = kKernelBatchBytes / std::max<int64_t>(1, p.per_chunk * p.unit_wire);
   n = std::max<int64_t>(1, std::min(n, chunks / 4));
-  return {p.units, n * p.per_chunk};
+  return {p.units, n * p.per_chunk, n > 1 ? (chunks - 1) * p.per_chunk : p.units};
 }
 
 int64_t verify_launches(BoundHandle &h, uint32_t k, int64_t chunk_bytes) {

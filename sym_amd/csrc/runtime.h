@@ -122,12 +122,19 @@ ChunkPlan chunk_plan(const DeviceProgram &dp, uint32_t src_width, int64_t chunk_
 // chunks until it holds kKernelBatchBytes of wire. A member keeps at least
 // four batches, so that the last one, which runs after the last copy,
 // stays short.
+// The last chunk is a batch of its own when batches take several chunks:
+// its kernel is what runs after the last copy lands.
 constexpr int64_t kKernelBatchBytes = int64_t{256} << 20;
 struct KernelBatches {
   int64_t units, per; // chunk-axis units, units per batch (whole chunks)
-  int64_t end(int64_t k0) const { return std::min(units, k0 + per); }
+  int64_t last;       // first unit of the last chunk when it is a batch of its own, else units
+  int64_t end(int64_t k0) const {
+    const int64_t e = std::min(units, k0 + per);
+    return k0 < last && e > last ? last : e;
+  }
 };
 KernelBatches kernel_batches(const ChunkPlan &p);
+
 
 // Host staging transform: source elements [e0, e1) at boundary 0 -> wire
 // elements at boundary `k` (leading per-tensor stages applied elementwise).

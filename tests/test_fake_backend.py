@@ -108,6 +108,11 @@ def cases(tmp_path_factory):
     blob = W.c1_plan().blob
     want = O.execute_layout(O.bind(O.decode_plan(blob), {"s0": n}), x.tobytes())
     c["c1"] = write_case(root, "c1", blob, x, want, {"s0": n})
+    # C1 at 16 MiB: chunks of several MiB
+    n = 1 << 22
+    x = W.c1_input(n)
+    want = O.execute_layout(O.bind(O.decode_plan(blob), {"s0": n}), x.tobytes())
+    c["c1big"] = write_case(root, "c1big", blob, x, want, {"s0": n})
     # C2 (typed, one per-tensor cast): the host applies it at boundary 1
     shape = (2, 3, 32, 48)
     x = W.c2_input(*shape)
@@ -171,6 +176,20 @@ def test_upload_orders_and_results(driver, cases):
         assert r["checked"] == 2
     chunked = [r for r in res if "chunk=16384" in lines[res.index(r)]]
     assert max(r["report"]["chunks"] for r in chunked) >= 8
+
+
+def test_large_chunks_and_the_last_batch(driver, cases):
+    """16 MiB of source in chunks of 2 to 16 MiB: kernel batches of several
+    chunks, the last chunk a batch of its own."""
+    lines = ["h2d %s pinned=%d chunk=%d nbuf=2 threads=4 repeat=2 %s" % (cases["c1big"], pinned, ch, DELAYS)
+             for pinned in (0, 1) for ch in (16 << 20, 2 << 20)]
+    res = run(driver, lines)
+    for r in res:
+        ok(r)
+        assert r["checked"] == 2
+    # 8 chunks of 2 MiB: batches of two chunks up to the last, which is
+    # alone: [0,2) [2,4) [4,6) [6,7) [7,8)
+    assert [r["report"]["kernel_launches"] for r in res] == [1, 5, 1, 5]
 
 
 def test_host_stages_and_device_stages(driver, cases):
