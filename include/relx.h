@@ -182,7 +182,17 @@ int relx_bound_query(const relx_bound *bound, relx_bound_info *out);
  * CudaBackend (libreloc/cuda/CudaBackend.cu:55-282) and the retained
  * ScratchBackend of dispatch::Resources
  * (libreloc/src/DispatchResources.cpp:44,552-686). `max_retained_bytes`
- * bounds pinned + device scratch kept between calls (0 = unbounded). */
+ * bounds the scratch kept between calls, pinned ring plus device wire arena,
+ * as the reference's maxRetainedBytes does
+ * (libreloc/include/reloc/DispatchResources.h:57-61): once a blocking call,
+ * or relx_ctx_synchronize, finds every call on the context completed, the
+ * ring and the arena are released, the larger first, until what is kept
+ * fits; the next call that needs them allocates them again. 0 keeps none;
+ * a negative value sets no bound. Submitted and no_wait calls keep their
+ * scratch until such a point. The parameter tables of the plans run on the
+ * context are kept apart from this bound, by content (at most 4096 tables
+ * or 16 MiB; a fresh binding of the same plan and parameters uploads
+ * nothing), until the context is closed. */
 int relx_ctx_create(int device, int64_t max_retained_bytes, relx_ctx **out, relx_err *err);
 
 /* Drain and free. A context whose completion is unknown is quarantined (its
@@ -457,7 +467,8 @@ int relx_verify_launches(const relx_bound *bound, int wire_boundary, int64_t chu
 /* Block until every call on the context has completed: its own streams, and
  * the device-resident launches that report a status (see
  * relx_relayout_device). Fails with "channel_out_of_range" when one of those
- * launches selected a channel outside its parameters. */
+ * launches selected a channel outside its parameters. Then releases scratch
+ * beyond the context's max_retained_bytes. */
 int relx_ctx_synchronize(relx_ctx *ctx, relx_err *err);
 
 /* Kernel timing of a context's blocking uploads (relx_execute_h2d and

@@ -397,7 +397,8 @@ int relx_ctx_close(relx_ctx *ctx, relx_err *err) {
 int relx_ctx_stats_get(const relx_ctx *ctx, relx_ctx_stats *out) {
   if (!ctx || !out)
     return RELX_ERROR;
-  const relx::Context &c = *ctx->ctx;
+  relx::Context &c = *ctx->ctx;
+  std::lock_guard<std::mutex> g(c.mu);
   out->pinned_bytes = static_cast<int64_t>(c.slots.size() * c.slot_bytes);
   out->device_bytes = static_cast<int64_t>(c.wire_cap);
   out->calls = c.calls;
@@ -806,6 +807,8 @@ int relx_ctx_synchronize(relx_ctx *ctx, relx_err *err) {
     if (!relx::drain(*ctx->ctx))
       throw relx::Error("backend_failure", "stream synchronize failed");
     relx::resolve_checks(*ctx->ctx);
+    ctx->ctx->unsynced = false; // every call on the context has completed
+    relx::trim_retained(*ctx->ctx);
   });
 }
 

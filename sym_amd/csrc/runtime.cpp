@@ -280,6 +280,77 @@ void ensure_wire(Context &ctx, size_t bytes) {
   ctx.wire_cap = cap;
 }
 
+// The device copy of program k's parameter tables: the context's copy of
+// these contents when it holds one, else a new entry when the cache has room,
+// else the handle's own copy. Call with ctx.mu held and ctx.device current.
+BoundHandle::DevParams context_params(Context &ctx, BoundHandle &h, uint32_t k) {
+  const DeviceProgram &dp = h.program(k);
+  const size_t fb = dp.pf.size() * sizeof(float), ib = dp.pi.size() * sizeof(int32_t);
+  std::string key(sizeof(fb), '\0'); // the float bytes' length, then both tables
+  std::memcpy(&key[0], &fb, sizeof(fb));
+  key.append(reinterpret_cast<const char *>(dp.pf.data()), fb);
+  key.append(reinterpret_cast<const char *>(dp.pi.data()), ib);
+  auto it = ctx.param_cache.find(key);
+  if (it != ctx.param_cache.end())
+    return it->second;
+  const size_t ioff = (fb + 255) / 256 * 256, bytes = ioff + ib;
+  if (ctx.param_cache.size() >= kParamCacheEntries ||
+      bytes > kParamCacheBytes - std::min(kParamCacheBytes, ctx.param_cache_bytes))
+    return h.device_params(ctx.device, k);
+  std::vector<uint8_t> host(bytes, 0);
+  std::memcpy(host.data(), dp.pf.data(), fb);
+  std::memcpy(host.data() + ioff, dp.pi.data(), ib);
+  void *d = nullptr;
+  HIPCHECK(hipMalloc(&d, bytes));
+  const hipError_t e = hipMemcpy(d, host.data(), bytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(d);
+    HIPCHECK(e);
+  }
+  BoundHandle::DevParams par{static_cast<float *>(d),
+                             reinterpret_cast<int32_t *>(static_cast<uint8_t *>(d) + ioff)};
+  ctx.param_cache.emplace(std::move(key), par);
+  ctx.param_cache_bytes += bytes;
+  return par;
+}
+
+} // namespace
+
+// Scratch kept between calls is bounded by ctx.max_retained (negative: no
+// bound): once every call on the context has completed, the staging ring and
+// the wire arena are released, the larger first, until what is kept fits.
+// The next call that needs them allocates them again (reference
+// dispatch::Resources: oversize scratch is released after completion,
+// libreloc/include/reloc/DispatchResources.h:57-61,
+// libreloc/src/DispatchResources.cpp:120-128,225).
+void trim_retained(Context &ctx) {
+  if (ctx.max_retained < 0 || ctx.unsynced)
+    return;
+  const size_t limit = static_cast<size_t>(ctx.max_retained);
+  for (;;) {
+    const size_t ring = ctx.slots.size() * ctx.slot_bytes;
+    if (ring + ctx.wire_cap <= limit)
+      return;
+    if (ring >= ctx.wire_cap) {
+      for (hipEvent_t e : ctx.slot_ev)
+        HIPCHECK(hipEventSynchronize(e));
+      for (void *s : ctx.slots)
+        HIPCHECK(hipHostFree(s));
+      for (hipEvent_t e : ctx.slot_ev)
+        HIPCHECK(hipEventDestroy(e));
+      ctx.slots.clear();
+      ctx.slot_ev.clear();
+      ctx.slot_bytes = 0;
+    } else {
+      HIPCHECK(hipFree(ctx.wire));
+      ctx.wire = nullptr;
+      ctx.wire_cap = 0;
+    }
+  }
+}
+
+namespace {
+
 void ensure_ring(Context &ctx, int n, size_t slot_bytes) {
   if (static_cast<int>(ctx.slots.size()) >= n && ctx.slot_bytes >= slot_bytes)
     return;
@@ -578,7 +649,7 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
     const DeviceProgram &dp = *m.dp;
     const ChunkPlan &p = plans[mi];
     const BoundHandle::DevParams par =
-        sc ? BoundHandle::DevParams{sc->pf, sc->pi} : m.h->device_params(ctx.device, m.k);
+        sc ? BoundHandle::DevParams{sc->pf, sc->pi} : context_params(ctx, *m.h, m.k);
     const uint32_t sw = m.h->bound->typed ? m.h->bound->source_type.width()
                                           : m.h->bound->layout.element_size;
     uint8_t *wire = (sc ? sc->wire : ctx.wire) + m.wire_off;
@@ -724,6 +795,8 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
   }
   HIPCHECK(hipEventSynchronize(ctx.done_ev));
   ctx.unsynced = false;
+  if (!sc)
+    trim_retained(ctx);
   if (timing) {
     for (size_t i = 0; i < tpairs; ++i) {
       float ms = 0.0f;
@@ -852,7 +925,7 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
   int32_t *status = ctx.status + (ctx.status_next++ % kStatusSlots);
   if (dp.family == kFamGeneric)
     clear_status(status);
-  const BoundHandle::DevParams par = h.device_params(ctx.device, 0);
+  const BoundHandle::DevParams par = context_params(ctx, h, 0);
   uint8_t *result = ctx.wire;
   uint8_t *out = static_cast<uint8_t *>(dst);
   struct Pending {
@@ -919,6 +992,7 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
     HIPCHECK(hipStreamWaitEvent(caller, ctx.done_ev, 0));
   HIPCHECK(hipEventSynchronize(ctx.done_ev));
   ctx.unsynced = false;
+  trim_retained(ctx);
   if (dp.family == kFamGeneric) {
     if (read_status(status))
       throw Error("channel_out_of_range", "a stage selected a channel outside its parameters");
@@ -1028,6 +1102,10 @@ void destroy_context(Context &ctx) {
   if (ctx.param_stage)
     (void)hipHostFree(ctx.param_stage);
   ctx.param_stage = nullptr;
+  for (auto &kv : ctx.param_cache)
+    (void)hipFree(kv.second.pf);
+  ctx.param_cache.clear();
+  ctx.param_cache_bytes = 0;
   if (ctx.wire)
     (void)hipFree(ctx.wire);
   ctx.wire = nullptr;
@@ -1190,7 +1268,7 @@ void relayout_device(Context &ctx, BoundHandle &h, uint32_t k, const void *wire,
                      hipStream_t stream) {
   DeviceGuard guard(ctx.device);
   const DeviceProgram &dp = h.program(k);
-  const BoundHandle::DevParams par = h.device_params(ctx.device, k);
+  const BoundHandle::DevParams par = context_params(ctx, h, k);
   if (dp.family != kFamGeneric) {
     // Fast families have their channels proven in range when the program is
     // built; their edge boxes (element-wise) get the sink flag, never read.

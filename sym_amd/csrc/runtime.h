@@ -300,9 +300,19 @@ struct Context {
   // parameter tables it uploads (kScratchParamBytes, allocated here).
   uint8_t *scratch = nullptr;
   uint8_t *param_stage = nullptr;
+  // Parameter tables by content: a fresh binding of a plan with the same
+  // tables (the same plan and parameters, bound again for the next call)
+  // finds them here and uploads nothing. Each entry is one device block
+  // (floats, then ints at a 256-byte offset), written once and freed with
+  // the context; past kParamCacheEntries or kParamCacheBytes a bound handle
+  // keeps its own copy instead.
+  std::map<std::string, BoundHandle::DevParams> param_cache;
+  size_t param_cache_bytes = 0;
   std::unique_ptr<Workers> workers;
   unsigned worker_threads = 0;
-  int64_t max_retained = 0;
+  // Scratch kept between calls (ring + wire arena), in bytes; negative: no
+  // bound. Checked once a blocking call has completed.
+  int64_t max_retained = -1;
   std::mutex mu;
   int64_t calls = 0, failures = 0;
   // The last call returned before its work completed (a submitted group or
@@ -326,6 +336,14 @@ constexpr size_t kParamStageHalf = kScratchParamBytes / 2;
 // The device address of `device`'s copy of the scratch, found once per
 // device with hipGetSymbolAddress; call with `device` current.
 uint8_t *scratch_address(int device);
+
+// Bounds of Context::param_cache.
+constexpr size_t kParamCacheEntries = 4096;
+constexpr size_t kParamCacheBytes = size_t{16} << 20;
+
+// Release ring and wire arena until what the context keeps fits its
+// max_retained; a no-op while a call may still be running.
+void trim_retained(Context &ctx);
 
 constexpr uint32_t kStatusSlots = 1024;
 constexpr uint32_t kDeviceChecks = 64; // size of Context::check_ev

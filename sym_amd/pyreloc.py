@@ -437,13 +437,17 @@ def _options(n_buffers=0, chunk_bytes=0, host_stages=-1, gather_threads=0, sourc
 class Context:
     """A retained per-device execution context (streams, pinned ring, device
     wire scratch): the role of the reference's TransferResources /
-    dispatch::Resources owners."""
+    dispatch::Resources owners. `max_retained_bytes` bounds the ring and
+    wire arena kept once the context's calls have completed (None: no
+    bound; 0 keeps none)."""
 
-    def __init__(self, device=0, max_retained_bytes=0):
+    def __init__(self, device=0, max_retained_bytes=None):
+        if max_retained_bytes is not None and int(max_retained_bytes) < 0:
+            raise ValueError("max_retained_bytes must be >= 0")
+        limit = -1 if max_retained_bytes is None else min(int(max_retained_bytes), (1 << 63) - 1)
         err = N.relx_err()
         h = ctypes.c_void_p()
-        if N.lib().relx_ctx_create(int(device), int(max_retained_bytes), ctypes.byref(h),
-                                   ctypes.byref(err)):
+        if N.lib().relx_ctx_create(int(device), limit, ctypes.byref(h), ctypes.byref(err)):
             _raise(err)
         self._h = h
         self.device = device

@@ -191,6 +191,17 @@ def cuda_pointer_device(pointer):
 
 # ------------------------------------------------------------ resources
 
+def _check_limit(name, v):
+    """A resource limit is a non-negative integer that fits 64 bits, as the
+    reference's size_t/unsigned arguments (test_transfer_resources.py:87-94)."""
+    if isinstance(v, bool) or not isinstance(v, int):
+        raise TypeError("%s must be an integer" % name)
+    if v < 0:
+        raise ValueError("%s must be >= 0" % name)
+    if v >= 1 << 64:
+        raise OverflowError("%s does not fit 64 bits" % name)
+
+
 class _ContextCache:
     """Retained per-device contexts created on first use: the role of the
     reference's TransferResourceCache and dispatch::Resources owners
@@ -199,8 +210,14 @@ class _ContextCache:
     contexts, `close()` all of them. Construction touches no GPU."""
 
     def __init__(self, max_retained_bytes, limits):
-        self._max_retained = int(max_retained_bytes)
-        self._limits = dict(limits, retained_bytes=int(max_retained_bytes))
+        # None: no bound (the module's own contexts)
+        if max_retained_bytes is not None:
+            _check_limit("max_retained_bytes", max_retained_bytes)
+        for name, v in limits.items():
+            if v is not None:
+                _check_limit(name, v)
+        self._max_retained = max_retained_bytes
+        self._limits = dict(limits, retained_bytes=self._max_retained)
         self._pid = os.getpid()
         self._lock = threading.Lock()
         self._contexts = {}
@@ -329,7 +346,7 @@ def default_resources():
     global _default_cache
     with _default_lock:
         if _default_cache is None:
-            _default_cache = _ContextCache(0, {})
+            _default_cache = _ContextCache(None, {})
         return _default_cache
 
 

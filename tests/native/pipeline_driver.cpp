@@ -36,6 +36,7 @@
 #include <fstream>
 #include <iostream>
 #include <map>
+#include <memory>
 #include <sstream>
 #include <string>
 #include <thread>
@@ -78,7 +79,26 @@ struct Case {
   std::string src, want;
   std::string error; // load or bind failure
   std::vector<std::string> keep; // parameter and index bytes
+  // what the bound was made from, for a fresh binding per call (layout and
+  // typed plans)
+  std::vector<std::string> sym_names, param_names;
+  std::vector<int64_t> sym_values;
+  std::vector<relx_param> params;
+  bool indexed = false;
 };
+
+// A new binding of the case's plan with its symbols and parameters.
+relx_bound *bind_again(const Case &c) {
+  std::vector<const char *> np;
+  for (const std::string &n : c.sym_names)
+    np.push_back(n.c_str());
+  relx_bound *b = nullptr;
+  relx_err err{};
+  if (relx_bind(c.plan, np.data(), c.sym_values.data(), static_cast<int>(np.size()), c.params.data(),
+                static_cast<int>(c.params.size()), &b, &err) != RELX_OK)
+    return nullptr;
+  return b;
+}
 
 bool load_case(const std::string &dir, Case &c) {
   c.dir = dir;
@@ -146,6 +166,11 @@ bool load_case(const std::string &dir, Case &c) {
     return false;
   }
   relx_bound_query(c.bound, &c.info);
+  c.sym_names = std::move(names);
+  c.sym_values = std::move(values);
+  c.param_names = std::move(pnames); // the params' name pointers move with the buffer
+  c.params = std::move(params);
+  c.indexed = indexed;
   c.src = read_file(dir + "/src.bin");
   if (file_exists(dir + "/want.bin"))
     c.want = read_file(dir + "/want.bin");
@@ -175,6 +200,7 @@ struct Result {
   int64_t mismatches = 0, checked = 0;
   std::vector<std::string> notes;
   int quarantined = 0;
+  int64_t pinned_bytes = 0, device_bytes = 0; // the context's scratch after the scenario
   Call close{RELX_OK, "", "", 0};
   relx_report report{};
 };
@@ -287,13 +313,25 @@ void run_h2d(const Case &c, const Opts &o, Result &r, relx_ctx *ctx) {
   // may still be reading and writing; one synchronization at the end
   const bool burst = nowait && o.get("burst", 0) != 0;
   bool failed = false;
+  // rebind: every call runs a fresh binding of the plan, freed after the call
+  const bool rebind = o.get("rebind", 0) != 0 && !c.indexed;
+  std::unique_ptr<relx_bound, void (*)(relx_bound *)> fresh(nullptr, relx_bound_free);
   for (int i = 0; i < repeat && !failed; ++i) {
     relx_options opt = options_of(o);
     caller.apply(opt);
     if (!burst || i == 0)
       caller.produce(dst, poison.data(), out); // an earlier writer of the destination
+    relx_bound *bound = c.bound;
+    if (rebind) {
+      fresh.reset(bind_again(c));
+      if (!fresh) {
+        r.notes.push_back("rebind failed");
+        return;
+      }
+      bound = fresh.get();
+    }
     relx_err e{};
-    const int rc = relx_execute_h2d(ctx, c.bound, src, c.src.size(), dst, out, &opt, &r.report, &e);
+    const int rc = relx_execute_h2d(ctx, bound, src, c.src.size(), dst, out, &opt, &r.report, &e);
     r.calls.push_back(call_of(rc, e));
     if (rc != RELX_OK) {
       relx_ctx_stats st{};
@@ -502,7 +540,7 @@ void run_threads(const Case &c, const Opts &o, Result &r, relx_ctx *ctx) {
   std::vector<relx_ctx *> ctxs(static_cast<size_t>(nt), ctx);
   for (int t = 0; t < nt && !shared; ++t) {
     relx_err e{};
-    if (relx_ctx_create(0, 0, &ctxs[static_cast<size_t>(t)], &e) != RELX_OK) {
+    if (relx_ctx_create(0, o.get("retained", -1), &ctxs[static_cast<size_t>(t)], &e) != RELX_OK) {
       r.notes.push_back(std::string("context: ") + e.code);
       return;
     }
@@ -655,7 +693,8 @@ int main() {
         fake_configure(&pre);
       }
       relx_err e{};
-      const int rc = relx_ctx_create(static_cast<int>(o.get("device", 0)), 0, &ctx, &e);
+      const int rc =
+          relx_ctx_create(static_cast<int>(o.get("device", 0)), o.get("retained", -1), &ctx, &e);
       create = call_of(rc, e);
       g_armed = k; // the scenario arms the knobs once its buffers exist
       if (rc == RELX_OK) {
@@ -678,6 +717,8 @@ int main() {
         relx_ctx_stats st{};
         relx_ctx_stats_get(ctx, &st);
         r.quarantined = st.quarantined;
+        r.pinned_bytes = st.pinned_bytes;
+        r.device_bytes = st.device_bytes;
         if (o.get("close", 1)) {
           relx_err e2{};
           r.close = call_of(relx_ctx_close(ctx, &e2), e2);
@@ -692,6 +733,7 @@ int main() {
     for (size_t i = 0; i < r.calls.size(); ++i)
       js << (i ? "," : "") << call_json(r.calls[i]);
     js << "],\"close\":" << call_json(r.close) << ",\"quarantined\":" << r.quarantined
+       << ",\"pinned_bytes\":" << r.pinned_bytes << ",\"device_bytes\":" << r.device_bytes
        << ",\"checked\":" << r.checked << ",\"mismatches\":" << r.mismatches << ",\"notes\":[";
     for (size_t i = 0; i < r.notes.size(); ++i)
       js << (i ? "," : "") << jstr(r.notes[i]);
@@ -703,7 +745,9 @@ int main() {
        << ",\"kernel_launches\":" << r.report.kernel_launches << ",\"direct_dma\":" << r.report.direct_dma
        << ",\"wire_boundary\":" << r.report.wire_boundary << "},\"counts\":{\"copies\":" << counts.copies
        << ",\"launches\":" << counts.launches << ",\"syncs\":" << counts.syncs
-       << ",\"unemulated\":" << counts.unemulated << "}}";
+       << ",\"unemulated\":" << counts.unemulated << ",\"mallocs\":" << counts.mallocs
+       << ",\"host_mallocs\":" << counts.host_mallocs << ",\"frees\":" << counts.frees
+       << ",\"host_frees\":" << counts.host_frees << "}}";
     std::cout << js.str() << std::endl;
     fake_configure(nullptr);
     fake_reset();

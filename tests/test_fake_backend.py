@@ -19,6 +19,9 @@ libreloc/test/TransferTestSupport.h:83-164):
     submitted groups in flight together, device-to-host, device-resident
     relayouts, the allocation-free upload; results equal the oracle's and
     no access is unordered, with delays and jitter on every operation;
+  * resources: parameter tables found by content across fresh bindings,
+    and the ring and wire arena released down to max_retained_bytes once
+    the context's calls have completed;
   * faults: allocation failures, copies, launches, event records and
     stream waits refused when submitted, copies and kernels that fault on
     their stream (a sticky device error), a synchronize that fails, and a
@@ -275,6 +278,43 @@ def test_allocation_free_upload(driver, cases):
     lines = ["static %s %s" % (cases["c1"], DELAYS), "static %s %s" % (cases["fz2"], DELAYS)]
     for r in run(driver, lines):
         ok(r)
+
+
+def test_parameter_tables_uploaded_once_per_context(driver, cases):
+    """A fresh binding per call finds its parameter tables in the context:
+    the calls allocate the wire arena and one table block, however many
+    bindings run (each binding's own pair of tables would be two more per
+    call)."""
+    for name in ("c5", "c1"):
+        res = run(driver, ["h2d %s check=0 repeat=4 rebind=%d %s" % (cases[name], rb, DELAYS)
+                           for rb in (0, 1)])
+        for r in res:
+            ok(r)
+            assert r["counts"]["mallocs"] == 2, r["counts"]
+        assert res[0]["counts"] == res[1]["counts"]
+
+
+def test_retained_scratch_bound(driver, cases):
+    """max_retained_bytes: after each blocking call the ring (3 slots of
+    1 MiB) and then the wire arena (2 MiB) are released until what is kept
+    fits; the next call allocates them again. A negative bound keeps both
+    (reference DispatchResources.h:57-61)."""
+    base = "h2d %s repeat=3 chunk=65536 nbuf=3 %s" % (cases["c1"], DELAYS)
+    res = run(driver, [base + " retained=%d" % lim for lim in (-1, 0, 2 << 20, 5 << 20)])
+    for r in res:
+        ok(r)
+        assert r["checked"] == 3
+    kept = [(r["pinned_bytes"], r["device_bytes"]) for r in res]
+    assert kept == [(3 << 20, 2 << 20), (0, 0), (0, 2 << 20), (3 << 20, 2 << 20)]
+    # device blocks: wire arena per call when it is released, plus the table block
+    assert [r["counts"]["mallocs"] for r in res] == [2, 4, 2, 2]
+    assert [r["counts"]["host_mallocs"] for r in res] == [3, 9, 9, 3]
+    # a no_wait call keeps its scratch until the synchronize that completes it
+    r = run(driver, ["h2d %s nowait=1 repeat=2 chunk=65536 nbuf=3 retained=0 %s"
+                     % (cases["c1"], DELAYS)])[0]
+    ok(r)
+    assert (r["pinned_bytes"], r["device_bytes"]) == (0, 0)
+    assert r["counts"]["mallocs"] == 3, r["counts"]
 
 
 def test_checker_reports_a_missing_wait(driver, cases):

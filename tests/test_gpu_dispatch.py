@@ -94,6 +94,60 @@ def test_template_reuse_over_many_views(resources, rng):
         assert rep["implementation"] == "hip_relayout@1"  # pageable source: the cast is staged
 
 
+def _c5_want(x, s):
+    inv = (np.float32(1) / s).astype(np.float32)
+    wid = np.ascontiguousarray(x.transpose(0, 2, 1, 3)).astype(np.float32)
+    return O.quantize_f32_s8(wid, inv[None, :, None, None])
+
+
+def test_fresh_bindings_find_their_own_parameters(resources, rng):
+    """Each call binds C5 afresh (the headline step's pattern), alternating
+    three scale tables and a binding kept from the first call: the context
+    keeps parameter tables by content, so every call must still quantize
+    with its own scales (oracle, bit-exact)."""
+    B, S = 2, 256
+    plan = P.load_typed_plan(W.c5_plan().blob)
+    x, _ = W.c5_input(B, S, seed=5)
+    scales = [rng.uniform(0.02, 0.05, 32).astype(np.float32) for _ in range(3)]
+    kept = P.bind_typed(plan, {"B": B, "S": S}, W.param("scale", scales[0]))
+    for i, k in enumerate([0, 1, 2, 1, 0, 2, -1, 2]):
+        bound = kept if k < 0 else P.bind_typed(plan, {"B": B, "S": S}, W.param("scale", scales[k]))
+        s = scales[0] if k < 0 else scales[k]
+        out = torch.empty((B, 32, S, 128), dtype=torch.int8, device="cuda")
+        say("fresh binding", i, "scales", k)
+        req = P.prepare_dispatch(bound, host_view(x), device_view(out), "h2d")
+        P.execute_dispatch(req, caller_stream=torch.cuda.current_stream().cuda_stream,
+                           resources=resources)
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), _c5_want(x, s)), (i, k)
+
+
+@pytest.mark.parametrize("limit", [0, 3 << 20])
+def test_retained_scratch_is_bounded(rng, limit):
+    """max_retained_bytes of a resource cache: after each call the ring and
+    the wire arena are released until what is kept fits, and the next call
+    allocates them again with the same results."""
+    B, S = 2, 1024  # 16 MiB of f16 source, 8 MiB of int8 output
+    plan = P.load_typed_plan(W.c5_plan().blob)
+    x, s = W.c5_input(B, S, seed=6)
+    want = _c5_want(x, s)
+    cache = P.DispatchResources(max_retained_bytes=limit)
+    try:
+        for i in range(3):
+            out = torch.empty((B, 32, S, 128), dtype=torch.int8, device="cuda")
+            say("retained limit", limit, "call", i)
+            b = P.bind_typed(plan, {"B": B, "S": S}, W.param("scale", s))
+            P.execute_dispatch(P.prepare_dispatch(b, host_view(x), device_view(out), "h2d"),
+                               caller_stream=torch.cuda.current_stream().cuda_stream,
+                               resources=cache, chunk_size=1 << 20)
+            torch.cuda.synchronize()
+            assert np.array_equal(out.cpu().numpy(), want), i
+            st = cache.stats()
+            assert st["retained_bytes"] <= limit, st
+    finally:
+        cache.close()
+
+
 def test_group_dispatch_c4_like(resources, rng):
     rows, cols = 512, 256
     plan = P.Plan(W.c4_plan().blob)

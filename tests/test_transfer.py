@@ -250,6 +250,32 @@ def test_resource_caches_touch_no_gpu_until_used():
     assert d.closed
 
 
+@pytest.mark.parametrize("options", [
+    {"max_contexts": -1}, {"max_retained_bytes": -1}, {"max_contexts_per_device": -1},
+    {"max_background_workers": -1}, {"max_live_staging_bytes": -1},
+    {"acquire_timeout_ms": -1}, {"max_contexts": 1.5}, {"max_contexts": 2**100},
+])
+def test_resource_limits_reject_invalid_values(options):
+    """The reference's invalid-limit cases
+    (libreloc/python/tests/test_transfer_resources.py:87-94)."""
+    with pytest.raises((TypeError, ValueError, OverflowError)):
+        P.TransferResourceCache(**options)
+
+
+@pytest.mark.parametrize("options", [{"max_retained_bytes": -1}, {"max_live_bytes": -2},
+                                     {"max_streams": 0.5}, {"acquire_timeout_ms": -1}])
+def test_dispatch_resource_limits_reject_invalid_values(options):
+    with pytest.raises((TypeError, ValueError, OverflowError)):
+        P.DispatchResources(**options)
+
+
+def test_resource_limits_accept_zero_and_none():
+    assert P.TransferResourceCache(max_retained_bytes=0, max_live_staging_bytes=None,
+                                   acquire_timeout_ms=None).stats()["limits"]["retained_bytes"] == 0
+    assert P.DispatchResources(max_retained_bytes=0, acquire_timeout_ms=5).stats()["limits"][
+        "acquire_timeout_ms"] == 5
+
+
 def test_resource_caches_refuse_pickling_and_foreign_processes():
     c = P.TransferResourceCache()
     with pytest.raises(TypeError):
