@@ -1005,7 +1005,7 @@ def headline(torch, P, args, h2d_ceiling):
                                    "implementation": prep_rep["implementation"]}},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "k_permute<2, 1, 6> (f16 -> f32 -> int8, [B,S,32,128] -> [B,32,S,128])",
+                     "kernel": "k_permute<2, 1, 6, true> (f16 -> f32 -> int8, [B,S,32,128] -> [B,32,S,128], cached stores)",
                      "launch": "one kernel batch of the upload: %d batch entries [%d,%d,32,128]"
                                % (units, units, S),
                      "kernel_ms_per_launch_events": round(kernel_ms, 5),

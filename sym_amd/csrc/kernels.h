@@ -872,13 +872,15 @@ __global__ __launch_bounds__(kBlock) void k_interleave1p(const uint8_t *src, int
 // run), applies the stages on the way into LDS, which it fills in
 // destination order [c][t][e], then writes C contiguous runs of T*E
 // elements. Reads are whole source rows, writes whole destination runs.
-template <int WIN, int WOUT, int CH>
+// CACHED_ST: the runs are stored through the caches instead of streaming
+// (permute_cached_stores).
+template <int WIN, int WOUT, int CH, bool CACHED_ST>
 __global__ __launch_bounds__(kBlock) void k_permute(KArgs a) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int VI = 16 / WIN, BO = VI * WOUT;
   constexpr int U = 4; // source vectors in flight per thread
   constexpr bool NTL = RELX_NT_LOAD(kFamPermute, WIN, WOUT, 1);
-  constexpr bool NTS = RELX_NT_STORE(kFamPermute, WIN, WOUT, 1);
+  constexpr bool NTS = !CACHED_ST && RELX_NT_STORE(kFamPermute, WIN, WOUT, 1);
   asm volatile("" ::"s"(a.src), "s"(a.dst), "s"(a.work), "s"(a.sbase), "s"(a.dbase), "s"(a.p_t),
                "s"(a.p_lds), "s"(a.p_dsc));
   hot(a.p_tiles);
@@ -1033,10 +1035,30 @@ hipError_t interleave_cp(const KArgs &a, hipStream_t s) {
   }
 }
 
+#ifndef RELX_PERMUTE_CACHED_STORES
+#define RELX_PERMUTE_CACHED_STORES 1
+#endif
+// A permute launch stores its runs through the caches when it writes at most
+// 128 MiB into planes (destination runs of one c) 512 KiB or more apart, and
+// streams them otherwise. Measured on the MI355X over 23 C5 shapes, kernel
+// time with cached against streaming stores: 2.7-7.9% faster with planes of
+// 512 KiB and more up to 128 MiB of result (8x4096, the headline upload's
+// kernel batch: 70.8 -> 65.2 us), within 1.6% either way for shorter planes
+// at 128 MiB, and 1.6-5.6% slower past 128 MiB or for shorter planes below.
+inline bool permute_cached_stores(const KArgs &a, int wout) {
+  return RELX_PERMUTE_CACHED_STORES &&
+         static_cast<int64_t>(a.work) * a.p_lds <= (int64_t{128} << 20) &&
+         a.p_dsc * wout >= (int64_t{512} << 10);
+}
+
 template <int WIN, int WOUT, int CH>
 hipError_t permute_launch(const KArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL((k_permute<WIN, WOUT, CH>), dim3(static_cast<unsigned>(a.work)),
-                     dim3(kBlock), a.p_lds, s, a);
+  if (permute_cached_stores(a, WOUT))
+    hipLaunchKernelGGL((k_permute<WIN, WOUT, CH, true>), dim3(static_cast<unsigned>(a.work)),
+                       dim3(kBlock), a.p_lds, s, a);
+  else
+    hipLaunchKernelGGL((k_permute<WIN, WOUT, CH, false>), dim3(static_cast<unsigned>(a.work)),
+                       dim3(kBlock), a.p_lds, s, a);
   return hipGetLastError();
 }
 
