@@ -225,6 +225,9 @@ struct DeviceGuard {
   }
 };
 
+#ifndef RELX_ZERO_COPY_BYTES
+#define RELX_ZERO_COPY_BYTES (1 << 20)
+#endif
 constexpr int kChunkEvents = 32; // device-to-host kernel events, reused round robin
 
 // A call's status flag, which the element-wise kernels set (pinned host
@@ -340,6 +343,7 @@ void trim_retained(Context &ctx) {
         HIPCHECK(hipEventDestroy(e));
       ctx.slots.clear();
       ctx.slot_ev.clear();
+      ctx.slot_pending.clear();
       ctx.slot_bytes = 0;
     } else {
       HIPCHECK(hipFree(ctx.wire));
@@ -375,6 +379,47 @@ void ensure_ring(Context &ctx, int n, size_t slot_bytes) {
     HIPCHECK(hipEventRecord(e, ctx.copies[0])); // a recorded, completed state
     ctx.slot_ev.push_back(e);
   }
+  ctx.slot_pending.assign(ctx.slots.size(), false);
+}
+
+// The host writes a staging slot only after the device work that last read
+// it: the slot's event is waited for when one was recorded since the slot
+// was last known idle.
+void slot_acquire(Context &ctx, int slot) {
+  const size_t i = static_cast<size_t>(slot);
+  if (ctx.slot_pending[i]) {
+    HIPCHECK(hipEventSynchronize(ctx.slot_ev[i]));
+    ctx.slot_pending[i] = false;
+  }
+}
+
+// Once the work that reads the slot is enqueued on `s`. `track` is false for
+// a blocking call that stages no more chunks than the ring has slots: its
+// final synchronization proves every read of the slot done before the host
+// can write it again, so no event is recorded (two runtime calls fewer per
+// chunk, about 4 us of a small call).
+void slot_release(Context &ctx, int slot, hipStream_t s, bool track) {
+  if (!track)
+    return;
+  const size_t i = static_cast<size_t>(slot);
+  HIPCHECK(hipEventRecord(ctx.slot_ev[i], s));
+  ctx.slot_pending[i] = true;
+}
+
+// A call from another thread than the previous call's, after that call
+// completed: it synchronizes with the previous call's end (done_ev, already
+// complete) before it writes any staging slot, so that its host writes are
+// ordered after every device read of the earlier calls through the runtime,
+// not only through the context's lock. Calls from one thread are ordered by
+// program order; after a call that returned early the slots' events order
+// them.
+void order_after_previous_thread(Context &ctx) {
+  const std::thread::id self = std::this_thread::get_id();
+  if (ctx.last_thread == self)
+    return;
+  if (ctx.last_thread != std::thread::id() && !ctx.unsynced)
+    HIPCHECK(hipEventSynchronize(ctx.done_ev));
+  ctx.last_thread = self;
 }
 
 bool probe_pinned(const void *p) {
@@ -421,6 +466,7 @@ struct Member {
   size_t wire_off;
   bool table; // indexed: the table crosses PCIe and the device gathers the rows
   int64_t arena_bytes; // wire arena bytes of this member
+  bool zero_copy = false; // one small chunk: the kernels read its ring slot
 };
 
 // The device memory an allocation-free call uses in place of the context's
@@ -557,6 +603,7 @@ void execute_static(Context &ctx, BoundHandle &h, const void *src, size_t src_by
 
 void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
              relx_report *total, Completion *comp, const StaticScratch *sc) {
+  order_after_previous_thread(ctx); // before any host access to the ring or the arena
   size_t wire_total = 0;
   for (const Member &m : ms)
     wire_total = std::max(wire_total, m.wire_off + static_cast<size_t>(m.arena_bytes));
@@ -571,7 +618,7 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
   // byte ranges of the table, multiples of 256 bytes).
   size_t max_slot = 0;
   std::vector<ChunkPlan> plans;
-  for (const Member &m : ms) {
+  for (Member &m : ms) {
     const DeviceProgram &dp = *m.dp;
     ChunkPlan p{};
     if (m.table) {
@@ -583,6 +630,13 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
       p.unit_wire = p.unit_src = 1;
     } else {
       p = chunk_plan(dp, source_width(*m.h->bound), opt.chunk_bytes, m.direct);
+      // A staged wire of at most RELX_ZERO_COPY_BYTES that crosses as one
+      // chunk: the kernels read its ring slot over PCIe, with no copy ahead
+      // of them. Kernels read only the library's own page-locked memory,
+      // never the caller's (a pinned source keeps its direct copy, which
+      // measured faster than staging it for a zero-copy read).
+      m.zero_copy = !sc && !m.direct && p.units <= p.per_chunk &&
+                    dp.wire_bytes <= static_cast<int64_t>(RELX_ZERO_COPY_BYTES);
     }
     if (!m.direct)
       max_slot = std::max(max_slot, static_cast<size_t>(p.per_chunk * p.unit_wire));
@@ -597,6 +651,14 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
     throw Error("invalid_options", "an allocation-free call has no staging ring");
   if (max_slot)
     ensure_ring(ctx, nslots, max_slot);
+  // Slot events are needed by a call that returns before its work completes
+  // and by one that reuses a slot within itself.
+  int64_t staged = 0;
+  for (size_t i = 0; i < ms.size(); ++i)
+    if (!ms[i].direct)
+      staged += (plans[i].units + plans[i].per_chunk - 1) / plans[i].per_chunk;
+  const bool track_slots =
+      comp != nullptr || opt.no_wait != 0 || staged > static_cast<int64_t>(ctx.slots.size());
   const unsigned threads = opt.gather_threads > 0 ? static_cast<unsigned>(opt.gather_threads) : 8u;
   if (!sc && (!ctx.workers || ctx.worker_threads != threads)) {
     ctx.workers = std::make_unique<Workers>(threads);
@@ -668,13 +730,13 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
                                   hipMemcpyHostToDevice, cs));
         } else {
           uint8_t *s = static_cast<uint8_t *>(ctx.slots[static_cast<size_t>(slot)]);
-          HIPCHECK(hipEventSynchronize(ctx.slot_ev[static_cast<size_t>(slot)]));
+          slot_acquire(ctx, slot);
           const uint8_t *from = m.src + b0;
           ctx.workers->parallel_for(n, int64_t{1} << 18, [&](int64_t x, int64_t y) {
             std::memcpy(s + x, from + x, static_cast<size_t>(y - x));
           });
           HIPCHECK(hipMemcpyAsync(wire + b0, s, static_cast<size_t>(n), hipMemcpyHostToDevice, cs));
-          HIPCHECK(hipEventRecord(ctx.slot_ev[static_cast<size_t>(slot)], cs));
+          slot_release(ctx, slot, cs, track_slots);
           slot = (slot + 1) % static_cast<int>(ctx.slots.size());
         }
         ++chunks;
@@ -685,12 +747,14 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
                                      m.dst_bytes, cs);
     }
     const KernelBatches kb = kernel_batches(p);
+    int zc_slot = -1; // the ring slot a zero-copy member's kernels read
     int64_t kb0 = 0; // first unit of the kernel batch being gathered
     for (int64_t v0 = 0; v0 < (m.table ? 0 : p.units); v0 += p.per_chunk) {
       const int64_t v1 = std::min(p.units, v0 + p.per_chunk);
       const int64_t woff = v0 * p.unit_wire, wbytes = (v1 - v0) * p.unit_wire;
       const int64_t chunk_no = nchunk;
       hipStream_t cs = ctx.copy_stream(nchunk++);
+      const uint8_t *kwire = wire; // what the batch's kernels read
       if (m.direct) {
         TraceRange tr("relx.h2d.submit", chunk_no);
         HIPCHECK(hipMemcpyAsync(wire + woff, m.src + woff, static_cast<size_t>(wbytes),
@@ -699,7 +763,7 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
         uint8_t *s = static_cast<uint8_t *>(ctx.slots[static_cast<size_t>(slot)]);
         {
           TraceRange tr("relx.h2d.slot_wait", chunk_no);
-          HIPCHECK(hipEventSynchronize(ctx.slot_ev[static_cast<size_t>(slot)]));
+          slot_acquire(ctx, slot);
         }
         TraceRange tr("relx.h2d.stage", chunk_no);
         const int64_t e0 = v0 * (p.unit_src / sw), e1 = v1 * (p.unit_src / sw);
@@ -719,9 +783,14 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
             host_transform(prep, k, sw, src_base, s, a, b);
           });
         }
-        HIPCHECK(hipMemcpyAsync(wire + woff, s, static_cast<size_t>(wbytes),
-                                hipMemcpyHostToDevice, cs));
-        HIPCHECK(hipEventRecord(ctx.slot_ev[static_cast<size_t>(slot)], cs));
+        if (m.zero_copy) {
+          kwire = s; // the slot is released after the kernels that read it
+          zc_slot = slot;
+        } else {
+          HIPCHECK(hipMemcpyAsync(wire + woff, s, static_cast<size_t>(wbytes),
+                                  hipMemcpyHostToDevice, cs));
+          slot_release(ctx, slot, cs, track_slots);
+        }
         slot = (slot + 1) % static_cast<int>(ctx.slots.size());
       }
       ++chunks;
@@ -736,8 +805,10 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
       hipEvent_t *tev = timing ? timing_pair(ctx, tpairs++) : nullptr;
       if (tev)
         HIPCHECK(hipEventRecord(tev[0], cs));
-      const int64_t nl = launch_program(dp, kb0, v1, kb0 == 0, v1 == p.units, wire, m.dst,
+      const int64_t nl = launch_program(dp, kb0, v1, kb0 == 0, v1 == p.units, kwire, m.dst,
                                         par.pf, par.pi, status, cs);
+      if (zc_slot >= 0)
+        slot_release(ctx, zc_slot, cs, track_slots);
       if (tev) {
         HIPCHECK(hipEventRecord(tev[1], cs));
         ctx.kt.launches += nl;
@@ -795,6 +866,7 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
   }
   HIPCHECK(hipEventSynchronize(ctx.done_ev));
   ctx.unsynced = false;
+  std::fill(ctx.slot_pending.begin(), ctx.slot_pending.end(), false); // every read is done
   if (!sc)
     trim_retained(ctx);
   if (timing) {
@@ -879,6 +951,7 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
                  size_t dst_bytes, const relx_options &opt, relx_report *report) {
   TraceRange call_range("relx.d2h.call", ctx.calls, "call");
   DeviceGuard guard(ctx.device);
+  order_after_previous_thread(ctx);
   if (h.bound->indexed) // libreloc/src/Dispatch.cpp:196-201: indexed sources are host rows
     throw Error("plan_mismatch", "indexed source requires the prepared host row shape");
   const DeviceProgram &dp = h.program(0);
@@ -992,6 +1065,7 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
     HIPCHECK(hipStreamWaitEvent(caller, ctx.done_ev, 0));
   HIPCHECK(hipEventSynchronize(ctx.done_ev));
   ctx.unsynced = false;
+  std::fill(ctx.slot_pending.begin(), ctx.slot_pending.end(), false);
   trim_retained(ctx);
   if (dp.family == kFamGeneric) {
     if (read_status(status))

@@ -276,6 +276,7 @@ struct Context {
   std::vector<void *> slots;
   size_t slot_bytes = 0;
   std::vector<hipEvent_t> slot_ev;
+  std::vector<bool> slot_pending; // an event was recorded since the slot was last known idle
   std::vector<hipEvent_t> chunk_ev;
   hipEvent_t start_ev = nullptr, done_ev = nullptr;
   hipEvent_t join_ev[kCopyStreams] = {}; // one per copy stream, for joins
@@ -319,6 +320,7 @@ struct Context {
   // no_wait): done_ev marks its end, and the next call that reuses the wire
   // arena orders its streams after it.
   bool unsynced = false;
+  std::thread::id last_thread; // the thread of the previous pipeline call
   bool quarantined = false;
   bool closed = false;
   ~Context(); // frees the status flags (the rest goes in destroy_context)

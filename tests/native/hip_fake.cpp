@@ -204,6 +204,18 @@ bool inside(uintptr_t lo, uintptr_t hi, Mem kind, const char *what) {
   return true;
 }
 
+// A kernel reads device memory, or the library's own page-locked staging (a
+// zero-copy chunk); never page-locked memory of the caller.
+bool kernel_readable(uintptr_t lo, uintptr_t hi, const char *what) {
+  if (hi <= lo)
+    return true;
+  uintptr_t base = 0;
+  const Alloc *a = find_alloc(lo, &base);
+  if (a && a->kind == Mem::Pinned && !a->user && hi <= base + a->bytes)
+    return true;
+  return inside(lo, hi, Mem::Device, what);
+}
+
 int pick_delay(int d) {
   if (d <= 0)
     return 0;
@@ -465,7 +477,7 @@ hipError_t enqueue_kernel(hipStream_t hs, const char *what,
     return hipErrorLaunchFailure;
   bool ok = inside(write.first, write.second, Mem::Device, what);
   for (const auto &r : reads)
-    ok = inside(r.first, r.second, Mem::Device, what) && ok;
+    ok = kernel_readable(r.first, r.second, what) && ok;
   if (!ok)
     return hipErrorInvalidValue;
   const uint64_t seq = stream_step(s);
@@ -773,6 +785,16 @@ hipError_t launch_box(int family, const KArgs &a, int32_t *status, hipStream_t s
   const bool stages = a.chain.n > 0;
   if (stages)
     ++g_counts.unemulated;
+  {
+    // a kernel that reads the library's own page-locked staging (a
+    // zero-copy chunk): the host has just filled it, as for a copy from it
+    const Alloc *al = find_alloc(slo);
+    if (al && al->kind == Mem::Pinned && !al->user) {
+      ++g_counts.zero_copy;
+      HostAgent &h = host_tick();
+      access(slo, shi, true, h.vc, h.id, h.vc[static_cast<size_t>(h.id)], "host staging write");
+    }
+  }
   std::vector<std::pair<uintptr_t, uintptr_t>> reads{{slo, shi}};
   // parameter tables: from the table to the end of its allocation
   for (const void *p : {static_cast<const void *>(a.pf), static_cast<const void *>(a.pi)}) {

@@ -53,6 +53,7 @@ typedef struct fake_counts {
   int64_t mallocs, host_mallocs, copies, launches, records, waits, syncs;
   int64_t frees, host_frees, live_device, live_pinned;
   int64_t unemulated; // kernels whose value stages the stand-in does not run
+  int64_t zero_copy;  // kernels that read the library's page-locked staging
 } fake_counts;
 
 // Set the knobs and reset the call counters they count against.

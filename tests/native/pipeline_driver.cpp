@@ -747,7 +747,7 @@ int main() {
        << ",\"launches\":" << counts.launches << ",\"syncs\":" << counts.syncs
        << ",\"unemulated\":" << counts.unemulated << ",\"mallocs\":" << counts.mallocs
        << ",\"host_mallocs\":" << counts.host_mallocs << ",\"frees\":" << counts.frees
-       << ",\"host_frees\":" << counts.host_frees << "}}";
+       << ",\"host_frees\":" << counts.host_frees << ",\"zero_copy\":" << counts.zero_copy << "}}";
     std::cout << js.str() << std::endl;
     fake_configure(nullptr);
     fake_reset();

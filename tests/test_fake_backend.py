@@ -317,6 +317,27 @@ def test_retained_scratch_bound(driver, cases):
     assert r["counts"]["mallocs"] == 3, r["counts"]
 
 
+def test_small_staged_uploads_read_their_slot(driver, cases):
+    """A staged upload of one chunk of at most 1 MiB of wire: its kernel
+    reads the ring slot (zero-copy), with no copy ahead of it; a pinned
+    source keeps its direct copy, and a chunked upload its copies. Blocking
+    calls back to back, no_wait calls and calls from several threads all
+    reuse the slot in order, with the results of the oracle."""
+    lines = ["h2d %s repeat=3 %s" % (cases["c1"], DELAYS),
+             "h2d %s repeat=3 pinned=1 %s" % (cases["c1"], DELAYS),
+             "h2d %s repeat=3 chunk=65536 nbuf=2 %s" % (cases["c1"], DELAYS),
+             "h2d %s repeat=4 nowait=1 burst=1 %s" % (cases["c1"], DELAYS),
+             "h2d %s repeat=2 %s" % (cases["c2"], DELAYS),
+             "h2d %s repeat=2 %s" % (cases["ix"], DELAYS),
+             "threads %s threads_n=3 repeat=3 shared=1 %s" % (cases["c1"], DELAYS)]
+    res = run(driver, lines)
+    for r in res:
+        ok(r)
+    zc = [r["counts"]["zero_copy"] for r in res]
+    assert zc[:6] == [3, 0, 0, 4, 2, 2], zc
+    assert zc[6] == 9, zc
+
+
 def test_checker_reports_a_missing_wait(driver, cases):
     """The device source is written on the caller's stream, but the call is
     told of no producer stream: the relayout reads it unordered."""
