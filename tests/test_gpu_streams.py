@@ -210,11 +210,36 @@ def test_no_wait_calls_back_to_back(ctx, pinned):
         assert np.array_equal(out.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("no_wait", [False, True])
+def test_small_uploads_read_their_slot(ctx, no_wait):
+    """Uploads of one small chunk from pageable sources: the kernel reads the
+    ring slot in page-locked host memory (zero-copy). Back-to-back calls with
+    different data reuse the three slots; blocking calls record no slot
+    events, no_wait calls do and are synchronized once at the end."""
+    n = 8
+    cases = [c2_case(2, 32, 32 + 16 * i) for i in range(n)]
+    outs = [torch.empty(w.size, dtype=torch.uint8, device="cuda") for _, _, w in cases]
+    torch.cuda.synchronize()
+    for i, ((x, b, want), out) in enumerate(zip(cases, outs)):
+        say("small upload", i, "no_wait" if no_wait else "blocking")
+        rep = ctx.execute_h2d(b, x.ctypes.data, x.nbytes, out.data_ptr(), out.numel(),
+                              no_wait=no_wait, source_pinned=0)
+        assert rep["chunks"] == 1 and not rep["direct_dma"], rep
+        if not no_wait:
+            assert np.array_equal(out.cpu().numpy(), want), i
+    ctx.synchronize()
+    for i, ((_, _, want), out) in enumerate(zip(cases, outs)):
+        assert np.array_equal(out.cpu().numpy(), want), i
+
+
+@pytest.mark.parametrize("chunk", [32768, 0], ids=["chunked", "one_chunk"])
 @pytest.mark.parametrize("shared", [True, False])
-def test_threads_upload_at_once(shared):
+def test_threads_upload_at_once(shared, chunk):
     """Host threads upload at once through one context (its calls are
     serialized) or one context each, sharing the bound plan and its device
-    caches; each thread's result equals the oracle's."""
+    caches; each thread's result equals the oracle's. One chunk: each call's
+    kernel reads its ring slot (zero-copy), calls from different threads
+    taking turns on one context's slots."""
     import threading
     x, b, want = c2_case(4, 64, 64)
     n, rounds = 4, 5
@@ -227,14 +252,14 @@ def test_threads_upload_at_once(shared):
         try:
             for _ in range(rounds):
                 ctxs[i].execute_h2d(b, x.ctypes.data, x.nbytes, outs[i].data_ptr(), outs[i].numel(),
-                                    chunk_bytes=32768, gather_threads=2)
+                                    chunk_bytes=chunk, gather_threads=2)
                 got = outs[i].cpu().numpy()
                 if not np.array_equal(got, want):
                     errors.append((i, int(np.argmax(got != want))))
         except Exception as e:  # reported by the main thread
             errors.append((i, repr(e)))
 
-    say("threads", n, "shared" if shared else "one context each")
+    say("threads", n, "shared" if shared else "one context each", "chunk", chunk)
     ts = [threading.Thread(target=work, args=(i,)) for i in range(n)]
     for t in ts:
         t.start()
