@@ -161,7 +161,7 @@ typedef struct relx_bound_info {
   int64_t result_extents[RELX_MAX_RANK];
   char kernel[32]; /* device kernel family the program runs */
   int host_stages_max;  /* leading per-tensor stages a host may apply */
-  int host_stages_auto; /* of those, the narrowing ones applied for a pageable source */
+  int host_stages_auto; /* of those, the narrowing ones the host applies by default */
   int64_t wire_bytes_at[RELX_MAX_STAGES + 1]; /* H2D wire (source layout) at boundary k */
   /* indexed (v2) plans (reference IndexedBoundPlan, libreloc/include/reloc/Bind.h):
    * the physical source is table_rows rows of row_elements elements;
@@ -218,7 +218,8 @@ typedef struct relx_options {
   int n_buffers;        /* pinned ring slots (default 3) */
   int64_t chunk_bytes;  /* wire bytes per chunk (0 = schedule picks) */
   int host_stages;      /* leading per-tensor cast stages the host applies
-                           while staging (-1 = auto, 0 = none) */
+                           while staging (-1 = auto: the leading narrowing
+                           ones, whatever the source's memory; 0 = none) */
   int gather_threads;   /* host staging threads (0 = default 8) */
   int source_pinned;    /* 1: source is page-locked; DMA it directly.
                            -1: probe; 0: pageable (stage through the ring) */

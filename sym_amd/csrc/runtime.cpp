@@ -510,8 +510,13 @@ void execute_members(Context &ctx, int n, BoundHandle *const *bounds, const void
     const bool pinned = !indexed && (opt.source_pinned > 0 ||
                                      (opt.source_pinned < 0 && probe_pinned(m.src)));
     const uint32_t nst = static_cast<uint32_t>(h->prep.stages.size());
+    // Automatic: the leading narrowing stages, from a pinned source too.
+    // Staging C2 (f32 -> f16) from a pinned source takes 0.22 ms against
+    // 0.36 ms for the direct DMA of the f32 source (32 images; 0.85 against
+    // 1.40 ms for 128): the host casts faster than PCIe moves the bytes it
+    // saves. A source with no such stage is sent by direct DMA.
     if (hs < 0)
-      m.k = pinned ? 0 : auto_host_stages(*h);
+      m.k = auto_host_stages(*h);
     else
       m.k = static_cast<uint32_t>(std::min<int>(hs, static_cast<int>(nst)));
     for (uint32_t j = 0; j < m.k; ++j)

@@ -179,14 +179,21 @@ def test_planar_to_interleaved_with_channel_pad(ctx, shape, lo, hi, dtype, cast)
     assert dev.cpu().numpy().tobytes() == want
 
 
-def test_c2_pinned_source_direct_dma(ctx):
+@pytest.mark.parametrize("host_stages", [-1, 0])
+def test_c2_pinned_source(ctx, host_stages):
+    """Automatic: the f32 -> f16 cast is staged from the pinned source too;
+    with no host stages the f32 source crosses by direct DMA."""
     x = torch.from_numpy(W.c2_input()).pin_memory()
     plan = P.Plan(W.c2_plan().blob)
     b = P.Bound(plan, {})
     out = torch.empty(b.destination_bytes, dtype=torch.uint8, device="cuda")
-    say("c2 pinned direct")
-    rep = ctx.execute_h2d(b, x.data_ptr(), x.numel() * 4, out.data_ptr(), out.numel())
-    assert rep["direct_dma"] == 1 and rep["wire_boundary"] == 0
+    say("c2 pinned, host_stages", host_stages)
+    rep = ctx.execute_h2d(b, x.data_ptr(), x.numel() * 4, out.data_ptr(), out.numel(),
+                          host_stages=host_stages)
+    if host_stages == 0:
+        assert rep["direct_dma"] == 1 and rep["wire_boundary"] == 0
+    else:
+        assert rep["direct_dma"] == 0 and rep["wire_boundary"] == 1
     want = f16_bits(np.pad(x.numpy(), [(0, 0), (0, 1), (0, 0), (0, 0)]).transpose(0, 2, 3, 1))
     assert np.array_equal(out.cpu().numpy().view(np.uint16).reshape(want.shape), want)
 
