@@ -315,6 +315,14 @@ def test_retained_scratch_bound(driver, cases):
     ok(r)
     assert (r["pinned_bytes"], r["device_bytes"]) == (0, 0)
     assert r["counts"]["mallocs"] == 3, r["counts"]
+    # device-to-host calls release their result buffer and ring the same way
+    res = run(driver, ["d2h %s repeat=3 retained=0 pinned=%d %s" % (cases["c1"], p, DELAYS)
+                       for p in (0, 1)])
+    for r in res:
+        ok(r)
+        assert (r["pinned_bytes"], r["device_bytes"]) == (0, 0)
+        assert r["counts"]["mallocs"] == 4, r["counts"]  # a result buffer per call + the tables
+    assert [r["counts"]["host_mallocs"] for r in res] == [9, 0]
 
 
 def test_small_staged_uploads_read_their_slot(driver, cases):
