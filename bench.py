@@ -68,6 +68,9 @@ def parse():
     ap.add_argument("--summarize-stats", metavar="TRACE_DIR",
                     help="per-config kernel durations from a rocprofv3 --kernel-trace run of "
                          "--traffic-probe (its output line saved as TRACE_DIR/probe.json)")
+    ap.add_argument("--summarize-report", metavar="REPORT_FILE",
+                    help="markdown tables (profiles/configs_report.md) from the saved output of "
+                         "--report")
     ap.add_argument("--trace-configs", metavar="CONFIGS",
                     help="end-to-end uploads of these configs only, pageable then pinned (8 warm-up "
                          "calls and 6 timed calls each), for a rocprofv3 trace; prints the call plan")
@@ -1036,8 +1039,57 @@ def headline(torch, P, args, h2d_ceiling):
     }
 
 
+def summarize_report(path):
+    """The per-config tables of profiles/configs_report.md from the saved
+    output of --report: device-resident kernel rates, end-to-end uploads from
+    pageable and pinned sources, downloads, and C1's small-N latencies.
+    Prints markdown."""
+    with open(path) as f:
+        rows = [json.loads(l) for l in f if l.startswith("{")]
+    head = {}
+    for r in rows:
+        if "pinned_h2d_ceiling_GBps" in r and "config" not in r:
+            head.update(r)
+        if "hbm_copy_GBps" in r:
+            head.update(r)
+    vc = head.get("vector_copy_GBps") or {}
+    out = ["Measured pinned H2D ceiling: **%.2f GB/s**; torch 1 GiB device copy: %.1f GB/s%s." % (
+        head["pinned_h2d_ceiling_GBps"], head.get("hbm_copy_GBps", float("nan")),
+        ("; librelx 16-byte vector copy: " + ", ".join("%s %.0f GB/s" % kv for kv in vc.items())) if vc else ""),
+        "", "| config | kernel | device us | achieved GB/s | HBM frac | e2e pageable p50 ms | PCIe frac | "
+        "e2e pinned p50 ms | PCIe frac |", "|---|---|---:|---:|---:|---:|---:|---:|---:|"]
+    cell = lambda d, k: d.get(k, "-") if d else "-"
+    for r in rows:
+        if "device" not in r or r.get("config", "").endswith("_d2h"):
+            continue
+        d, a, b = r["device"], r.get("e2e_pageable"), r.get("e2e_pinned")
+        out.append("| %s | %s | %.2f | %.1f | %.3f | %s | %s | %s | %s |" % (
+            r["config"], r["kernel"], d["ms_per_step"] * 1e3, d["achieved_GBps"], d["hbm_frac"],
+            cell(a, "p50_ms"), cell(a, "pcie_frac"), cell(b, "p50_ms"), cell(b, "pcie_frac")))
+    d2h = [r for r in rows if r.get("config", "").endswith("_d2h")]
+    if d2h:
+        out += ["", "Device -> host (KV eviction: the C5 source resident on the device, the int8 result "
+                "into host memory; PCIe fraction against the measured pinned D2H ceiling, **%.2f GB/s**):"
+                % d2h[0]["pinned_d2h_ceiling_GBps"], "",
+                "| config | pageable p50 ms | GB/s | PCIe frac | pinned p50 ms | GB/s | PCIe frac | chunks |",
+                "|---|---:|---:|---:|---:|---:|---:|---:|"]
+        for r in d2h:
+            a, b = r["pageable"], r["pinned"]
+            out.append("| %s | %s | %s | %s | %s | %s | %s | %s |" % (
+                r["config"], a["p50_ms"], a["effective_GBps"], a["pcie_frac"], b["p50_ms"],
+                b["effective_GBps"], b["pcie_frac"], a["chunks"]))
+    lat = [r for r in rows if "e2e_latency_us_p50" in r]
+    if lat:
+        out += ["", "C1 small N (latency-bound), end-to-end p50 / p95 us: " + ", ".join(
+            "N=%d: %.1f / %.1f" % (r["N"], r["e2e_latency_us_p50"], r["e2e_latency_us_p95"]) for r in lat)]
+    print("\n".join(out))
+
+
 def main():
     args = parse()
+    if args.summarize_report:
+        summarize_report(args.summarize_report)
+        return
     if args.summarize_stats:
         with open(os.path.join(args.summarize_stats, "probe.json")) as f:
             summarize_stats(args.summarize_stats, json.loads(f.read().strip().splitlines()[-1]))
