@@ -421,11 +421,17 @@ def execute_dispatch(request, *, caller_stream=None, n_buffers=2, n_streams=2, g
         device = src.device if d2h else dst.device
         ctx = _resources_for(resources, device)
         run = ctx.execute_d2h if d2h else ctx.execute_h2d
+        # direct_dense_upload=False: a dense pinned source is staged through
+        # the ring instead of sent by direct DMA; pipeline=False: the whole
+        # buffer is staged, then sent as one chunk (reference
+        # TransferOptions, libreloc/include/reloc/Transfer.h:129-134)
+        source_pinned = _pinning(pinning) if direct_dense_upload or d2h else 0
+        chunk = int(chunk_size or 0) if pipeline else 1 << 62
         rep = run(request.template.bound, src.address, src.capacity_bytes - src.offset_bytes,
                   dst.address, dst.capacity_bytes - dst.offset_bytes,
-                  n_buffers=n_buffers, chunk_bytes=int(chunk_size or 0),
+                  n_buffers=n_buffers, chunk_bytes=chunk,
                   host_stages=request.selected["host_stages"],
-                  gather_threads=gather_threads, source_pinned=_pinning(pinning),
+                  gather_threads=gather_threads, source_pinned=source_pinned,
                   caller_stream=caller_stream)
         request.consumed = True
         request.report = _report(rep, request)

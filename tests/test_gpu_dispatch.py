@@ -122,6 +122,35 @@ def test_fresh_bindings_find_their_own_parameters(resources, rng):
         assert np.array_equal(out.cpu().numpy(), _c5_want(x, s)), (i, k)
 
 
+@pytest.mark.parametrize("opts,pipeline_kind,chunks", [
+    ({}, "direct_dma", None),
+    ({"direct_dense_upload": False}, "pinned_ring", None),
+    ({"pipeline": False, "direct_dense_upload": False}, "pinned_ring", 1),
+    ({"pipeline": False}, "direct_dma", 1)])
+def test_dispatch_upload_options(resources, opts, pipeline_kind, chunks):
+    """direct_dense_upload=False stages a dense pinned source through the
+    ring; pipeline=False sends the whole buffer as one chunk (reference
+    TransferOptions, Transfer.h:129-134). Results bit-exact either way."""
+    B, S = 4, 1024
+    plan = P.load_typed_plan(W.c5_plan().blob)
+    x, s = W.c5_input(B, S, seed=9)
+    xp = torch.from_numpy(x).pin_memory()
+    b = P.bind_typed(plan, {"B": B, "S": S}, W.param("scale", s))
+    out = torch.empty((B, 32, S, 128), dtype=torch.int8, device="cuda")
+    view = P.BufferView(xp.data_ptr(), x.nbytes, 0, list(x.shape),
+                        [st // 2 for st in x.strides], 2, "host")
+    say("dispatch options", opts)
+    rep = P.execute_dispatch(P.prepare_dispatch(b, view, device_view(out), "h2d"),
+                             chunk_size=4 << 20, resources=resources, **opts)
+    torch.cuda.synchronize()
+    assert rep["host_pipeline"] == pipeline_kind, rep
+    if chunks is not None:
+        assert rep["host_chunks"] == chunks, rep
+    else:
+        assert rep["host_chunks"] > 1, rep
+    assert np.array_equal(out.cpu().numpy(), _c5_want(x, s))
+
+
 @pytest.mark.parametrize("limit", [0, 3 << 20])
 def test_retained_scratch_is_bounded(rng, limit):
     """max_retained_bytes of a resource cache: after each call the ring and
