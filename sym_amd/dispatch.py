@@ -468,19 +468,42 @@ def prepare_dispatch_group(entries):
     return GroupRequest(items)
 
 
-def execute_dispatch_group(group, *, caller_stream=None, gather_threads=1, gather_pool=None,
-                           pinning="auto", min_pinned_bytes=None, max_scratch_bytes=1 << 62,
-                           resources=None, owners=None, device_layout=False, n_buffers=2,
-                           chunked_members=True):
+def _check_group_scratch(group, max_scratch_bytes):
+    """The group's members hold their wire in the device arena together
+    until the group completes (each 256-byte aligned): a group whose wire
+    exceeds max_scratch_bytes is refused before anything is enqueued, and
+    its requests are spent, as the reference's owner refuses scratch past
+    its live-byte limit (libreloc/src/DispatchResources.cpp:120-137;
+    the group is consumed, libreloc/python/tests/torch_frontend/test_group.py:176-179)."""
+    def wire(r):
+        b, k = _unwrap(r.template.bound), r.selected["host_stages"]
+        return int(b.info.wire_bytes_at[k if k >= 0 else b.info.host_stages_auto])
+
+    need = sum((wire(r) + 255) // 256 * 256 for r in group.items)
+    if need > max_scratch_bytes:
+        group.consumed = True
+        for r in group.items:
+            r.consumed = True
+        raise TransferError("insufficient_capacity",
+                            "typed scratch live-byte limit exceeded: the group's wire takes %d bytes, "
+                            "max_scratch_bytes is %d" % (need, max_scratch_bytes))
+
+
+def execute_dispatch_group(group, *, caller_stream=None, gather_threads=8, gather_pool=None,
+                           pinning="auto", min_pinned_bytes=None, max_scratch_bytes=64 << 20,
+                           resources=None, owners=None, device_layout=False, n_buffers=1,
+                           chunked_members=False):
     """All members through one ring and one barrier; returns the group
     report with per-item reports (reference execute_dispatch_group,
-    libreloc/src/Dispatch.cpp:1833-1981)."""
+    libreloc/src/Dispatch.cpp:1833-1981; defaults of
+    libreloc/python/PyDispatch.cpp:648-655)."""
     if group.executing or group.consumed:
         raise TransferError("already_executed", "group is executing or already executed")
     if gather_threads < 1 or not max_scratch_bytes:
         raise ValueError("gather_threads and max_scratch_bytes must be positive")
     gather_threads = _gather_threads(gather_threads, gather_pool)
     _pinning(pinning)
+    _check_group_scratch(group, max_scratch_bytes)
     group.executing = True
     try:
         dev = max(0, group.items[0].destination.device)
@@ -574,6 +597,7 @@ def submit_dispatch_group(group, *, caller_stream=None, gather_threads=8, gather
         raise ValueError("gather_threads and max_scratch_bytes must be positive")
     gather_threads = _gather_threads(gather_threads, gather_pool)
     _pinning(pinning)
+    _check_group_scratch(group, max_scratch_bytes)
     dev = max(0, group.items[0].destination.device)
     ctx = _resources_for(resources, dev)
     bounds = [r.template.bound for r in group.items]

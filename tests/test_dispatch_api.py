@@ -267,3 +267,25 @@ def test_callers_find_every_name_they_use(name):
     sig = inspect.signature(obj.__init__ if inspect.isclass(obj) else obj)
     args = [None] * (n + (1 if inspect.isclass(obj) else 0))  # self
     sig.bind_partial(*args, **{k: None for k in kws})
+
+
+def test_group_scratch_limit_refused_before_launch():
+    """A group whose wire exceeds max_scratch_bytes is refused before any
+    work (no GPU is touched), and its requests are spent, as the reference's
+    owner refuses scratch past its live-byte limit
+    (libreloc/python/tests/torch_frontend/test_group.py:176-179)."""
+    b = c2_bound()
+    src = np.zeros((2, 3, 224, 224), np.float32)
+    entries = [(b, host_view(src), fake_device_view([2, 224, 224, 4], 2), "h2d") for _ in range(3)]
+    g = P.prepare_dispatch_group(entries)
+    wire = 3 * 2 * 3 * 224 * 224 * 2  # three f16 wires after the staged cast
+    with pytest.raises(P.TransferError, match="live-byte limit") as e:
+        P.execute_dispatch_group(g, max_scratch_bytes=wire // 2)
+    assert e.value.code == "insufficient_capacity"
+    assert g.consumed and all(r.consumed for r in g.items)
+    with pytest.raises(P.TransferError, match="already_executed"):
+        P.execute_dispatch_group(g, max_scratch_bytes=1 << 40)
+    g2 = P.prepare_dispatch_group(entries)
+    with pytest.raises(P.TransferError, match="live-byte limit"):
+        P.submit_dispatch_group(g2, max_scratch_bytes=1000, owners=((), ()))
+    assert g2.consumed
