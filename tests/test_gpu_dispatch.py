@@ -233,12 +233,14 @@ def _c5_expected(x, s):
 
 
 @pytest.mark.parametrize("pinned", [False, True])
-@pytest.mark.parametrize("chunk", [0, 64 << 10])
-def test_c5_kv_evict_device_to_host(resources, pinned, chunk):
+@pytest.mark.parametrize("chunk,S", [(0, 1024), (64 << 10, 1024), (0, 4096)])
+def test_c5_kv_evict_device_to_host(resources, pinned, chunk, S):
     """C5's quantizing permute in the other direction (KV eviction): a device
     f16 [B,S,32,128] tensor to a host int8 [B,32,S,128] buffer, chunked
-    (ring reuse with two slots at 64 KiB) into pageable or pinned memory."""
-    B, S = 2, 1024
+    (ring reuse with two slots at 64 KiB) into pageable or pinned memory.
+    S = 4096: the permute stores its result through the caches (planes
+    512 KiB apart), and the copies that follow read it."""
+    B = 2
     x, s = W.c5_input(B, S, seed=77)
     b = P.Bound(P.Plan(W.c5_plan().blob), {"B": B, "S": S}, W.param("scale", s))
     xs = torch.from_numpy(x.view(np.uint16).view(np.int16).copy()).cuda()
