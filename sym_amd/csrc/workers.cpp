@@ -78,8 +78,8 @@ void Workers::loop(unsigned id) {
 }
 
 void Workers::parallel_for(int64_t n, int64_t grain,
-                           const std::function<void(int64_t, int64_t)> &fn) {
-  const unsigned total = size();
+                           const std::function<void(int64_t, int64_t)> &fn, unsigned max_parts) {
+  const unsigned total = max_parts ? std::min(max_parts, size()) : size();
   const int64_t parts =
       std::max<int64_t>(1, std::min<int64_t>(total, n / std::max<int64_t>(1, grain)));
   if (parts <= 1 || threads_.empty()) {

@@ -28,7 +28,9 @@ public:
   explicit Workers(unsigned threads);
   ~Workers();
   unsigned size() const { return static_cast<unsigned>(threads_.size()) + 1; }
-  void parallel_for(int64_t n, int64_t grain, const std::function<void(int64_t, int64_t)> &fn);
+  // At most `max_parts` ranges (0: one per thread of the pool).
+  void parallel_for(int64_t n, int64_t grain, const std::function<void(int64_t, int64_t)> &fn,
+                    unsigned max_parts = 0);
 
 private:
   void loop(unsigned id);

@@ -1,8 +1,9 @@
 // Stress test of relx::Workers (sym_amd/csrc/workers.cpp), built with g++
 // under ThreadSanitizer by tests/test_workers.py: many jobs in a row, jobs of
 // every size, workers that are slow to start (the caller then claims their
-// ranges) and workers that sleep between jobs; every element of every job
-// must be visited exactly once.
+// ranges), workers that sleep between jobs, and jobs that cap their ranges
+// below the pool's size (the other workers stay idle); every element of
+// every job must be visited exactly once.
 #include <atomic>
 #include <chrono>
 #include <cstdio>
@@ -25,6 +26,8 @@ int main() {
         hits[static_cast<size_t>(i)].store(0, std::memory_order_relaxed);
       if (mode == 3)
         std::this_thread::sleep_for(std::chrono::microseconds(300)); // workers go to sleep
+      // every third job caps its ranges at 1..threads+1 (0: one per thread)
+      const unsigned cap = job % 3 == 2 ? 1 + static_cast<unsigned>(rng() % (threads + 1)) : 0;
       w.parallel_for(n, grain, [&](int64_t a, int64_t b) {
         if (mode == 1 && a > 0)
           std::this_thread::sleep_for(std::chrono::microseconds(50));
@@ -33,7 +36,7 @@ int main() {
           if (mode == 2 && (i & 1023) == 0)
             std::this_thread::yield();
         }
-      });
+      }, cap);
       for (int64_t i = 0; i < n; ++i)
         if (hits[static_cast<size_t>(i)].load(std::memory_order_relaxed) != 1) {
           std::printf("threads %u job %d n %lld: element %lld visited %d times\n", threads, job,
