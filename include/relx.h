@@ -220,7 +220,8 @@ typedef struct relx_options {
   int host_stages;      /* leading per-tensor cast stages the host applies
                            while staging (-1 = auto: the leading narrowing
                            ones, whatever the source's memory; 0 = none) */
-  int gather_threads;   /* host staging threads (0 = default 8) */
+  int gather_threads;   /* host staging threads (0 = default: 8, and 12 for
+                           the host row gathers of indexed plans) */
   int source_pinned;    /* 1: source is page-locked; DMA it directly.
                            -1: probe; 0: pageable (stage through the ring) */
   uint64_t caller_stream; /* hipStream_t the call is ordered after and that
