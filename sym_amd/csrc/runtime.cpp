@@ -405,10 +405,10 @@ void slot_acquire(Context &ctx, int slot) {
   }
 }
 
-// Once the work that reads the slot is enqueued on `s`. `track` is false for
-// a blocking call that stages no more chunks than the ring has slots: its
-// final synchronization proves every read of the slot done before the host
-// can write it again, so no event is recorded (two runtime calls fewer per
+// Once the work that reads the slot is enqueued on `s`. `track` is false
+// when no later chunk of a blocking call reuses the slot: the call's final
+// synchronization proves every read of the slot done before the host can
+// write it again, so no event is recorded (two runtime calls fewer per
 // chunk, about 4 us of a small call).
 void slot_release(Context &ctx, int slot, hipStream_t s, bool track) {
   if (!track)
@@ -668,14 +668,17 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
     throw Error("invalid_options", "an allocation-free call has no staging ring");
   if (max_slot)
     ensure_ring(ctx, nslots, max_slot);
-  // Slot events are needed by a call that returns before its work completes
-  // and by one that reuses a slot within itself.
+  // A slot's event is needed when the call returns before its work
+  // completes, or when a later chunk of this call reuses the slot (staged
+  // chunk j takes slot j mod ring size).
   int64_t staged = 0;
   for (size_t i = 0; i < ms.size(); ++i)
     if (!ms[i].direct)
       staged += (plans[i].units + plans[i].per_chunk - 1) / plans[i].per_chunk;
-  const bool track_slots =
-      comp != nullptr || opt.no_wait != 0 || staged > static_cast<int64_t>(ctx.slots.size());
+  const bool early = comp != nullptr || opt.no_wait != 0;
+  const int64_t nring = static_cast<int64_t>(ctx.slots.size());
+  int64_t staged_no = 0; // staged chunks so far
+  auto next_track = [&] { return early || staged_no++ + nring < staged; };
   // Staging workers: the caller's count for every job when it gives one;
   // else 8, and 12 for the host row gathers of indexed plans, whose random
   // rows want more reads in flight (ix f32 -> f16, 64 Ki rows of 4 KiB:
@@ -760,7 +763,7 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
             std::memcpy(s + x, from + x, static_cast<size_t>(y - x));
           }, parts);
           HIPCHECK(hipMemcpyAsync(wire + b0, s, static_cast<size_t>(n), hipMemcpyHostToDevice, cs));
-          slot_release(ctx, slot, cs, track_slots);
+          slot_release(ctx, slot, cs, next_track());
           slot = (slot + 1) % static_cast<int>(ctx.slots.size());
         }
         ++chunks;
@@ -772,6 +775,7 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
     }
     const KernelBatches kb = kernel_batches(p);
     int zc_slot = -1; // the ring slot a zero-copy member's kernels read
+    bool zc_track = false;
     int64_t kb0 = 0; // first unit of the kernel batch being gathered
     for (int64_t v0 = 0; v0 < (m.table ? 0 : p.units); v0 += p.per_chunk) {
       const int64_t v1 = std::min(p.units, v0 + p.per_chunk);
@@ -810,10 +814,11 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
         if (m.zero_copy) {
           kwire = s; // the slot is released after the kernels that read it
           zc_slot = slot;
+          zc_track = next_track();
         } else {
           HIPCHECK(hipMemcpyAsync(wire + woff, s, static_cast<size_t>(wbytes),
                                   hipMemcpyHostToDevice, cs));
-          slot_release(ctx, slot, cs, track_slots);
+          slot_release(ctx, slot, cs, next_track());
         }
         slot = (slot + 1) % static_cast<int>(ctx.slots.size());
       }
@@ -832,7 +837,7 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
       const int64_t nl = launch_program(dp, kb0, v1, kb0 == 0, v1 == p.units, kwire, m.dst,
                                         par.pf, par.pi, status, cs);
       if (zc_slot >= 0)
-        slot_release(ctx, zc_slot, cs, track_slots);
+        slot_release(ctx, zc_slot, cs, zc_track);
       if (tev) {
         HIPCHECK(hipEventRecord(tev[1], cs));
         ctx.kt.launches += nl;
