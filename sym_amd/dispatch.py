@@ -415,6 +415,12 @@ def execute_dispatch(request, *, caller_stream=None, n_buffers=2, n_streams=2, g
         if gather_threads < 0:
             raise ValueError("gather_threads must be >= 0 (0 = all cores)")
         gather_threads = _gather_threads(gather_threads, gather_pool)
+        live = _live_limit(resources)
+        if live is not None and request.template.direction == "h2d" and _request_wire(request) > live:
+            request.consumed = True
+            raise TransferError("insufficient_capacity",
+                                "typed scratch live-byte limit exceeded: the wire takes %d bytes, "
+                                "max_live_bytes is %d" % (_request_wire(request), live))
         request.executing = True
         src, dst = request.source, request.destination
         d2h = request.template.direction == "d2h"
@@ -468,6 +474,19 @@ def prepare_dispatch_group(entries):
     return GroupRequest(items)
 
 
+def _request_wire(r):
+    """Device wire bytes a request stages (its selected host boundary)."""
+    b, k = _unwrap(r.template.bound), r.selected["host_stages"]
+    return int(b.info.wire_bytes_at[k if k >= 0 else b.info.host_stages_auto])
+
+
+def _live_limit(resources):
+    """The live-byte cap of a DispatchResources owner (None: no cap)."""
+    limits = getattr(resources, "_limits", None) or {}
+    v = limits.get("live_bytes")
+    return v if v else None
+
+
 def _check_group_scratch(group, max_scratch_bytes):
     """The group's members hold their wire in the device arena together
     until the group completes (each 256-byte aligned): a group whose wire
@@ -475,11 +494,7 @@ def _check_group_scratch(group, max_scratch_bytes):
     its requests are spent, as the reference's owner refuses scratch past
     its live-byte limit (libreloc/src/DispatchResources.cpp:120-137;
     the group is consumed, libreloc/python/tests/torch_frontend/test_group.py:176-179)."""
-    def wire(r):
-        b, k = _unwrap(r.template.bound), r.selected["host_stages"]
-        return int(b.info.wire_bytes_at[k if k >= 0 else b.info.host_stages_auto])
-
-    need = sum((wire(r) + 255) // 256 * 256 for r in group.items)
+    need = sum((_request_wire(r) + 255) // 256 * 256 for r in group.items)
     if need > max_scratch_bytes:
         group.consumed = True
         for r in group.items:
@@ -503,7 +518,7 @@ def execute_dispatch_group(group, *, caller_stream=None, gather_threads=8, gathe
         raise ValueError("gather_threads and max_scratch_bytes must be positive")
     gather_threads = _gather_threads(gather_threads, gather_pool)
     _pinning(pinning)
-    _check_group_scratch(group, max_scratch_bytes)
+    _check_group_scratch(group, min(max_scratch_bytes, _live_limit(resources) or max_scratch_bytes))
     group.executing = True
     try:
         dev = max(0, group.items[0].destination.device)
@@ -597,7 +612,7 @@ def submit_dispatch_group(group, *, caller_stream=None, gather_threads=8, gather
         raise ValueError("gather_threads and max_scratch_bytes must be positive")
     gather_threads = _gather_threads(gather_threads, gather_pool)
     _pinning(pinning)
-    _check_group_scratch(group, max_scratch_bytes)
+    _check_group_scratch(group, min(max_scratch_bytes, _live_limit(resources) or max_scratch_bytes))
     dev = max(0, group.items[0].destination.device)
     ctx = _resources_for(resources, dev)
     bounds = [r.template.bound for r in group.items]

@@ -289,3 +289,23 @@ def test_group_scratch_limit_refused_before_launch():
     with pytest.raises(P.TransferError, match="live-byte limit"):
         P.submit_dispatch_group(g2, max_scratch_bytes=1000, owners=((), ()))
     assert g2.consumed
+
+
+def test_live_byte_limit_of_the_owner_refused_before_launch():
+    """DispatchResources(max_live_bytes=...) caps the scratch of one call
+    (reference DispatchResources.h:57-61: maxLiveBytes also caps scratch
+    during a call): a request whose wire exceeds it is refused before any
+    work, with no GPU touched; 0 means no cap."""
+    b = c2_bound()
+    src = np.zeros((2, 3, 224, 224), np.float32)
+    wire = 2 * 3 * 224 * 224 * 2  # the f16 wire after the staged cast
+    owner = P.DispatchResources(max_live_bytes=wire - 1)
+    req = P.prepare_dispatch(b, host_view(src), fake_device_view([2, 224, 224, 4], 2), "h2d")
+    with pytest.raises(P.TransferError, match="live-byte limit") as e:
+        P.execute_dispatch(req, resources=owner)
+    assert e.value.code == "insufficient_capacity" and req.consumed
+    g = P.prepare_dispatch_group([(b, host_view(src), fake_device_view([2, 224, 224, 4], 2), "h2d")])
+    with pytest.raises(P.TransferError, match="live-byte limit"):
+        P.execute_dispatch_group(g, resources=owner, max_scratch_bytes=1 << 40)
+    assert owner.stats()["context_creations"] == 0
+    owner.close()
