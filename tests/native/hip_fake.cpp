@@ -132,6 +132,18 @@ struct HostAgent {
   VClock vc;
 };
 thread_local HostAgent t_host;
+thread_local uint64_t t_call = 0; // library calls this thread has begun
+// Per library staging allocation: who last staged it (host agent, call,
+// destination of the kernels that read it).
+struct Staged {
+  int agent;
+  uint64_t call;
+  const void *dst;
+  bool operator==(const Staged &o) const {
+    return agent == o.agent && call == o.call && dst == o.dst;
+  }
+};
+std::map<uintptr_t, Staged> g_staged;
 thread_local int t_device = 0;
 thread_local hipError_t t_last = hipSuccess;
 
@@ -399,6 +411,7 @@ hipError_t release(void *p, Mem kind, const char *what) {
   g_acc.erase(std::remove_if(g_acc.begin(), g_acc.end(),
                              [&](const Access &a) { return a.lo < hi && lo < a.hi; }),
               g_acc.end());
+  g_staged.erase(lo);
   g_allocs.erase(it);
   if (!in_use) // memory a device operation may still touch is kept
     std::free(p);
@@ -788,11 +801,18 @@ hipError_t launch_box(int family, const KArgs &a, int32_t *status, hipStream_t s
   {
     // a kernel that reads the library's own page-locked staging (a
     // zero-copy chunk): the host has just filled it, as for a copy from it
-    const Alloc *al = find_alloc(slo);
+    // (once per chunk: the chunk's later kernels read the same staging)
+    uintptr_t base = 0;
+    const Alloc *al = find_alloc(slo, &base);
     if (al && al->kind == Mem::Pinned && !al->user) {
       ++g_counts.zero_copy;
       HostAgent &h = host_tick();
-      access(slo, shi, true, h.vc, h.id, h.vc[static_cast<size_t>(h.id)], "host staging write");
+      const Staged now{h.id, t_call, a.dst};
+      auto it = g_staged.find(base);
+      if (t_call == 0 || it == g_staged.end() || !(it->second == now)) {
+        access(slo, shi, true, h.vc, h.id, h.vc[static_cast<size_t>(h.id)], "host staging write");
+        g_staged[base] = now;
+      }
     }
   }
   std::vector<std::pair<uintptr_t, uintptr_t>> reads{{slo, shi}};
@@ -901,6 +921,7 @@ void fake_reset(void) {
   for (hipError_t &e : g_sticky)
     e = hipSuccess;
   g_acc.clear();
+  g_staged.clear();
   g_violations.clear();
 }
 
@@ -963,6 +984,11 @@ void fake_host_adopt(int token) {
     return;
   HostAgent &h = host_tick();
   vjoin(h.vc, g_tokens[static_cast<size_t>(token)]);
+}
+
+void fake_call_begin(void) {
+  std::lock_guard<std::mutex> g(g_mu);
+  ++t_call;
 }
 
 void fake_shutdown(void) {

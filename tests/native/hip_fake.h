@@ -81,6 +81,13 @@ void fake_mark_user_pinned(const void *p);
 int fake_host_handoff(void);
 void fake_host_adopt(int token);
 
+// The calling thread starts a library call. The library stages a zero-copy
+// chunk on the host once and then launches the chunk's kernels (one per box
+// of its program) against it; the stand-in records that staging as a host
+// write of the slot at the first kernel of a call that reads the slot for a
+// destination, not again at the later kernels of the same chunk.
+void fake_call_begin(void);
+
 // Stop every stream's worker (streams of quarantined contexts included).
 void fake_shutdown(void);
 }

@@ -331,6 +331,7 @@ void run_h2d(const Case &c, const Opts &o, Result &r, relx_ctx *ctx) {
       bound = fresh.get();
     }
     relx_err e{};
+    fake_call_begin();
     const int rc = relx_execute_h2d(ctx, bound, src, c.src.size(), dst, out, &opt, &r.report, &e);
     r.calls.push_back(call_of(rc, e));
     if (rc != RELX_OK) {
@@ -342,6 +343,7 @@ void run_h2d(const Case &c, const Opts &o, Result &r, relx_ctx *ctx) {
         for (++i; i < repeat; ++i) {
           relx_err e3{};
           relx_options o3 = options_of(o);
+          fake_call_begin();
           r.calls.push_back(call_of(
               relx_execute_h2d(ctx, c.bound, src, c.src.size(), dst, out, &o3, nullptr, &e3), e3));
         }
@@ -402,6 +404,7 @@ void run_group(const Case &c, const Opts &o, Result &r, relx_ctx *ctx, bool subm
     relx_err e{};
     relx_report total{};
     int rc;
+    fake_call_begin();
     if (submit) {
       relx_completion *comp = nullptr;
       rc = relx_submit_group_h2d(ctx, n, bounds.data(), sp.data(), sb.data(), dp.data(), db.data(), &opt,
@@ -474,6 +477,7 @@ void run_d2h(const Case &c, const Opts &o, Result &r, relx_ctx *ctx) {
     caller.apply(opt);
     caller.produce(src, c.src.data(), c.src.size()); // the device source's producer
     relx_err e{};
+    fake_call_begin();
     const int rc = relx_execute_d2h(ctx, c.bound, src, c.src.size(), dst, out, &opt, &r.report, &e);
     r.calls.push_back(call_of(rc, e));
     if (rc == RELX_OK)
@@ -566,6 +570,7 @@ void run_threads(const Case &c, const Opts &o, Result &r, relx_ctx *ctx) {
       for (int k = 0; k < repeat; ++k) {
         relx_options opt = options_of(o);
         relx_err e{};
+        fake_call_begin();
         const int rc = relx_execute_h2d(ctxs[i], c.bound, srcs[i].data(), c.src.size(), dsts[i], out,
                                         &opt, nullptr, &e);
         calls[i].push_back(call_of(rc, e));
@@ -614,6 +619,7 @@ void run_static(const Case &c, const Opts &o, Result &r, relx_ctx *ctx) {
     relx_options opt = options_of(o);
     opt.source_pinned = 1;
     relx_err e{};
+    fake_call_begin();
     const int rc = relx_execute_h2d_static(ctx, c.bound, src, c.src.size(), dst, out, &opt, &r.report, &e);
     r.calls.push_back(call_of(rc, e));
     if (rc != RELX_OK) {

@@ -133,6 +133,11 @@ def cases(tmp_path_factory):
     iplan = EN.encode_index_select(["N", "D"], "float32", "M", "int64", "float32")
     syms = {"N": 4096, "D": 64, "M": len(idx)}
     c["ix"] = write_case(root, "ix", iplan, table, table[idx].tobytes(), syms, index=(64, idx))
+    # a (128, 96) f16 transpose: a tile kernel and an edge kernel read the
+    # one chunk
+    plan, src, _ = F.make_plan(255)
+    want = O.execute_layout(O.bind(O.decode_plan(plan.blob), {}), src.tobytes())
+    c["edge"] = write_case(root, "edge", plan.blob, src, want)
     # random layout plans (pads, transposes, reshapes) from the fuzz set
     k = 0
     for seed in range(0, 200):
@@ -330,20 +335,26 @@ def test_small_staged_uploads_read_their_slot(driver, cases):
     reads the ring slot (zero-copy), with no copy ahead of it; a pinned
     source keeps its direct copy, and a chunked upload its copies. Blocking
     calls back to back, no_wait calls and calls from several threads all
-    reuse the slot in order, with the results of the oracle."""
+    reuse the slot in order, with the results of the oracle, also where
+    several kernels of one call read the slot."""
     lines = ["h2d %s repeat=3 %s" % (cases["c1"], DELAYS),
              "h2d %s repeat=3 pinned=1 %s" % (cases["c1"], DELAYS),
              "h2d %s repeat=3 chunk=65536 nbuf=2 %s" % (cases["c1"], DELAYS),
              "h2d %s repeat=4 nowait=1 burst=1 %s" % (cases["c1"], DELAYS),
              "h2d %s repeat=2 %s" % (cases["c2"], DELAYS),
              "h2d %s repeat=2 %s" % (cases["ix"], DELAYS),
-             "threads %s threads_n=3 repeat=3 shared=1 %s" % (cases["c1"], DELAYS)]
+             "threads %s threads_n=3 repeat=3 shared=1 %s" % (cases["c1"], DELAYS),
+             "h2d %s repeat=3 %s" % (cases["edge"], DELAYS),
+             "h2d %s repeat=3 nowait=1 burst=1 %s" % (cases["edge"], DELAYS)]
     res = run(driver, lines)
     for r in res:
         ok(r)
     zc = [r["counts"]["zero_copy"] for r in res]
     assert zc[:6] == [3, 0, 0, 4, 2, 2], zc
     assert zc[6] == 9, zc
+    # two kernels per call read the one staging of its chunk
+    assert [r["report"]["kernel_launches"] for r in res[7:]] == [2, 2], res[7:]
+    assert zc[7:] == [6, 6], zc
 
 
 def test_checker_reports_a_missing_wait(driver, cases):
