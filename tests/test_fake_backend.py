@@ -357,6 +357,33 @@ def test_small_staged_uploads_read_their_slot(driver, cases):
     assert zc[7:] == [6, 6], zc
 
 
+def test_random_layout_plans_under_delays(driver, tmp_path):
+    """Random layout plans from the fuzz set (seeds 200..420: pads,
+    transposes with edge tiles, reshapes), each uploaded blocking from
+    pageable and pinned sources, in no_wait calls back to back and in small
+    chunks, evicted device-to-host and relaid on the device, under jittered
+    delays: the oracle's results and no unordered access."""
+    lines = []
+    for seed in range(200, 420):
+        r = F.make_plan(seed)
+        if r is None or r[0].typed:
+            continue
+        plan, src, _ = r
+        try:
+            want = O.execute_layout(O.bind(O.decode_plan(plan.blob), {}), src.tobytes())
+        except (O.BindError, O.ExecutionError):
+            continue
+        d = write_case(str(tmp_path), "f%d" % seed, plan.blob, src, want)
+        dl = "delay_copy=200 delay_kernel=200 jitter=1 seed=%d" % seed
+        lines += ["h2d %s repeat=2 %s" % (d, dl), "h2d %s repeat=2 pinned=1 %s" % (d, dl),
+                  "h2d %s repeat=3 nowait=1 burst=1 %s" % (d, dl),
+                  "h2d %s repeat=2 chunk=4096 nbuf=2 %s" % (d, dl),
+                  "d2h %s repeat=2 %s" % (d, dl), "device %s %s" % (d, dl)]
+    assert len(lines) >= 60, len(lines)
+    for r in run(driver, lines, timeout=600):
+        ok(r)
+
+
 def test_checker_reports_a_missing_wait(driver, cases):
     """The device source is written on the caller's stream, but the call is
     told of no producer stream: the relayout reads it unordered."""
