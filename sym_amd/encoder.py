@@ -10,7 +10,9 @@ docs/reloc-plan-format.md:
 
   * the view starts as the identity over the source (axis k has the source's
     row-major stride); transposes permute axes, reshapes split/merge them
-    (symbolic splits emit divisibility constraints), pads attach to an axis;
+    (symbolic splits emit divisibility constraints), pads attach to an axis
+    (a second same-fill pad of the axis widens it; a reshape keeps a padded
+    axis only 1:1);
   * value stages record their logical operand shape and a channel map over
     the logical result coordinates; pending pad fills fold through later
     per-tensor stages (a per-channel stage after a pad is rejected);
@@ -354,23 +356,41 @@ def encode(source_shape: Sequence, source_dtype: str, ops: Sequence, *, force_ty
                 if s.channel is not None:
                     s.channel = _remap_dims(s.channel, inv)
         elif isinstance(op, Reshape):
-            if pads:
-                raise EncodeError("reshape after pad is not folded")
             for s in stages:
                 if s.channel is not None:
                     raise EncodeError("reshape after a per-channel stage is not folded")
-            axes, divs = _reshape(axes, [expr(t) for t in op.to])
+            target = [expr(t) for t in op.to]
+            if any(t.kind == "const" and t.value <= 0 for t in target):
+                raise EncodeError("reshape to a non-positive extent")
+            if pads:
+                axes, divs = _reshape_padded(axes, pads, target)
+            else:
+                axes, divs = _reshape(axes, target)
             for d in divs:
                 if d not in divisibility:
                     divisibility.append(d)
         elif isinstance(op, Pad):
             if not 0 <= op.axis < len(axes):
                 raise EncodeError("pad axis out of range")
-            if any(p.axis == op.axis for p in pads):
-                raise EncodeError("one pad per axis")
+            lo, hi = expr(op.lo), expr(op.hi)
+            # sym/dialect/reloc/Transforms/PlanBuilder.cpp:497-506: a provably
+            # negative width is refused, two zero widths record nothing
+            if any(w.kind == "const" and w.value < 0 for w in (lo, hi)):
+                raise EncodeError("negative pad width")
+            if lo.is_const(0) and hi.is_const(0):
+                continue
             bits = op.bits if op.bits is not None else _value_bits(op.value, dtype)
-            lo = expr(op.lo)
-            pads.append(_PadState(op.axis, lo, expr(op.hi), bits, bits, dtype, len(stages)))
+            old = next((p for p in pads if p.axis == op.axis), None)
+            if old is not None:
+                # PlanBuilder.cpp:534-548: a second pad of the axis with the
+                # same fill, entering at the same value stage, wraps the first
+                # (widths add); the format keeps one fill per axis
+                if old.bits != bits or old.stage != len(stages):
+                    raise EncodeError("one pad per axis: a second pad needs the same fill "
+                                      "and value stage")
+                old.lo, old.hi = add(old.lo, lo), add(old.hi, hi)
+            else:
+                pads.append(_PadState(op.axis, lo, hi, bits, bits, dtype, len(stages)))
             # earlier stages' channel maps read the padded axis shifted by the
             # leading width (the reference builder does the same,
             # sym/dialect/reloc/Transforms/PlanBuilder.h:44-47)
@@ -409,6 +429,45 @@ def _remap_dims(e: E, inv: List[int]) -> E:
     if e.kind in ("const", "sym"):
         return e
     return E(e.kind, _remap_dims(e.a, inv), _remap_dims(e.b, inv))
+
+
+def _reshape_padded(axes: List[_Axis], pads: List[_PadState], target: List[E]):
+    """Reshape a padded view: each padded axis must be kept 1:1 (a target
+    entry equal to its padded extent, the axes before it regrouping onto the
+    entries before that one); the unpadded axes between regroup among
+    themselves. A split or merge of a padded axis is refused, as the valid
+    region would no longer be a per-axis box (the reference builder's rule,
+    sym/dialect/reloc/Transforms/PlanBuilder.cpp reshape fold; unittest
+    PlanBuilderTest.cpp:631-682). Moves the pads to their new positions."""
+    by_axis = {p.axis: p for p in pads}
+    out: List[_Axis] = []
+    divs: List[Tuple[E, int]] = []
+    where = {}
+    a0 = t0 = 0
+    for i in sorted(by_axis):
+        p = by_axis[i]
+        ext = add(add(axes[i].extent, p.lo), p.hi)
+        for j in range(t0, len(target)):
+            if not target[j] == ext:
+                continue
+            try:
+                seg, d = _reshape(axes[a0:i], target[t0:j])
+            except EncodeError:
+                continue
+            break
+        else:
+            raise EncodeError("reshape splits or merges a padded axis")
+        out += seg
+        divs += d
+        where[i] = len(out)
+        out.append(_Axis(axes[i].extent, axes[i].stride, axes[i].src_pos))
+        a0, t0 = i + 1, j + 1
+    seg, d = _reshape(axes[a0:], target[t0:])
+    out += seg
+    divs += d
+    for p in pads:
+        p.axis = where[p.axis]
+    return out, divs
 
 
 def _reshape(axes: List[_Axis], target: List[E]):
