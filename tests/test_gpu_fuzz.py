@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 
 from oracle import relx_oracle as O
+from sym_amd import encoder as EN
 from sym_amd import pyreloc as P
 from tests import fuzz_plans as F
 
@@ -93,3 +94,55 @@ def test_random_plans_on_the_gpu(ctx, block):
             assert host[:out_bytes].numpy().tobytes() == want, (seed, ops, "d2h", pinned)
         n_run += 1
     assert n_run > min(30, len(SEEDS) // 16)
+
+
+# Plans of the encoder's pad rules (a same-fill pad widened, a padded axis
+# kept through a reshape that merges the axes before it, then transposed),
+# at sizes that take several kernel tiles; the truth is numpy's.
+RULE_CASES = [
+    ([64, 96, 48], [EN.Pad(2, 3, 5, 1.5), EN.Pad(2, 1, 0, 1.5), EN.Reshape((64 * 96, 57)),
+                    EN.Transpose((1, 0))]),
+    ([40, 3, 130], [EN.Pad(0, 2, 6), EN.Reshape((48, 390))]),
+    ([6, 4, 256], [EN.Pad(2, 0, 64), EN.Reshape((24, 320)), EN.Transpose((1, 0))]),
+]
+
+
+def _numpy_rule(shape, ops):
+    x = np.arange(int(np.prod(shape)), dtype=np.float32).reshape(shape)
+    for op in ops:
+        if isinstance(op, EN.Pad):
+            w = [(0, 0)] * x.ndim
+            w[op.axis] = (op.lo, op.hi)
+            x = np.pad(x, w, constant_values=op.value)
+        elif isinstance(op, EN.Reshape):
+            x = x.reshape(op.to)
+        else:
+            x = x.transpose(op.perm)
+    return np.ascontiguousarray(x).tobytes()
+
+
+@pytest.mark.parametrize("case", range(len(RULE_CASES)))
+def test_encoder_rule_plans_on_the_gpu(ctx, case):
+    shape, ops = RULE_CASES[case]
+    plan = EN.encode(shape, "float32", ops)
+    src = np.arange(int(np.prod(shape)), dtype=np.float32).reshape(shape)
+    want = _numpy_rule(shape, ops)
+    assert oracle_bytes(plan, src) == want
+    b = P.Bound(P.Plan(plan.blob), {}, None)
+    assert b.total_bytes == len(want)
+    out = torch.empty(len(want), dtype=torch.uint8, device="cuda")
+    for chunk in (0, 4096):
+        say("encoder rule case", case, "kernel", b.kernel, "h2d chunk", chunk)
+        out.fill_(0xA5)
+        ctx.execute_h2d(b, src.ctypes.data, src.nbytes, out.data_ptr(), len(want),
+                        chunk_bytes=chunk, caller_stream=torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert out.cpu().numpy().tobytes() == want, (case, chunk)
+    say("encoder rule case", case, "device-resident")
+    d_src = torch.from_numpy(src.view(np.uint8).reshape(-1).copy()).cuda()
+    out.fill_(0xA5)
+    ctx.relayout_device(b, d_src.data_ptr(), out.data_ptr(),
+                        stream=torch.cuda.current_stream().cuda_stream)
+    ctx.synchronize()
+    torch.cuda.synchronize()
+    assert out.cpu().numpy().tobytes() == want, (case, "device")
