@@ -124,6 +124,21 @@ def floordiv(a: E, b: E) -> E:
     return E("floordiv", a, b)
 
 
+def sub(a: E, b: E) -> E:
+    if a.is_const() and b.is_const():
+        return E.c(a.value - b.value)
+    if b.is_const(0):
+        return a
+    return E("sub", a, b)
+
+
+def align_up_pad(e, align: int) -> E:
+    """The trailing pad width that rounds extent `e` up to a multiple of
+    `align`: ((e + align - 1) // align) * align - e."""
+    e = expr(e)
+    return sub(mul(floordiv(add(e, E.c(align - 1)), E.c(align)), E.c(align)), e)
+
+
 def mod(a: E, b: E) -> E:
     if a.is_const() and b.is_const():
         return E.c(a.value % b.value)
@@ -809,7 +824,9 @@ def _finalize(source_shape, source_dtype, axes, pads, stages, divisibility, dtyp
     # a layout-only plan whose axes move nothing is a pure view
     view = not typed and not new_pads and all(a.stride == s for a, s in zip(maxes, dstr))
     w.u8(1 if view else 0)  # no_copy
-    w.u8(0)  # runtime_pad_check
+    # a symbolic pad width leaves the padded range to be checked at bind time
+    # (sym/dialect/reloc/Transforms/PlanBuilder.cpp:74-79)
+    w.u8(1 if any(not (p.lo.is_const() and p.hi.is_const()) for p in new_pads.values()) else 0)
     w.u32(len(maxes))
     w.u32(len(maxes))
     inv = [perm.index(i) for i in range(len(perm))]

@@ -156,3 +156,17 @@ def test_pads_through_reshapes():
     # and a transpose after that still finds it
     _, got = run([2, 3, 6], [Pad(2, 1, 1), Reshape((6, 8)), Transpose((1, 0))])
     assert np.array_equal(got, pad(iota([2, 3, 6]), 2, 1, 1).reshape(6, 8).T.ravel())
+
+
+def test_alignment_pad_binds_with_a_runtime_check():
+    # PlanBuilderTest.cpp:600-617: hi = align_up(N, A) - N
+    for align in (64, 128):
+        plan = EN.encode(["N"], "float32", [Pad(0, 0, EN.align_up_pad("N", align))])
+        dec = O.decode_plan(plan.blob)
+        assert dec.runtime_pad_check
+        for n in (150, align, 1):
+            x = iota([n])
+            got = O.execute_layout(O.bind(dec, {"N": n}), x.tobytes())
+            assert got == pad(x, 0, 0, (-n) % align).tobytes(), (align, n)
+    # static widths need no check
+    assert not O.decode_plan(EN.encode([6], "float32", [Pad(0, 1, 1)]).blob).runtime_pad_check
