@@ -875,7 +875,7 @@ __global__ __launch_bounds__(kBlock) void k_interleave1p(const uint8_t *src, int
 // CACHED_ST: the runs are stored through the caches instead of streaming
 // (permute_cached_stores).
 template <int WIN, int WOUT, int CH, bool CACHED_ST>
-__global__ __launch_bounds__(kBlock) void k_permute(KArgs a) {
+__device__ __forceinline__ void permute_body(const KArgs &a) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int VI = 16 / WIN, BO = VI * WOUT;
   constexpr int U = 4; // source vectors in flight per thread
@@ -962,6 +962,33 @@ __global__ __launch_bounds__(kBlock) void k_permute(KArgs a) {
     const vec4 val = reinterpret_cast<const vec4 *>(lds)[w];
     st16<NTS>(reinterpret_cast<vec4 *>(dst + c * a.p_dsc * WOUT) + j, val);
   }
+}
+
+template <int WIN, int WOUT, int CH, bool CACHED_ST>
+__global__ __launch_bounds__(kBlock) void k_permute(KArgs a) {
+  permute_body<WIN, WOUT, CH, CACHED_ST>(a);
+}
+
+// The same kernel at eight waves per SIMD (at most 64 VGPRs): 256 CUs then
+// hold 2048 blocks of four waves at once, and the power-of-two block counts
+// of activation shapes (2048 at [1,4096,32,128], 4096 at [8,1024,..], 16384
+// at [8,4096,..]) run as whole rounds, instead of ending on a round of 256
+// blocks, one per CU, too few to keep HBM busy. The f16 -> int8 chain needs
+// 69 VGPRs without the bound, which leaves seven waves. Measured on the
+// MI355X, two alternating passes: 1x4096 11.45 -> 11.21 us, 8x1024 19.1 ->
+// 18.85 us, 8x4096 66.1 -> 65.25 us, 64x1024 125.4 -> 124.5 us; no shape
+// slower.
+template <int WIN, int WOUT, int CH, bool CACHED_ST>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_permute8(
+    KArgs a) {
+  permute_body<WIN, WOUT, CH, CACHED_ST>(a);
+}
+
+// Chains whose permute fits eight waves without spilling registers: the
+// generic per-stage chain and the dequantizing chains over one-byte
+// sources do not (they spill hundreds of VGPRs under the bound).
+constexpr bool permute_eight_waves(int win, int ch) {
+  return ch != kChainGeneric && !(win == 1 && (ch == kChainDeqF16 || ch == kChainDeq));
 }
 
 // ------------------------------------------------------------ launch
@@ -1053,12 +1080,19 @@ inline bool permute_cached_stores(const KArgs &a, int wout) {
 
 template <int WIN, int WOUT, int CH>
 hipError_t permute_launch(const KArgs &a, hipStream_t s) {
-  if (permute_cached_stores(a, WOUT))
-    hipLaunchKernelGGL((k_permute<WIN, WOUT, CH, true>), dim3(static_cast<unsigned>(a.work)),
-                       dim3(kBlock), a.p_lds, s, a);
-  else
-    hipLaunchKernelGGL((k_permute<WIN, WOUT, CH, false>), dim3(static_cast<unsigned>(a.work)),
-                       dim3(kBlock), a.p_lds, s, a);
+  const dim3 grid(static_cast<unsigned>(a.work)), block(kBlock);
+  const bool cached = permute_cached_stores(a, WOUT);
+  if constexpr (permute_eight_waves(WIN, CH)) {
+    if (cached)
+      hipLaunchKernelGGL((k_permute8<WIN, WOUT, CH, true>), grid, block, a.p_lds, s, a);
+    else
+      hipLaunchKernelGGL((k_permute8<WIN, WOUT, CH, false>), grid, block, a.p_lds, s, a);
+  } else {
+    if (cached)
+      hipLaunchKernelGGL((k_permute<WIN, WOUT, CH, true>), grid, block, a.p_lds, s, a);
+    else
+      hipLaunchKernelGGL((k_permute<WIN, WOUT, CH, false>), grid, block, a.p_lds, s, a);
+  }
   return hipGetLastError();
 }
 
