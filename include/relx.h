@@ -224,15 +224,22 @@ typedef struct relx_options {
                            the host row gathers of indexed plans) */
   int source_pinned;    /* 1: source is page-locked; DMA it directly.
                            -1: probe; 0: pageable (stage through the ring) */
-  uint64_t caller_stream; /* hipStream_t the call is ordered after and that
-                             waits for the call's end, when has_caller_stream
-                             is set; 0 is HIP's legacy null stream */
+  uint64_t caller_stream; /* hipStream_t the call's kernels and direct
+                             copies are ordered after, and that a no_wait
+                             call's end is ordered before, when
+                             has_caller_stream is set; 0 is HIP's legacy
+                             null stream */
   int no_wait;          /* 1: return after enqueue; the caller's stream (or
                            relx_ctx_synchronize) orders later work */
   int has_caller_stream; /* 1: order after caller_stream (reference
                             TransferOptions::hasCallerStream,
                             libreloc/include/reloc/Transfer.h:126-128);
                             0: no producer stream to order after */
+  int n_streams;        /* copy streams the call's chunks alternate over
+                           (reference execute_dispatch n_streams,
+                           libreloc/python/PyDispatch.cpp:159-235): 1 puts
+                           every copy and kernel on one stream; 0 (default)
+                           and 2 or more use the context's two copy streams */
 } relx_options;
 
 /* Scalar report of one call (reference dispatch::Report,
@@ -248,6 +255,15 @@ typedef struct relx_report {
   int64_t kernel_launches;
   int wire_boundary;
   int direct_dma; /* 1 when the source was DMA'd without staging */
+  /* The host side of the call (reference Report::hostChunkBytes /
+   * hostBuffers and the staging rows, libreloc/include/reloc/Dispatch.h:
+   * 104-124, Transfer.h:112-119): */
+  int64_t host_chunk_bytes; /* bytes of the largest chunk moved (staged or DMA'd) */
+  int64_t host_buffers;     /* ring slots the staged chunks cycled through (0: none staged) */
+  int64_t staging_bytes;    /* page-locked bytes of the staging ring the call used (0: none) */
+  int64_t staging_slots;    /* that ring's slot count */
+  int staging_reused;       /* 1: the ring was kept from an earlier call (nothing allocated) */
+  int copy_streams;         /* copy streams the call's chunks used */
 } relx_report;
 
 /* Run one bound plan: host source (dense, source layout, source dtype) ->
@@ -255,8 +271,11 @@ typedef struct relx_report {
  * the chunked pinned H2D pipeline on the copy stream; relayout and value
  * stages run as HIP kernels behind each chunk's copy on its copy stream, while
  * the next chunk's copy runs on the other copy stream. With
- * `has_caller_stream` the copies start after the work enqueued on
- * `caller_stream` so far, and `caller_stream` waits for the call's end.
+ * `has_caller_stream` the call's kernels and its direct copies of a
+ * page-locked source run after the work enqueued on `caller_stream` so far
+ * (copies out of the library's staging ring touch no caller memory and
+ * start at once); a call that returns early (no_wait) makes `caller_stream`
+ * wait for its end, and a blocking call has completed when it returns.
  * Replaces dispatch::executeDispatch (libreloc/src/Dispatch.cpp:1983-2046)
  * for the H2D direction, executeTransfer (libreloc/src/Transfer.cpp:493-544)
  * for layout plans, and pyreloc.execute_dispatch / execute_transfer
@@ -274,17 +293,21 @@ int relx_execute_h2d(relx_ctx *ctx, const relx_bound *bound, const void *src, si
 /* The upload of relx_execute_h2d with no allocation: the call allocates no
  * device or pinned host memory (no hipMalloc, hipFree, hipHostMalloc or
  * allocating library routine). No counterpart in the reference; it is for
- * callers that cannot allocate: code under HIP graph capture, tight serving
- * loops, harnesses that forbid allocation. The wire is staged in the
- * library's static device scratch, a file-scope array of 64 MiB that each
- * GPU the library runs on holds until the process ends (63 MiB of wire, and
- * parameter tables of up to 512 KiB of floats and 512 KiB of ints), and the
- * source must be page-locked: it crosses by direct DMA, with no host stages.
- * Errors: "insufficient_capacity" for a wire or parameter tables beyond
- * those limits, "invalid_options" for a pageable source or host stages,
- * "plan_mismatch" for an indexed plan, else as relx_execute_h2d. Every call
- * on a GPU shares that GPU's scratch and leaves its contents behind: calls
- * that overlap on one GPU (from several contexts or threads) race. */
+ * callers that cannot allocate: tight serving loops, harnesses that forbid
+ * allocation. It is not for HIP graph capture: a blocking call waits on the
+ * host, and each call copies its parameter tables from host memory when it
+ * is made. The wire is staged in the library's static device scratch, a
+ * file-scope array of 64 MiB that each GPU the library runs on holds until
+ * the process ends (63 MiB of wire, and parameter tables of up to 512 KiB
+ * of floats and 512 KiB of ints), and the source must be page-locked: it
+ * crosses by direct DMA, with no host stages. Errors:
+ * "insufficient_capacity" for a wire or parameter tables beyond those
+ * limits, "invalid_options" for a pageable source or host stages,
+ * "plan_mismatch" for an indexed plan, else as relx_execute_h2d. Every
+ * static call on a GPU uses that GPU's one scratch and leaves its contents
+ * behind; calls from several contexts or threads take it in turn (a lock
+ * per GPU, and each call's copies into the scratch wait on the device for
+ * the previous static call's end, also after a no_wait call). */
 int relx_execute_h2d_static(relx_ctx *ctx, const relx_bound *bound, const void *src,
                             size_t src_bytes, void *dst, size_t dst_bytes, const relx_options *opt,
                             relx_report *report, relx_err *err);

@@ -68,7 +68,8 @@ class relx_options(ctypes.Structure):
     _fields_ = [("n_buffers", ctypes.c_int), ("chunk_bytes", ctypes.c_int64),
                 ("host_stages", ctypes.c_int), ("gather_threads", ctypes.c_int),
                 ("source_pinned", ctypes.c_int), ("caller_stream", ctypes.c_uint64),
-                ("no_wait", ctypes.c_int), ("has_caller_stream", ctypes.c_int)]
+                ("no_wait", ctypes.c_int), ("has_caller_stream", ctypes.c_int),
+                ("n_streams", ctypes.c_int)]
 
 
 class relx_report(ctypes.Structure):
@@ -77,7 +78,10 @@ class relx_report(ctypes.Structure):
                 ("parameter_bytes", ctypes.c_int64),
                 ("payload_bytes_transferred", ctypes.c_int64), ("chunks", ctypes.c_int64),
                 ("kernel_launches", ctypes.c_int64), ("wire_boundary", ctypes.c_int),
-                ("direct_dma", ctypes.c_int)]
+                ("direct_dma", ctypes.c_int), ("host_chunk_bytes", ctypes.c_int64),
+                ("host_buffers", ctypes.c_int64), ("staging_bytes", ctypes.c_int64),
+                ("staging_slots", ctypes.c_int64), ("staging_reused", ctypes.c_int),
+                ("copy_streams", ctypes.c_int)]
 
     def as_dict(self):
         return {f: (getattr(self, f).decode() if f == "implementation" else getattr(self, f))

@@ -240,7 +240,7 @@ int32_t read_status(const int32_t *status) {
 void clear_status(int32_t *status) { *static_cast<volatile int32_t *>(status) = 0; }
 
 // `s` waits for the work enqueued so far on the other copy streams among
-// the first `used` (chunk c goes to stream c mod kCopyStreams).
+// the first `used` (chunk c goes to stream c mod the call's stream count).
 void join_copy_streams(Context &ctx, hipStream_t s, int64_t used) {
   for (int i = 0; i < kCopyStreams && i < used; ++i) {
     if (ctx.copies[i] == s)
@@ -265,6 +265,60 @@ void copy_streams_wait(Context &ctx, hipEvent_t ev) {
   for (hipStream_t c : ctx.copies)
     HIPCHECK(hipStreamWaitEvent(c, ev, 0));
 }
+
+// Order after the caller's stream (relx_options.has_caller_stream, handle 0
+// being the legacy null stream): the work enqueued on it so far may still
+// produce a device source, read or write the destination, or fill a
+// page-locked source. Only the call's operations that touch the caller's
+// memory are ordered after it: kernels (they write the destination) and
+// copies that read the caller's page-locked source. Copies out of the
+// staging ring write only the library's own wire arena. When the caller's
+// stream has no work left, nothing waits; else each of the call's streams
+// waits on an event recorded on it, just before its first such operation,
+// and not at all once that event has completed. On the MI355X a
+// hipStreamWaitEvent on a pending event costs 10-15 us of host time (25 us
+// on an event of the null stream), 0.15 us on a completed one: waiting on
+// both copy streams up front put 20-50 us of host time before a call's
+// first copy.
+class CallerOrder {
+public:
+  CallerOrder(Context &ctx, const relx_options &opt) : ctx_(ctx) {
+    if (!opt.has_caller_stream)
+      return;
+    hipStream_t caller = reinterpret_cast<hipStream_t>(opt.caller_stream);
+    const hipError_t q = hipStreamQuery(caller);
+    if (q == hipSuccess)
+      return; // every earlier operation of the caller's stream has completed
+    if (q != hipErrorNotReady)
+      HIPCHECK(q);
+    HIPCHECK(hipEventRecord(ctx.start_ev, caller));
+    pending_ = true;
+  }
+  // Before an operation on `s` that touches the caller's memory.
+  void before(hipStream_t s) {
+    if (!pending_)
+      return;
+    for (int i = 0; i < kCopyStreams; ++i)
+      if (ctx_.copies[i] == s && waited_[i])
+        return;
+    const hipError_t q = hipEventQuery(ctx_.start_ev);
+    if (q == hipSuccess) {
+      pending_ = false;
+      return;
+    }
+    if (q != hipErrorNotReady)
+      HIPCHECK(q);
+    HIPCHECK(hipStreamWaitEvent(s, ctx_.start_ev, 0));
+    for (int i = 0; i < kCopyStreams; ++i)
+      if (ctx_.copies[i] == s)
+        waited_[i] = true;
+  }
+
+private:
+  Context &ctx_;
+  bool pending_ = false;
+  bool waited_[kCopyStreams] = {};
+};
 
 void ensure_wire(Context &ctx, size_t bytes) {
   if (ctx.wire_cap >= bytes)
@@ -367,9 +421,14 @@ void ensure_workers(Context &ctx, unsigned need, bool exact) {
   ctx.worker_threads = need;
 }
 
-void ensure_ring(Context &ctx, int n, size_t slot_bytes) {
+// The staging ring holds at least `n` slots of at least `slot_bytes`; true
+// when this call allocated it (false: the ring kept from earlier calls fits).
+// A new ring has exactly `n` slots: a call that stages one chunk gets one
+// (reference: min(nBuffers, chunks) slots, libreloc/src/Dispatch.cpp:
+// 524-531).
+bool ensure_ring(Context &ctx, int n, size_t slot_bytes) {
   if (static_cast<int>(ctx.slots.size()) >= n && ctx.slot_bytes >= slot_bytes)
-    return;
+    return false;
   // drain users of the old ring before freeing it
   for (hipEvent_t e : ctx.slot_ev)
     HIPCHECK(hipEventSynchronize(e));
@@ -380,8 +439,8 @@ void ensure_ring(Context &ctx, int n, size_t slot_bytes) {
   ctx.slots.clear();
   ctx.slot_ev.clear();
   const size_t round = size_t{1} << 20;
-  ctx.slot_bytes = std::max(ctx.slot_bytes, (slot_bytes + round - 1) / round * round);
-  const int want = std::max<int>(n, 2);
+  ctx.slot_bytes = (slot_bytes + round - 1) / round * round;
+  const int want = std::max<int>(n, 1);
   for (int i = 0; i < want; ++i) {
     void *p = nullptr;
     HIPCHECK(hipHostMalloc(&p, ctx.slot_bytes, hipHostMallocDefault));
@@ -392,6 +451,16 @@ void ensure_ring(Context &ctx, int n, size_t slot_bytes) {
     ctx.slot_ev.push_back(e);
   }
   ctx.slot_pending.assign(ctx.slots.size(), false);
+  return true;
+}
+
+// Copy streams a call spreads its chunks over: relx_options.n_streams 1
+// keeps every copy and kernel on one stream; 0 (default) and 2 or more use
+// the context's kCopyStreams.
+int call_streams(const relx_options &opt) {
+  if (opt.n_streams < 0)
+    throw Error("invalid_options", "n_streams must be >= 0 (0: the default)");
+  return opt.n_streams == 1 ? 1 : kCopyStreams;
 }
 
 // The host writes a staging slot only after the device work that last read
@@ -491,6 +560,7 @@ struct StaticScratch {
   int32_t *pi;
   const std::vector<float> *host_pf;
   const std::vector<int32_t> *host_pi;
+  hipEvent_t last; // the end of the device's previous static call (StaticDevice::last)
 };
 
 } // namespace
@@ -572,8 +642,10 @@ void execute_members(Context &ctx, int n, BoundHandle *const *bounds, const void
 void execute_static(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes, void *dst,
                     size_t dst_bytes, const relx_options &opt, relx_report *report) {
   DeviceGuard guard(ctx.device);
-  if (!ctx.scratch || !ctx.param_stage)
+  if (!ctx.stat || !ctx.param_stage)
     throw Error("backend_failure", "the static scratch is not mapped on this context's device");
+  // one static call at a time on the device, whatever the context
+  std::lock_guard<std::mutex> serial(ctx.stat->mu);
   const Bound &b = *h.bound;
   if (b.indexed)
     throw Error("plan_mismatch", "the allocation-free upload takes layout and typed plans; "
@@ -612,9 +684,10 @@ void execute_static(Context &ctx, BoundHandle &h, const void *src, size_t src_by
   std::vector<Member> ms{Member{&h, static_cast<const uint8_t *>(src), src_bytes,
                                 static_cast<uint8_t *>(dst), dst_bytes, report, 0, &dp, true, 0,
                                 false, dp.wire_bytes}};
-  uint8_t *tables = ctx.scratch + kScratchWireBytes;
-  const StaticScratch sc{ctx.scratch, kScratchWireBytes, reinterpret_cast<float *>(tables),
-                         reinterpret_cast<int32_t *>(tables + kParamStageHalf), &dp.pf, &dp.pi};
+  uint8_t *tables = ctx.stat->addr + kScratchWireBytes;
+  const StaticScratch sc{ctx.stat->addr, kScratchWireBytes, reinterpret_cast<float *>(tables),
+                         reinterpret_cast<int32_t *>(tables + kParamStageHalf), &dp.pf, &dp.pi,
+                         ctx.stat->last};
   execute(ctx, ms, opt, nullptr, nullptr, &sc);
 }
 
@@ -659,22 +732,23 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
       max_slot = std::max(max_slot, static_cast<size_t>(p.per_chunk * p.unit_wire));
     plans.push_back(p);
   }
-  int64_t total_chunks = 0;
-  for (const ChunkPlan &p : plans)
-    total_chunks += (p.units + p.per_chunk - 1) / p.per_chunk;
-  const bool two_streams = total_chunks > 1; // else one copy stream does everything
+  int64_t total_chunks = 0, staged = 0; // every chunk, the staged ones
+  for (size_t i = 0; i < ms.size(); ++i) {
+    const int64_t n = (plans[i].units + plans[i].per_chunk - 1) / plans[i].per_chunk;
+    total_chunks += n;
+    if (!ms[i].direct)
+      staged += n;
+  }
+  const int ns = call_streams(opt);
+  const bool two_streams = total_chunks > 1 && ns > 1; // else one copy stream does everything
   const int nslots = opt.n_buffers > 0 ? opt.n_buffers : 3;
   if (max_slot && sc)
     throw Error("invalid_options", "an allocation-free call has no staging ring");
-  if (max_slot)
-    ensure_ring(ctx, nslots, max_slot);
+  const bool ring_new =
+      max_slot && ensure_ring(ctx, static_cast<int>(std::min<int64_t>(nslots, staged)), max_slot);
   // A slot's event is needed when the call returns before its work
   // completes, or when a later chunk of this call reuses the slot (staged
   // chunk j takes slot j mod ring size).
-  int64_t staged = 0;
-  for (size_t i = 0; i < ms.size(); ++i)
-    if (!ms[i].direct)
-      staged += (plans[i].units + plans[i].per_chunk - 1) / plans[i].per_chunk;
   const bool early = comp != nullptr || opt.no_wait != 0;
   const int64_t nring = static_cast<int64_t>(ctx.slots.size());
   int64_t staged_no = 0; // staged chunks so far
@@ -697,16 +771,11 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
   // by an event from another stream); the copy streams join at the end.
   if (ctx.unsynced) // the previous call may still read the wire arena
     copy_streams_wait(ctx, ctx.done_ev);
-  // The caller's stream (0 being the legacy null stream) may still be
-  // producing the destination's previous users or a device source: every
-  // private stream starts after the work enqueued on it so far
+  // The caller's stream orders the call's kernels and direct copies
   // (libreloc/src/Dispatch.cpp:1995, libreloc/cuda/CudaBackend.cu:190-208).
   const bool ordered = opt.has_caller_stream != 0;
   hipStream_t caller = reinterpret_cast<hipStream_t>(opt.caller_stream);
-  if (ordered) {
-    HIPCHECK(hipEventRecord(ctx.start_ev, caller));
-    copy_streams_wait(ctx, ctx.start_ev);
-  }
+  CallerOrder order(ctx, opt);
   bool any_generic = false;
   for (const Member &m : ms)
     any_generic = any_generic || m.dp->family == kFamGeneric;
@@ -714,6 +783,14 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
   if (any_generic)
     clear_status(status);
   if (sc) {
+    // The scratch is free once the device's previous static call, from any
+    // context, has completed: the table copies wait for its end, and the
+    // other copy stream waits for them below.
+    const hipError_t q = hipEventQuery(sc->last);
+    if (q == hipErrorNotReady)
+      HIPCHECK(hipStreamWaitEvent(ctx.copies[0], sc->last, 0));
+    else if (q != hipSuccess)
+      HIPCHECK(q);
     // The parameter tables go to the scratch through the context's pinned
     // staging (a DMA, no runtime staging), ahead of every chunk's kernel.
     const size_t fb = sc->host_pf->size() * sizeof(float), ib = sc->host_pi->size() * sizeof(int32_t);
@@ -751,8 +828,9 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
       hipStream_t cs = ctx.copies[0];
       for (int64_t b0 = 0; b0 < p.units; b0 += p.per_chunk) {
         const int64_t n = std::min(p.per_chunk, p.units - b0);
-        cs = ctx.copy_stream(nchunk++);
+        cs = ctx.copy_stream(nchunk++, ns);
         if (m.direct) {
+          order.before(cs);
           HIPCHECK(hipMemcpyAsync(wire + b0, m.src + b0, static_cast<size_t>(n),
                                   hipMemcpyHostToDevice, cs));
         } else {
@@ -768,8 +846,9 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
         }
         ++chunks;
       }
-      if (chunks > 1)
+      if (chunks > 1 && ns > 1)
         join_copy_streams(ctx, cs, nchunk);
+      order.before(cs);
       launches = index_select_device(ctx, *m.h, wire, static_cast<size_t>(bd.table_bytes), m.dst,
                                      m.dst_bytes, cs);
     }
@@ -781,10 +860,11 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
       const int64_t v1 = std::min(p.units, v0 + p.per_chunk);
       const int64_t woff = v0 * p.unit_wire, wbytes = (v1 - v0) * p.unit_wire;
       const int64_t chunk_no = nchunk;
-      hipStream_t cs = ctx.copy_stream(nchunk++);
+      hipStream_t cs = ctx.copy_stream(nchunk++, ns);
       const uint8_t *kwire = wire; // what the batch's kernels read
       if (m.direct) {
         TraceRange tr("relx.h2d.submit", chunk_no);
+        order.before(cs);
         HIPCHECK(hipMemcpyAsync(wire + woff, m.src + woff, static_cast<size_t>(wbytes),
                                 hipMemcpyHostToDevice, cs));
       } else {
@@ -831,6 +911,7 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
         join_copy_streams(ctx, cs, nchunk);
       // Timing events bracket the batch's launches on the stream they run
       // on; the first completes when the batch's copies have landed.
+      order.before(cs);
       hipEvent_t *tev = timing ? timing_pair(ctx, tpairs++) : nullptr;
       if (tev)
         HIPCHECK(hipEventRecord(tev[0], cs));
@@ -862,6 +943,12 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
       r.kernel_launches = launches;
       r.wire_boundary = static_cast<int>(m.k);
       r.direct_dma = m.direct ? 1 : 0;
+      r.host_chunk_bytes = std::min(m.arena_bytes, p.per_chunk * p.unit_wire);
+      r.host_buffers = m.direct ? 0 : std::min(nring, chunks);
+      r.staging_bytes = staged ? nring * static_cast<int64_t>(ctx.slot_bytes) : 0;
+      r.staging_slots = staged ? nring : 0;
+      r.staging_reused = staged && !ring_new ? 1 : 0;
+      r.copy_streams = static_cast<int>(std::min<int64_t>(ns, total_chunks));
       sum.source_bytes += r.source_bytes;
       sum.wire_bytes += r.wire_bytes;
       sum.destination_bytes += r.destination_bytes;
@@ -869,14 +956,26 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
       sum.payload_bytes_transferred += r.payload_bytes_transferred;
       sum.chunks += r.chunks;
       sum.kernel_launches += r.kernel_launches;
+      sum.host_chunk_bytes = std::max(sum.host_chunk_bytes, r.host_chunk_bytes);
+      sum.direct_dma = mi == 0 ? r.direct_dma : sum.direct_dma && r.direct_dma;
+      sum.host_buffers = std::min(nring, staged);
+      sum.staging_bytes = r.staging_bytes;
+      sum.staging_slots = r.staging_slots;
+      sum.staging_reused = r.staging_reused;
+      sum.copy_streams = r.copy_streams;
     }
   }
   // join on the stream of the last chunk (the others are usually done)
-  hipStream_t last = nchunk > 0 ? ctx.copy_stream(nchunk - 1) : ctx.copies[0];
+  hipStream_t last = nchunk > 0 ? ctx.copy_stream(nchunk - 1, ns) : ctx.copies[0];
   if (two_streams)
     join_copy_streams(ctx, last, nchunk);
   HIPCHECK(hipEventRecord(ctx.done_ev, last));
-  if (ordered)
+  if (sc) // the next static call on the device writes the scratch after this
+    HIPCHECK(hipEventRecord(sc->last, last));
+  // A call that returns before its work completes orders the caller's
+  // stream after it; a blocking call has completed when it returns, so
+  // anything the caller enqueues next runs after it without a wait.
+  if (ordered && early)
     HIPCHECK(hipStreamWaitEvent(caller, ctx.done_ev, 0));
   if (total) {
     std::snprintf(sum.implementation, sizeof(sum.implementation), "hip_relayout_group");
@@ -1005,9 +1104,13 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
   const int64_t units = axis < 0 ? (out_bytes + plan.copy_bytes - 1) / plan.copy_bytes : plan.units;
   const int64_t row = axis < 0 ? plan.copy_bytes : plan.row, per = axis < 0 ? 1 : plan.per;
   const KArgs &a = dp.base;
-  const int nslots = opt.n_buffers > 0 ? opt.n_buffers : 3;
-  if (!pinned)
-    ensure_ring(ctx, nslots, static_cast<size_t>(std::min(per * row, out_bytes)));
+  const int64_t total_chunks = plan.outer * ((units + per - 1) / per);
+  // ring slots: n_buffers, at most one per chunk
+  const int nslots = static_cast<int>(
+      std::min<int64_t>(opt.n_buffers > 0 ? opt.n_buffers : 3, total_chunks));
+  const int ns = call_streams(opt);
+  const bool ring_new =
+      !pinned && ensure_ring(ctx, nslots, static_cast<size_t>(std::min(per * row, out_bytes)));
   const bool exact = opt.gather_threads > 0;
   const unsigned parts = exact ? static_cast<unsigned>(opt.gather_threads) : kStagingThreads;
   ensure_workers(ctx, parts, exact);
@@ -1015,13 +1118,11 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
     HIPCHECK(hipStreamWaitEvent(ctx.compute, ctx.done_ev, 0));
     copy_streams_wait(ctx, ctx.done_ev);
   }
-  const bool ordered = opt.has_caller_stream != 0;
-  hipStream_t caller = reinterpret_cast<hipStream_t>(opt.caller_stream);
-  if (ordered) { // the source is produced on the caller's stream (0: the null stream)
-    HIPCHECK(hipEventRecord(ctx.start_ev, caller));
-    HIPCHECK(hipStreamWaitEvent(ctx.compute, ctx.start_ev, 0));
-    copy_streams_wait(ctx, ctx.start_ev);
-  }
+  // The source is produced on the caller's stream (0: the null stream): the
+  // kernels run after it, and each copy waits on its chunk's kernel event,
+  // so the copies into the caller's destination follow too.
+  CallerOrder order(ctx, opt);
+  order.before(ctx.compute);
   int32_t *status = ctx.status + (ctx.status_next++ % kStatusSlots);
   if (dp.family == kFamGeneric)
     clear_status(status);
@@ -1065,7 +1166,7 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
       ev = (ev + 1) % kChunkEvents;
       HIPCHECK(hipEventRecord(ke, ctx.compute));
     }
-    hipStream_t cs = ctx.copy_stream(chunks);
+    hipStream_t cs = ctx.copy_stream(chunks, ns);
     HIPCHECK(hipStreamWaitEvent(cs, ke, 0));
     const int64_t off = (o * units + u0) * row;
     const int64_t bytes = std::min((u1 - u0) * row, out_bytes - off);
@@ -1086,10 +1187,9 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
   }
   while (next < pending.size())
     consume(pending[next++]);
-  join_copy_streams(ctx, ctx.copies[0], chunks);
+  join_copy_streams(ctx, ctx.copies[0], std::min<int64_t>(chunks, ns));
   HIPCHECK(hipEventRecord(ctx.done_ev, ctx.copies[0]));
-  if (ordered)
-    HIPCHECK(hipStreamWaitEvent(caller, ctx.done_ev, 0));
+  // blocking: the caller's stream needs no wait for work that has completed
   HIPCHECK(hipEventSynchronize(ctx.done_ev));
   ctx.unsynced = false;
   std::fill(ctx.slot_pending.begin(), ctx.slot_pending.end(), false);
@@ -1111,6 +1211,12 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
     r.kernel_launches = launches;
     r.wire_boundary = static_cast<int>(h.prep.stages.size());
     r.direct_dma = pinned ? 1 : 0;
+    r.host_chunk_bytes = std::min(per * row, out_bytes);
+    r.host_buffers = pinned ? 0 : nslots;
+    r.staging_bytes = pinned ? 0 : static_cast<int64_t>(ctx.slots.size() * ctx.slot_bytes);
+    r.staging_slots = pinned ? 0 : static_cast<int64_t>(ctx.slots.size());
+    r.staging_reused = !pinned && !ring_new ? 1 : 0;
+    r.copy_streams = static_cast<int>(std::min<int64_t>(ns, chunks));
   }
 }
 
@@ -1144,7 +1250,7 @@ std::unique_ptr<Context> make_context(int device, int64_t max_retained) {
     HIPCHECK(hipEventCreateWithFlags(&ctx->check_ev[i], hipEventDisableTiming));
   // set-up of the allocation-free upload: this device's scratch address and
   // the pinned staging of its parameter tables
-  ctx->scratch = scratch_address(device);
+  ctx->stat = &static_device(device);
   HIPCHECK(hipHostMalloc(reinterpret_cast<void **>(&ctx->param_stage), kScratchParamBytes,
                          hipHostMallocDefault));
   return ctx;

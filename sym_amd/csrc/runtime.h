@@ -266,12 +266,16 @@ struct KernelTimes {
 // downloads 6-13%.
 constexpr int kCopyStreams = RELX_COPY_STREAMS;
 
+struct StaticDevice; // the allocation-free upload's per-device state (below)
+
 struct Context {
   int device = 0;
   hipStream_t copies[kCopyStreams] = {};
   hipStream_t compute = nullptr;
-  hipStream_t copy_stream(int64_t chunk) const {
-    return copies[static_cast<size_t>(chunk % kCopyStreams)];
+  // The stream of chunk `chunk` when a call spreads its chunks over `ns`
+  // copy streams (1 or kCopyStreams).
+  hipStream_t copy_stream(int64_t chunk, int ns = kCopyStreams) const {
+    return copies[static_cast<size_t>(chunk % ns)];
   }
   std::vector<void *> slots;
   size_t slot_bytes = 0;
@@ -296,10 +300,11 @@ struct Context {
   bool time_kernels = false;
   KernelTimes kt;
   std::vector<hipEvent_t> time_ev; // timing event pairs, reused call to call
-  // The allocation-free upload: this device's copy of the static scratch
-  // (its address from hipGetSymbolAddress) and pinned staging for the
-  // parameter tables it uploads (kScratchParamBytes, allocated here).
-  uint8_t *scratch = nullptr;
+  // The allocation-free upload: this device's static state (its copy of the
+  // scratch, the event and lock its static calls share) and pinned staging
+  // for the parameter tables it uploads (kScratchParamBytes, allocated
+  // here).
+  StaticDevice *stat = nullptr;
   uint8_t *param_stage = nullptr;
   // Parameter tables by content: a fresh binding of a plan with the same
   // tables (the same plan and parameters, bound again for the next call)
@@ -335,9 +340,22 @@ constexpr size_t kScratchBytes = size_t{64} << 20;
 constexpr size_t kScratchParamBytes = size_t{1} << 20;
 constexpr size_t kScratchWireBytes = kScratchBytes - kScratchParamBytes;
 constexpr size_t kParamStageHalf = kScratchParamBytes / 2;
-// The device address of `device`'s copy of the scratch, found once per
-// device with hipGetSymbolAddress; call with `device` current.
-uint8_t *scratch_address(int device);
+// One device's share of the allocation-free upload, kept until the process
+// ends. Every context on the device uses it: a static call holds `mu` from
+// its checks to its return, its copies wait for `last` (recorded at the end
+// of the previous static call on the device, from any context) before they
+// write the scratch, and it records `last` again at its end. So calls from
+// several contexts or threads on one GPU take the scratch in turn, also
+// after a call that returned early (no_wait).
+struct StaticDevice {
+  uint8_t *addr = nullptr; // this device's copy of the scratch
+  hipEvent_t last = nullptr;
+  std::mutex mu;
+};
+// `device`'s static state: the scratch address from hipGetSymbolAddress and
+// the event, made on the first call for the device (a context's creation);
+// call with `device` current.
+StaticDevice &static_device(int device);
 
 // Bounds of Context::param_cache.
 constexpr size_t kParamCacheEntries = 4096;

@@ -371,15 +371,53 @@ def _resources_for(resources, device):
     return context_for(resources, max(0, device))
 
 
-def _pinning(pinning):
+def _staging_options(pinning, min_pinned_bytes):
+    """Validate the reference's staging options (parsePinning,
+    libreloc/python/PyPinning.h:6-15; min_pinned_bytes is an optional
+    size_t, libreloc/include/reloc/Transfer.h:136-141).
+
+    Here they choose nothing: this library stages every staged chunk
+    through its one retained ring of page-locked slots (the reference
+    allocates staging per call, page-locked or not by this policy, and its
+    unconfigured default is pageable). A staged source is read by the host
+    and sent from the ring; a page-locked source is sent by direct DMA when
+    direct_dense_upload allows it, whatever the policy. The values are
+    echoed in the report's staging rows."""
     if pinning not in ("auto", "pinned", "pageable"):
         raise ValueError("pinning must be auto, pinned or pageable")
-    # the source's own memory kind is probed; staging always goes through the
-    # context's pinned ring
-    return -1
+    if min_pinned_bytes is not None:
+        if isinstance(min_pinned_bytes, bool) or not hasattr(min_pinned_bytes, "__index__"):
+            raise TypeError("min_pinned_bytes must be an integer or None")
+        if not 0 <= min_pinned_bytes.__index__() < 1 << 64:
+            raise TypeError("min_pinned_bytes must be a byte count (0 <= n < 2**64)")
+    return pinning, min_pinned_bytes
 
 
-def _report(rep, request):
+def _retained_limit(resources):
+    """The owner's max_retained_bytes (None: no bound)."""
+    limits = getattr(resources, "_limits", None) or {}
+    return limits.get("retained_bytes")
+
+
+def _staging_rows(rep, staging):
+    """The staging row of a call that staged chunks (reference
+    StagingDecision rows, libreloc/python/PyPinning.h:16-36): the ring it
+    cycled through. memory_kind is always "pinned" (see _staging_options);
+    the reason is "forced_pinned" when the caller asked for that, else
+    "retained_pinned_ring"."""
+    if not rep["staging_slots"]:
+        return []
+    pinning, min_pinned_bytes, retained = staging
+    cap = rep["staging_bytes"]
+    return [{"policy": pinning, "memory_kind": "pinned", "wire_bytes": rep["wire_bytes"],
+             "staging_capacity_bytes": cap, "buffer_count": rep["staging_slots"],
+             "min_pinned_bytes": min_pinned_bytes,
+             "reason": "forced_pinned" if pinning == "pinned" else "retained_pinned_ring",
+             "retention_eligible": retained is None or cap <= retained,
+             "reused": bool(rep["staging_reused"])}]
+
+
+def _report(rep, request, staging):
     sel = request.selected
     return {"implementation": rep["implementation"], "policy": sel["policy"],
             "placement_reason": sel["placement_reason"], "method": "device_relayout",
@@ -393,8 +431,9 @@ def _report(rep, request):
             "host_kernel": "copy" if rep["implementation"] == "hip_table_gather" else
             "index_select" if request.template.bound.indexed else
             "host_stages" if rep["wire_boundary"] else "copy",
-            "host_chunks": rep["chunks"], "host_chunk_bytes": 0, "host_buffers": 0,
-            "kernel_launches": rep["kernel_launches"], "staging": []}
+            "host_chunks": rep["chunks"], "host_chunk_bytes": rep["host_chunk_bytes"],
+            "host_buffers": rep["host_buffers"], "copy_streams": rep["copy_streams"],
+            "kernel_launches": rep["kernel_launches"], "staging": _staging_rows(rep, staging)}
 
 
 def execute_dispatch(request, *, caller_stream=None, n_buffers=2, n_streams=2, gather_threads=1,
@@ -412,6 +451,7 @@ def execute_dispatch(request, *, caller_stream=None, n_buffers=2, n_streams=2, g
             raise ValueError("n_buffers must be >= 1")
         if n_streams < 1:
             raise ValueError("n_streams must be >= 1")
+        staging = _staging_options(pinning, min_pinned_bytes) + (_retained_limit(resources),)
         if gather_threads < 0:
             raise ValueError("gather_threads must be >= 0 (0 = all cores)")
         gather_threads = _gather_threads(gather_threads, gather_pool)
@@ -431,16 +471,17 @@ def execute_dispatch(request, *, caller_stream=None, n_buffers=2, n_streams=2, g
         # the ring instead of sent by direct DMA; pipeline=False: the whole
         # buffer is staged, then sent as one chunk (reference
         # TransferOptions, libreloc/include/reloc/Transfer.h:129-134)
-        source_pinned = _pinning(pinning) if direct_dense_upload or d2h else 0
+        # the source's own memory kind is probed (-1) unless direct DMA is off
+        source_pinned = -1 if direct_dense_upload or d2h else 0
         chunk = int(chunk_size or 0) if pipeline else 1 << 62
         rep = run(request.template.bound, src.address, src.capacity_bytes - src.offset_bytes,
                   dst.address, dst.capacity_bytes - dst.offset_bytes,
                   n_buffers=n_buffers, chunk_bytes=chunk,
                   host_stages=request.selected["host_stages"],
                   gather_threads=gather_threads, source_pinned=source_pinned,
-                  caller_stream=caller_stream)
+                  caller_stream=caller_stream, n_streams=n_streams)
         request.consumed = True
-        request.report = _report(rep, request)
+        request.report = _report(rep, request, staging)
         return dict(request.report)
     finally:
         request.executing = False
@@ -517,7 +558,7 @@ def execute_dispatch_group(group, *, caller_stream=None, gather_threads=8, gathe
     if gather_threads < 1 or not max_scratch_bytes:
         raise ValueError("gather_threads and max_scratch_bytes must be positive")
     gather_threads = _gather_threads(gather_threads, gather_pool)
-    _pinning(pinning)
+    staging = _staging_options(pinning, min_pinned_bytes) + (_retained_limit(resources),)
     _check_group_scratch(group, min(max_scratch_bytes, _live_limit(resources) or max_scratch_bytes))
     group.executing = True
     try:
@@ -533,14 +574,15 @@ def execute_dispatch_group(group, *, caller_stream=None, gather_threads=8, gathe
         items = []
         for r, rep in zip(group.items, reps):
             r.consumed = True
-            r.report = _report(rep, r)
+            r.report = _report(rep, r, staging)
             items.append(dict(r.report))
         group.consumed = True
         group.report = {"logical_transfers": len(items), "request_count": 1,
                         "completion_granularity": "group",
                         "payload_copy_calls": sum(i["host_chunks"] for i in items),
                         "kernel_launches": sum(i["kernel_launches"] for i in items),
-                        "output_bytes": total["destination_bytes"], "staging": [], "items": items}
+                        "output_bytes": total["destination_bytes"],
+                        "staging": _staging_rows(total, staging), "items": items}
         return dict(group.report)
     finally:
         group.executing = False
@@ -551,10 +593,11 @@ class DispatchCompletion:
     libreloc/python/PyDispatch.cpp:659-695): wait(), query() and
     wait_stream(stream). The group report is filled in once it completed."""
 
-    def __init__(self, group, native, items):
+    def __init__(self, group, native, items, staging):
         self.group = group
         self._native = native
         self._items = items
+        self._staging = staging
 
     def _finish(self):
         if self.group.consumed:
@@ -562,7 +605,7 @@ class DispatchCompletion:
         items = []
         for r, rep in zip(self._items, self._native.reports):
             r.consumed = True
-            r.report = _report(rep, r)
+            r.report = _report(rep, r, self._staging)
             items.append(dict(r.report))
         self.group.consumed = True
         self.group.report = {"logical_transfers": len(items), "request_count": 1,
@@ -570,7 +613,8 @@ class DispatchCompletion:
                              "payload_copy_calls": sum(i["host_chunks"] for i in items),
                              "kernel_launches": sum(i["kernel_launches"] for i in items),
                              "output_bytes": self._native.total["destination_bytes"],
-                             "staging": [], "items": items}
+                             "staging": _staging_rows(self._native.total, self._staging),
+                             "items": items}
 
     def wait(self):
         try:
@@ -611,7 +655,7 @@ def submit_dispatch_group(group, *, caller_stream=None, gather_threads=8, gather
     if gather_threads < 1 or not max_scratch_bytes:
         raise ValueError("gather_threads and max_scratch_bytes must be positive")
     gather_threads = _gather_threads(gather_threads, gather_pool)
-    _pinning(pinning)
+    staging = _staging_options(pinning, min_pinned_bytes) + (_retained_limit(resources),)
     _check_group_scratch(group, min(max_scratch_bytes, _live_limit(resources) or max_scratch_bytes))
     dev = max(0, group.items[0].destination.device)
     ctx = _resources_for(resources, dev)
@@ -627,4 +671,4 @@ def submit_dispatch_group(group, *, caller_stream=None, gather_threads=8, gather
     except Exception:
         group.executing = False
         raise
-    return DispatchCompletion(group, native, group.items)
+    return DispatchCompletion(group, native, group.items, staging)

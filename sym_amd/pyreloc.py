@@ -423,15 +423,16 @@ def bind_typed(plan, symbols, parameters):
 
 
 def _options(n_buffers=0, chunk_bytes=0, host_stages=-1, gather_threads=0, source_pinned=-1,
-             caller_stream=None, no_wait=False):
+             caller_stream=None, no_wait=False, n_streams=0):
     """Per-call options. `caller_stream` is a hipStream_t handle the call is
     ordered after (0 is the legacy null stream, torch's default stream);
     None means no producer stream, as the reference's caller_stream=None
-    (libreloc/python/PyDispatch.cpp:199-202)."""
+    (libreloc/python/PyDispatch.cpp:199-202). `n_streams`: 1 runs the call
+    on one copy stream; 0 (default) or more uses the context's two."""
     has = caller_stream is not None
     return N.relx_options(int(n_buffers), int(chunk_bytes), int(host_stages), int(gather_threads),
                           int(source_pinned), int(caller_stream) if has else 0,
-                          1 if no_wait else 0, 1 if has else 0)
+                          1 if no_wait else 0, 1 if has else 0, int(n_streams))
 
 
 class Context:
@@ -666,13 +667,32 @@ def measure_d2h(device=0, nbytes=256 << 20, iters=20, rounds=3):
 
 # The layout transfer API (sym_amd.transfer) and the typed dispatch API
 # (prepare_dispatch / execute_dispatch / groups, sym_amd.dispatch) are
-# re-exported here under pyreloc's names.
-from .transfer import (BufferView, DispatchResources, TransferRequest,  # noqa: E402,F401
-                       TransferResourceCache, cuda_enabled, cuda_pointer_device, execute_transfer,
-                       make_transfer, validate_transfer_source)
-from .dispatch import (Calibration, DispatchCompletion, DispatchRequest,  # noqa: E402,F401
-                       DispatchTemplate, GatherPool, GroupRequest, IndexSelectProgram, Resources,
-                       execute_dispatch, execute_dispatch_group, load_calibration,
-                       prepare_dispatch, prepare_dispatch_from_template, prepare_dispatch_group,
-                       prepare_dispatch_template, prepare_index_select_program, query_capability,
-                       select_dispatch, submit_dispatch_group)
+# re-exported here under pyreloc's names. They are looked up on first use
+# (module __getattr__), so any of the three modules can be imported first:
+# transfer and dispatch import this module themselves.
+_REEXPORTS = {
+    "transfer": ("BufferView", "DispatchResources", "TransferRequest", "TransferResourceCache",
+                 "cuda_enabled", "cuda_pointer_device", "execute_transfer", "make_transfer",
+                 "validate_transfer_source"),
+    "dispatch": ("Calibration", "DispatchCompletion", "DispatchRequest", "DispatchTemplate",
+                 "GatherPool", "GroupRequest", "IndexSelectProgram", "Resources",
+                 "execute_dispatch", "execute_dispatch_group", "load_calibration",
+                 "prepare_dispatch", "prepare_dispatch_from_template", "prepare_dispatch_group",
+                 "prepare_dispatch_template", "prepare_index_select_program", "query_capability",
+                 "select_dispatch", "submit_dispatch_group"),
+}
+_REEXPORTED = {name: mod for mod, names in _REEXPORTS.items() for name in names}
+
+
+def __getattr__(name):
+    mod = _REEXPORTED.get(name)
+    if mod is None:
+        raise AttributeError("module %r has no attribute %r" % (__name__, name))
+    import importlib
+    value = getattr(importlib.import_module("." + mod, __package__), name)
+    globals()[name] = value
+    return value
+
+
+def __dir__():
+    return sorted(set(globals()) | set(_REEXPORTED))

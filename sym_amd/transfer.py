@@ -43,6 +43,16 @@ def _direction(direction):
     return _DIRECTIONS[direction]
 
 
+def _integer(name, v, lo, hi):
+    """An integer argument in [lo, hi); anything else raises TypeError."""
+    if isinstance(v, bool) or not hasattr(v, "__index__"):
+        raise TypeError("BufferView: %s must be an integer, got %r" % (name, v))
+    v = v.__index__()
+    if not lo <= v < hi:
+        raise TypeError("BufferView: %s = %d is outside [%d, %d)" % (name, v, lo, hi))
+    return v
+
+
 class BufferView:
     """A framework buffer: the allocation it lives in (base, capacity) plus
     the logical view (offset, extents, element strides). kind is 'host' or
@@ -58,14 +68,18 @@ class BufferView:
             kind = "cuda"
         if kind not in ("host", "cuda"):
             raise ValueError("kind must be 'host' or 'cuda', got '%s'" % (kind,))
-        self.base = int(base)
-        self.capacity_bytes = int(capacity_bytes)
-        self.offset_bytes = int(offset_bytes)
-        self.extents = [int(e) for e in extents]
-        self.strides = [int(s) for s in strides]
-        self.element_size = int(element_size)
+        # the reference binds uintptr_t base, size_t capacity and offset,
+        # int64 extents and strides, uint32 element size and int device: a
+        # value those types cannot hold is refused as its binding refuses it
+        # (TypeError), never wrapped into range
+        self.base = _integer("base", base, 0, 1 << 64)
+        self.capacity_bytes = _integer("capacity_bytes", capacity_bytes, 0, 1 << 64)
+        self.offset_bytes = _integer("offset_bytes", offset_bytes, 0, 1 << 64)
+        self.extents = [_integer("extents", e, -(1 << 63), 1 << 63) for e in extents]
+        self.strides = [_integer("strides", s, -(1 << 63), 1 << 63) for s in strides]
+        self.element_size = _integer("element_size", element_size, 0, 1 << 32)
         self.kind = kind
-        self.device = int(device)
+        self.device = _integer("device", device, -(1 << 31), 1 << 31)
 
     @property
     def address(self):
@@ -446,7 +460,7 @@ def execute_transfer(request, *, caller_stream=None, n_buffers=4, n_streams=2, g
         request._consumed = True
         threads = gather_threads if gather_threads > 0 else (os.cpu_count() or 8)
         opt = _options(n_buffers=n_buffers, gather_threads=threads, host_stages=0,
-                       caller_stream=caller_stream)
+                       caller_stream=caller_stream, n_streams=n_streams)
         s, t = src.native(), dst.native()
         rep = N.relx_report()
         err = N.relx_err()
@@ -455,14 +469,16 @@ def execute_transfer(request, *, caller_stream=None, n_buffers=4, n_streams=2, g
                                          ctypes.byref(opt), ctypes.byref(rep), ctypes.byref(err)):
             _fail(err)
         r = rep.as_dict()
-        request._staging = [{
-            "policy": pinning, "memory_kind": "pinned",
-            "wire_bytes": r["wire_bytes"],
-            "staging_capacity_bytes": 0 if r["direct_dma"] else ctx.stats()["pinned_bytes"],
-            "buffer_count": 0 if r["direct_dma"] else n_buffers,
+        # the ring a staged transfer cycled through (none for direct DMA);
+        # this library's ring is always page-locked, whatever `pinning`
+        retained = (getattr(resources, "_limits", None) or {}).get("retained_bytes")
+        request._staging = [] if not r["staging_slots"] else [{
+            "policy": pinning, "memory_kind": "pinned", "wire_bytes": r["wire_bytes"],
+            "staging_capacity_bytes": r["staging_bytes"], "buffer_count": r["staging_slots"],
             "min_pinned_bytes": min_pinned_bytes,
-            "reason": "direct_dma" if r["direct_dma"] else "pinned_ring",
-            "retention_eligible": resources is not None, "reused": resources is not None}]
+            "reason": "forced_pinned" if pinning == "pinned" else "retained_pinned_ring",
+            "retention_eligible": retained is None or r["staging_bytes"] <= retained,
+            "reused": bool(r["staging_reused"])}]
         request.report = r
         return None
     finally:

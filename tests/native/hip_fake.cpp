@@ -650,6 +650,20 @@ hipError_t hipStreamSynchronize(hipStream_t stream) {
   return set_last(wait_stream(lk, resolve(stream)));
 }
 
+// Complete when every operation enqueued on the stream has run; the host is
+// then ordered after all of them, as after a synchronize.
+hipError_t hipStreamQuery(hipStream_t stream) {
+  std::lock_guard<std::mutex> g(g_mu);
+  ihipStream_t *s = resolve(stream);
+  if (g_sticky[s->device] != hipSuccess)
+    return set_last(g_sticky[s->device]);
+  if (!s->q.empty())
+    return hipErrorNotReady;
+  HostAgent &h = host_tick();
+  vjoin(h.vc, s->vc);
+  return hipSuccess;
+}
+
 hipError_t hipStreamWaitEvent(hipStream_t stream, hipEvent_t event, unsigned int) {
   std::lock_guard<std::mutex> g(g_mu);
   ihipStream_t *s = resolve(stream);
@@ -887,17 +901,27 @@ hipError_t copy16_launch(const void *src, void *dst, uint32_t n16, hipStream_t s
                                  [src, dst, n] { std::memcpy(dst, src, n); }));
 }
 
-uint8_t *scratch_address(int device) {
-  std::lock_guard<std::mutex> g(g_mu);
-  static uint8_t *scratch[8] = {};
+// The static state of noalloc.hip: the scratch as a device allocation of the
+// stand-in, and the event every static call on the device shares.
+StaticDevice &static_device(int device) {
+  static std::mutex mu; // not g_mu: the event is made through the stand-in's own calls
+  static StaticDevice *state[8] = {};
+  std::lock_guard<std::mutex> g(mu);
   if (device < 0 || device >= 8)
-    return nullptr;
-  if (!scratch[device]) {
-    scratch[device] = static_cast<uint8_t *>(raw_alloc(kScratchBytes));
-    g_allocs[reinterpret_cast<uintptr_t>(scratch[device])] =
-        Alloc{kScratchBytes, Mem::Device, device, false};
+    throw Error("backend_failure", "no such device");
+  if (!state[device]) {
+    auto *st = new StaticDevice;
+    {
+      std::lock_guard<std::mutex> gm(g_mu);
+      st->addr = static_cast<uint8_t *>(raw_alloc(kScratchBytes));
+      g_allocs[reinterpret_cast<uintptr_t>(st->addr)] =
+          Alloc{kScratchBytes, Mem::Device, device, false};
+    }
+    if (hipEventCreateWithFlags(&st->last, hipEventDisableTiming) != hipSuccess)
+      throw Error("backend_failure", "hipEventCreateWithFlags");
+    state[device] = st;
   }
-  return scratch[device];
+  return *state[device];
 }
 
 } // namespace relx

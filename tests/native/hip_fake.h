@@ -5,7 +5,7 @@
 // The stand-in implements the HIP calls the host sources make (memory,
 // streams, events, copies, pointer attributes) and the four device entry
 // points they launch through (relx::launch_box, relx::gather_launch,
-// relx::copy16_launch, relx::scratch_address). Streams are worker threads
+// relx::copy16_launch, relx::static_device). Streams are worker threads
 // that run their operations in order; events complete when their stream
 // reaches them. Device memory is host memory.
 //

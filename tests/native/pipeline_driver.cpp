@@ -24,10 +24,12 @@
 //            on the caller stream after the wire (table) was
 //            written on it
 //   static   relx_execute_h2d_static from a page-locked source
+//   static_pair  no_wait static calls alternating between two contexts on
+//            one device, then both synchronized
 //   threads  several host threads uploading at once, through one context
 //            (`shared=1`) or one context each
 // Options: pinned, chunk, nbuf, threads, hs (host stages), caller (none,
-// null, stream), nowait, repeat, members, twice, check, the fault knobs and
+// null, stream), nowait, streams (copy streams), repeat, members, twice, check, the fault knobs and
 // delays of fake_knobs, and devices / device (device count, context device).
 #include <chrono>
 #include <cstdio>
@@ -247,6 +249,7 @@ relx_options options_of(const Opts &o) {
   opt.gather_threads = static_cast<int>(o.get("threads", 0));
   opt.source_pinned = static_cast<int>(o.get("pinned", -1));
   opt.no_wait = static_cast<int>(o.get("nowait", 0));
+  opt.n_streams = static_cast<int>(o.get("streams", 0));
   return opt;
 }
 
@@ -636,6 +639,64 @@ void run_static(const Case &c, const Opts &o, Result &r, relx_ctx *ctx) {
   }
 }
 
+// Two contexts on one device alternate no_wait static calls (`repeat` in
+// all), each call into a destination of its own, then both contexts
+// synchronize: every call stages its wire in the device's one static
+// scratch, so each must start writing it only after the previous call,
+// from either context, has read it.
+void run_static_pair(const Case &c, const Opts &o, Result &r, relx_ctx *ctx) {
+  relx_ctx *other = nullptr;
+  relx_err ec{};
+  if (relx_ctx_create(0, -1, &other, &ec) != RELX_OK) {
+    r.notes.push_back(std::string("context: ") + ec.code);
+    return;
+  }
+  const size_t out = static_cast<size_t>(c.info.destination_bytes);
+  void *src = nullptr;
+  relx_err ea{};
+  relx_host_alloc(c.src.size(), &src, &ea);
+  fake_mark_user_pinned(src);
+  std::memcpy(src, c.src.data(), c.src.size());
+  const int repeat = static_cast<int>(o.get("repeat", 4));
+  std::vector<void *> dsts(static_cast<size_t>(repeat));
+  for (void *&d : dsts)
+    d = device_buffer(out, 0xA5);
+  std::vector<uint8_t> host(out);
+  arm();
+  bool ok = true;
+  for (int i = 0; i < repeat; ++i) {
+    relx_options opt = options_of(o);
+    opt.source_pinned = 1;
+    opt.no_wait = 1;
+    relx_err e{};
+    fake_call_begin();
+    const int rc = relx_execute_h2d_static(i % 2 ? other : ctx, c.bound, src, c.src.size(),
+                                           dsts[static_cast<size_t>(i)], out, &opt, &r.report, &e);
+    r.calls.push_back(call_of(rc, e));
+    ok = ok && rc == RELX_OK;
+  }
+  for (relx_ctx *x : {ctx, other}) {
+    relx_err e{};
+    const int rc = relx_ctx_synchronize(x, &e);
+    r.calls.push_back(call_of(rc, e));
+    ok = ok && rc == RELX_OK;
+  }
+  for (int i = 0; i < repeat && ok; ++i) {
+    void *d = dsts[static_cast<size_t>(i)];
+    fake_host_read(d, out, "host reads the result");
+    (void)hipMemcpy(host.data(), d, out, hipMemcpyDeviceToHost);
+    check(r, c, host.data(), out, o.get("check", 1) != 0);
+  }
+  relx_err e{};
+  if (relx_ctx_close(other, &e) != RELX_OK)
+    r.notes.push_back(std::string("close: ") + e.code);
+  if (ok) {
+    for (void *d : dsts)
+      (void)hipFree(d);
+    relx_host_free(src);
+  }
+}
+
 fake_knobs knobs_of(const Opts &o) {
   fake_knobs k{};
   k.fail_malloc_at = static_cast<int>(o.get("fail_malloc_at", 0));
@@ -716,6 +777,8 @@ int main() {
           run_device(c, o, r, ctx);
         else if (scenario == "static")
           run_static(c, o, r, ctx);
+        else if (scenario == "static_pair")
+          run_static_pair(c, o, r, ctx);
         else if (scenario == "threads")
           run_threads(c, o, r, ctx);
         else
@@ -749,7 +812,12 @@ int main() {
       js << (i ? "," : "") << jstr(fake_violation(i));
     js << "],\"report\":{\"implementation\":" << jstr(r.report.implementation) << ",\"chunks\":" << r.report.chunks
        << ",\"kernel_launches\":" << r.report.kernel_launches << ",\"direct_dma\":" << r.report.direct_dma
-       << ",\"wire_boundary\":" << r.report.wire_boundary << "},\"counts\":{\"copies\":" << counts.copies
+       << ",\"wire_boundary\":" << r.report.wire_boundary << ",\"wire_bytes\":" << r.report.wire_bytes
+       << ",\"host_chunk_bytes\":" << r.report.host_chunk_bytes
+       << ",\"host_buffers\":" << r.report.host_buffers << ",\"staging_bytes\":" << r.report.staging_bytes
+       << ",\"staging_slots\":" << r.report.staging_slots
+       << ",\"staging_reused\":" << r.report.staging_reused
+       << ",\"copy_streams\":" << r.report.copy_streams << "},\"counts\":{\"copies\":" << counts.copies
        << ",\"launches\":" << counts.launches << ",\"syncs\":" << counts.syncs
        << ",\"unemulated\":" << counts.unemulated << ",\"mallocs\":" << counts.mallocs
        << ",\"host_mallocs\":" << counts.host_mallocs << ",\"frees\":" << counts.frees

@@ -186,6 +186,39 @@ def test_upload_orders_and_results(driver, cases):
     assert max(r["report"]["chunks"] for r in chunked) >= 8
 
 
+def test_report_describes_the_schedule(driver, cases):
+    """The host side of the report (reference Report::hostChunkBytes,
+    hostBuffers and the staging rows) against the schedule each call ran:
+    16 MiB of f32 wire in 2 MiB chunks staged through a 3-slot ring (the
+    second call reuses it), sent by direct DMA, staged as one chunk (a ring
+    of one slot, as the reference sizes it: min(n_buffers, chunks)), and on
+    one copy stream."""
+    c = cases["c1big"]
+    M = 1 << 20
+    lines = ["h2d %s pinned=0 chunk=%d nbuf=3 threads=4 %s" % (c, 2 * M, DELAYS),
+             "h2d %s pinned=1 chunk=%d nbuf=3 threads=4 %s" % (c, 2 * M, DELAYS),
+             "h2d %s pinned=0 chunk=%d nbuf=2 threads=4 %s" % (c, 16 * M, DELAYS),
+             "h2d %s pinned=0 chunk=%d nbuf=2 threads=4 streams=1 %s" % (c, 2 * M, DELAYS),
+             "d2h %s pinned=0 chunk=%d nbuf=3 threads=4 %s" % (c, 4 * M, DELAYS)]
+    res = run(driver, lines)
+    for r in res:
+        ok(r)
+        assert r["checked"] == 2
+    rep = [r["report"] for r in res]
+    assert rep[0]["wire_bytes"] == 16 * M
+    assert (rep[0]["chunks"], rep[0]["host_chunk_bytes"], rep[0]["host_buffers"]) == (8, 2 * M, 3)
+    assert (rep[0]["staging_slots"], rep[0]["staging_bytes"], rep[0]["staging_reused"]) == (3, 6 * M, 1)
+    assert rep[0]["copy_streams"] == 2 and rep[0]["direct_dma"] == 0
+    assert (rep[1]["chunks"], rep[1]["host_chunk_bytes"], rep[1]["host_buffers"]) == (8, 2 * M, 0)
+    assert (rep[1]["staging_slots"], rep[1]["staging_bytes"], rep[1]["direct_dma"]) == (0, 0, 1)
+    assert (rep[2]["chunks"], rep[2]["host_chunk_bytes"], rep[2]["host_buffers"]) == (1, 16 * M, 1)
+    assert (rep[2]["staging_slots"], rep[2]["staging_bytes"], rep[2]["copy_streams"]) == (1, 16 * M, 1)
+    assert res[2]["pinned_bytes"] == 16 * M  # one slot: the ring the call needed, no more
+    assert (rep[3]["chunks"], rep[3]["copy_streams"], rep[3]["host_buffers"]) == (8, 1, 2)
+    assert (rep[4]["chunks"], rep[4]["host_chunk_bytes"], rep[4]["host_buffers"]) == (4, 4 * M, 3)
+    assert rep[4]["staging_slots"] == 3 and rep[4]["copy_streams"] == 2
+
+
 def test_large_chunks_and_the_last_batch(driver, cases):
     """16 MiB of source in chunks of 2 to 16 MiB: kernel batches of several
     chunks, the last chunk a batch of its own."""
@@ -285,6 +318,19 @@ def test_allocation_free_upload(driver, cases):
         ok(r)
 
 
+def test_allocation_free_calls_from_two_contexts(driver, cases):
+    """no_wait static calls alternating between two contexts on one device
+    share the device's static scratch: each call's copies into it wait for
+    the previous static call's end, whichever context made it (the checker
+    reports a copy that overwrites the scratch while a kernel of the other
+    context still reads it)."""
+    lines = ["static_pair %s repeat=%d %s" % (cases[name], n, DELAYS)
+             for name in ("c1", "fz2") for n in (2, 5)]
+    for r in run(driver, lines):
+        ok(r)
+        assert r["checked"] >= 2, r
+
+
 def test_parameter_tables_uploaded_once_per_context(driver, cases):
     """A fresh binding per call finds its parameter tables in the context:
     the calls allocate the wire arena and one table block, however many
@@ -327,7 +373,8 @@ def test_retained_scratch_bound(driver, cases):
         ok(r)
         assert (r["pinned_bytes"], r["device_bytes"]) == (0, 0)
         assert r["counts"]["mallocs"] == 4, r["counts"]  # a result buffer per call + the tables
-    assert [r["counts"]["host_mallocs"] for r in res] == [9, 0]
+    # the 1 MiB result crosses as one chunk: a ring of one slot per call
+    assert [r["counts"]["host_mallocs"] for r in res] == [3, 0]
 
 
 def test_small_staged_uploads_read_their_slot(driver, cases):

@@ -151,6 +151,46 @@ def test_dispatch_upload_options(resources, opts, pipeline_kind, chunks):
     assert np.array_equal(out.cpu().numpy(), _c5_want(x, s))
 
 
+def test_headline_schedule_end_to_end():
+    """C5 at B=64, S=4096 through execute_dispatch with the options of the
+    bench's steps (ordered after torch's stream, 8 staging threads, retained
+    resources), from a page-locked source (32 direct DMA chunks of 64 MiB,
+    kernel batches of 8, 8, ..., 6 and 2 batch entries) with 3 and with 2
+    ring slots, and from the pageable source with reloc_torch's 2 slots (64
+    staged chunks); every output byte equals the oracle (the reference checks
+    every eligible H2D row end to end, DispatchTest.cpp:883)."""
+    B, S = 64, 4096
+    plan = P.load_typed_plan(W.c5_plan().blob)
+    x, s = W.c5_input(B, S)
+    want = np.empty((B, 32, S, 128), np.int8)
+    for b0 in range(0, B, 2):
+        want[b0:b0 + 2] = _c5_want(x[b0:b0 + 2], s)
+    xp = torch.from_numpy(x).pin_memory()
+    pinned = P.BufferView(xp.data_ptr(), x.nbytes, 0, list(x.shape),
+                          [st // 2 for st in x.strides], 2, "host")
+    stream = torch.cuda.current_stream().cuda_stream
+    res = P.Resources(0)
+    try:
+        for view, slots, pipeline, chunks in ((pinned, 3, "direct_dma", 32),
+                                              (pinned, 2, "direct_dma", 32),
+                                              (host_view(x), 2, "pinned_ring", 64)):
+            out = torch.empty((B, 32, S, 128), dtype=torch.int8, device="cuda")
+            b = P.bind_typed(plan, {"B": B, "S": S}, W.param("scale", s))
+            say("headline schedule", pipeline, "slots", slots)
+            rep = P.execute_dispatch(P.prepare_dispatch(b, view, device_view(out), "h2d"),
+                                     caller_stream=stream, resources=res, gather_threads=8,
+                                     n_buffers=slots)
+            torch.cuda.synchronize()
+            assert rep["host_pipeline"] == pipeline and rep["host_chunks"] == chunks, rep
+            assert rep["kernel_launches"] == 9, rep
+            got = out.cpu().numpy()
+            for b0 in range(0, B, 8):
+                assert np.array_equal(got[b0:b0 + 8], want[b0:b0 + 8]), (pipeline, slots, b0)
+            del out, got
+    finally:
+        res.close()
+
+
 @pytest.mark.parametrize("limit", [0, 3 << 20])
 def test_retained_scratch_is_bounded(rng, limit):
     """max_retained_bytes of a resource cache: after each call the ring and

@@ -273,10 +273,11 @@ def _c4_expected_rows(q, s, rows):
     return f16_bits(O.dequantize_s8_f32(q[rows], s[rows, None], np.int32(0)))
 
 
-def test_c4_expert_group(ctx, rng):
+def test_c4_expert_group(ctx):
     """Two experts (6 matrices) as one grouped transfer at full size; every
-    element of 64 sampled rows per matrix checked, plus full-buffer equality
-    for the down projection (4096 x 14336)."""
+    element of every matrix checked against the oracle (gate/up [14336, 4096]
+    and down [4096, 14336]), in blocks of 2048 rows to bound the oracle's
+    memory."""
     pool = W.c4_pool(experts=2)
     plan = P.Plan(W.c4_plan().blob)
     bounds, srcs, dsts, outs = [], [], [], []
@@ -296,10 +297,9 @@ def test_c4_expert_group(ctx, rng):
     for e in range(2):
         for q, s in pool[e]:
             got = outs[i].cpu().numpy().view(np.uint16).reshape(q.shape)
-            rows = np.sort(rng.choice(q.shape[0], 64, replace=False))
-            assert np.array_equal(got[rows], _c4_expected_rows(q, s, rows)), (e, q.shape)
-            if q.shape[0] == 4096:
-                assert np.array_equal(got, _c4_expected_rows(q, s, np.arange(4096)))
+            for r0 in range(0, q.shape[0], 2048):
+                rows = np.arange(r0, min(q.shape[0], r0 + 2048))
+                assert np.array_equal(got[rows], _c4_expected_rows(q, s, rows)), (e, q.shape, r0)
             i += 1
 
 

@@ -269,6 +269,33 @@ def test_dispatch_resource_limits_reject_invalid_values(options):
         P.DispatchResources(**options)
 
 
+_VIEW = dict(base=1 << 20, capacity_bytes=4 << 20, offset_bytes=0, extents=[1024],
+             strides=[1], element_size=4, kind="host", device=-1)
+
+
+@pytest.mark.parametrize("field,value", [
+    ("base", -1), ("base", 1 << 64), ("capacity_bytes", -1), ("capacity_bytes", 1 << 64),
+    ("offset_bytes", -1), ("offset_bytes", 1 << 64), ("extents", [1 << 63]),
+    ("strides", [-(1 << 63) - 1]), ("element_size", -4), ("element_size", 1 << 32),
+    ("device", 1 << 31), ("base", 1.5), ("capacity_bytes", "4096"), ("offset_bytes", None)])
+def test_buffer_view_refuses_values_its_types_cannot_hold(field, value):
+    """The reference binds base as uintptr_t, capacity and offset as size_t,
+    extents and strides as int64, element size as uint32 and device as int
+    (PyTransfer.cpp:62-65,312-319): a negative capacity is refused there, not
+    wrapped into a 64-bit size that would turn the capacity checks off."""
+    with pytest.raises(TypeError):
+        P.BufferView(**dict(_VIEW, **{field: value}))
+
+
+def test_buffer_view_accepts_the_edges_of_its_types():
+    v = P.BufferView(**dict(_VIEW, base=(1 << 64) - 1, capacity_bytes=(1 << 64) - 1,
+                            offset_bytes=0, extents=[(1 << 63) - 1], strides=[-(1 << 63)],
+                            element_size=(1 << 32) - 1, device=-(1 << 31)))
+    assert v.base == (1 << 64) - 1 and v.extents == [(1 << 63) - 1]
+    v = P.BufferView(**dict(_VIEW, base=np.uint64(4096), capacity_bytes=np.int64(64)))
+    assert v.base == 4096 and v.capacity_bytes == 64 and type(v.base) is int
+
+
 def test_resource_limits_accept_zero_and_none():
     assert P.TransferResourceCache(max_retained_bytes=0, max_live_staging_bytes=None,
                                    acquire_timeout_ms=None).stats()["limits"]["retained_bytes"] == 0
