@@ -55,6 +55,10 @@ def parse():
     ap.add_argument("--e2e-samples", type=int, default=40)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-table", action="store_true",
+                    help="skip the per-config table of the bench line")
+    ap.add_argument("--table-samples", type=int, default=TABLE_SAMPLES,
+                    help="timed calls per config and source in the per-config table")
     ap.add_argument("--report", action="store_true", help="one JSON line per config")
     ap.add_argument("--configs", default="c1,c2,c3,c4,c5")
     ap.add_argument("--traffic-probe", action="store_true",
@@ -373,16 +377,48 @@ def first_call_ms(torch, P, case):
 
 
 def host_info():
-    model = ""
+    """The host's CPU as /proc/cpuinfo and sysfs describe it: the model
+    string in full (with family/model/stepping, since a virtual machine may
+    report only "AMD EPYC"), and how the affinity mask's CPUs map onto
+    physical cores (SMT siblings share a core's load/store units and its
+    memory bandwidth)."""
+    info, first = {}, True
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
+                if not line.strip():
+                    first = False
+                if first and ":" in line:
+                    k, v = (s.strip() for s in line.split(":", 1))
+                    if k in ("model name", "cpu family", "model", "stepping", "cpu MHz",
+                             "cache size", "siblings", "cpu cores"):
+                        info[k] = v
     except OSError:
         pass
-    return {"cpu_model": model, "nproc": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0))}
+    cpus = sorted(os.sched_getaffinity(0))
+    cores = set()
+    for c in cpus:
+        try:
+            base = "/sys/devices/system/cpu/cpu%d/topology/" % c
+            with open(base + "physical_package_id") as f:
+                pkg = f.read().strip()
+            with open(base + "core_id") as f:
+                cores.add((pkg, f.read().strip()))
+        except OSError:
+            cores.add(("?", str(c)))
+    mem = None
+    try:
+        with open("/proc/meminfo") as f:
+            mem = int(f.readline().split()[1]) * 1024
+    except (OSError, ValueError, IndexError):
+        pass
+    return {"cpu_model": info.get("model name", ""),
+            "cpu_id": "family %s model %s stepping %s" % (info.get("cpu family", "?"),
+                                                          info.get("model", "?"),
+                                                          info.get("stepping", "?")),
+            "cpu_mhz": info.get("cpu MHz"), "cache": info.get("cache size"),
+            "nproc": os.cpu_count(), "affinity_cpus": len(cpus),
+            "affinity_physical_cores": len(cores), "host_memory_bytes": mem}
 
 
 def hbm_copy_ceiling(torch, nbytes=1 << 30, iters=20):
@@ -840,6 +876,168 @@ def c4_report(torch, ctx, P, args, h2d_ceiling):
                            "steps": len(steps)}}
 
 
+# ------------------------------------------------------- per-config table
+
+# The reference's measurement protocol: 8 warm-up calls, then 100 samples,
+# p50 and p95 (bench/results/typed-h2d-221/README.md:23-26).
+TABLE_WARMUP, TABLE_SAMPLES = 8, 100
+
+
+def _calls(fn, samples, warmup=TABLE_WARMUP):
+    for _ in range(warmup):
+        rep = fn()
+    ts = []
+    for _ in range(samples):
+        t = time.perf_counter()
+        rep = fn()
+        ts.append(time.perf_counter() - t)
+    return float(np.percentile(ts, 50)), float(np.percentile(ts, 95)), rep
+
+
+def _e2e_row(p50, p95, rep, out_bytes, ceiling, samples):
+    return {"p50_ms": round(p50 * 1e3, 4), "p95_ms": round(p95 * 1e3, 4),
+            "effective_GBps": round(out_bytes / p50 / 1e9, 2), "wire_bytes": rep["wire_bytes"],
+            "pcie_frac": round(rep["wire_bytes"] / p50 / 1e9 / ceiling, 4),
+            "chunks": rep["chunks"], "implementation": rep["implementation"], "samples": samples}
+
+
+def config_table(torch, P, args, h2d_ceiling, c5_headline):
+    """BASELINE.json's five configs at full size, each measured in this run:
+
+    * `e2e_pageable` / `e2e_pinned`: relx_execute_h2d of the config's bound
+      plan from a pageable and from a page-locked copy of its source, with
+      the library's automatic choices, 8 warm-up calls, then p50/p95 of
+      `samples` calls; pcie_frac = wire bytes / p50 / the pinned H2D ceiling
+      measured at the start of this run. C4 is the grouped step (2 of 8
+      experts, 6 matrices) over 20 drawn steps, as the reference reports it;
+      C1 adds its small-N latencies on the one plan.
+    * `kernel`: the device relayout alone over resident buffers, launched
+      back to back on one stream between two events (`us`), against 8 TB/s
+      in algorithmic bytes (wire read + result written + parameters), and
+      against a 16-byte vector copy of the same bytes run in the same
+      process (`copy_GBps`, `of_copy`).
+
+    A fresh context; every end-to-end leg runs before any kernel or copy
+    leg, since large device frees can slow later pinned copies on streams
+    created before them."""
+    from sym_amd import workloads as W
+    samples = args.table_samples
+    ctx = P.Context(0)
+    names = ["c1", "c2", "c3"] + ["c5_%dx%d" % bs for bs in W.C5_SHAPES]
+    rows, kernels = {}, []
+    for name in names:
+        log("table: %s end to end" % name)
+        if name == "c5_%dx%d" % (HEADLINE_B, HEADLINE_S):
+            x, sc = c5_headline
+            case = Case(name, "C5 f16 [64,4096,32,128] -> [B,32,S,128] -> f32 -> int8 (per-head scale)",
+                        W.c5_plan().blob, {"B": HEADLINE_B, "S": HEADLINE_S}, W.param("scale", sc), x,
+                        widths=(2, 1))
+        else:
+            case = make_case(name)
+        big = case.wire_bytes >= (1 << 30)
+        n = max(10, samples // 4) if big else samples  # 2 GiB calls: 25 samples (40 ms each)
+        row = {"workload": case.workload, "kernel": case.kernel}
+        out = torch.empty(case.out_bytes, dtype=torch.uint8, device="cuda")
+        for pinned in (False, True):
+            if pinned:
+                held = torch.from_numpy(case.src.view(np.uint8).reshape(-1)).pin_memory()
+                ptr, nb = held.data_ptr(), held.numel()
+            else:
+                held, ptr, nb = None, case.src.ctypes.data, case.src.nbytes
+            p50, p95, rep = _calls(lambda: ctx.execute_h2d(case.bound, ptr, nb, out.data_ptr(),
+                                                           case.out_bytes,
+                                                           source_pinned=1 if pinned else 0), n)
+            row["e2e_pinned" if pinned else "e2e_pageable"] = _e2e_row(p50, p95, rep, case.out_bytes,
+                                                                       h2d_ceiling, n)
+            del held
+        del out
+        if name == "c1":
+            lat = {}
+            for small in (128, 192, 256):
+                sc1 = Case("c1", "C1 N=%d" % small, W.c1_plan().blob, {"s0": small}, None,
+                           W.c1_input(small))
+                o1 = torch.empty(sc1.out_bytes, dtype=torch.uint8, device="cuda")
+                p50, p95, _ = _calls(lambda: ctx.execute_h2d(sc1.bound, sc1.src.ctypes.data,
+                                                             sc1.src.nbytes, o1.data_ptr(),
+                                                             sc1.out_bytes), samples)
+                lat[str(small)] = {"p50_us": round(p50 * 1e6, 1), "p95_us": round(p95 * 1e6, 1)}
+            row["small_n_latency"] = lat
+        rows[name] = row
+        kernels.append((name, case.bound, case.wire_bytes, case.out_bytes))
+        del case
+    log("table: c4 grouped steps")
+    rows["c4"], c4_kernel = c4_table(torch, ctx, P, h2d_ceiling)
+    kernels.append(c4_kernel)
+    for name, bound, wire, out_bytes in kernels:
+        log("table: %s kernel" % name)
+        ms_step, kms = device_rate(torch, ctx, bound, wire, out_bytes, 200, 20)
+        alg = wire + out_bytes + bound.parameter_bytes
+        rows[name]["kernel"] = {"name": rows[name]["kernel"], "us": round(ms_step * 1e3, 3),
+                                "us_event_per_launch": round(kms * 1e3, 3),
+                                "algorithmic_bytes": alg,
+                                "GBps": round(alg / ms_step / 1e6, 1),
+                                "hbm_frac": round(alg / ms_step / 1e6 / HBM_PEAK_GBS, 4)}
+    for name, bound, wire, out_bytes in kernels:
+        k = rows[name]["kernel"]
+        copy = P.measure_copy(0, max(16, k["algorithmic_bytes"] // 2), 100, 3)
+        k["copy_GBps"] = round(copy, 1)
+        k["of_copy"] = round(k["GBps"] / copy, 4)
+    ctx.close()
+    order = ["c1", "c2", "c3", "c4"] + ["c5_%dx%d" % bs for bs in W.C5_SHAPES]
+    return {"protocol": "per config: %d warm-up calls, then p50/p95 of %d calls (25 for the 2 GiB "
+                        "C5 shape; C4: 20 grouped steps), pageable and page-locked sources; kernel: "
+                        "200 back-to-back launches between events over resident buffers, and a "
+                        "16-byte copy of the same bytes in the same run" % (TABLE_WARMUP, samples),
+            "pinned_h2d_ceiling_GBps": round(h2d_ceiling, 2),
+            "rows": {k: rows[k] for k in order}}
+
+
+def c4_table(torch, ctx, P, h2d_ceiling):
+    """C4 per step: 2 of 8 experts drawn uniformly, their 6 int8 matrices as
+    one grouped transfer (p50/p95 over 20 drawn steps after 3 warm-up
+    steps), from a pageable and from a page-locked expert pool; the kernel
+    leg is one gate matrix."""
+    from sym_amd import workloads as W
+    pool = W.c4_pool()
+    steps = W.c4_steps(20)
+    plan = P.Plan(W.c4_plan().blob)
+    bounds = {(e, j): P.Bound(plan, {"s0": q.shape[0], "s1": q.shape[1]}, W.param("scale", s))
+              for e in range(8) for j, (q, s) in enumerate(pool[e])}
+    dst = [torch.empty(bounds[(0, 0)].destination_bytes, dtype=torch.uint8, device="cuda")
+           for _ in range(6)]
+
+    def run(experts, pinned):
+        bl, sl, dl = [], [], []
+        for k, (e, j) in enumerate((e, j) for e in experts for j in range(3)):
+            q = pool[e][j][0]
+            bl.append(bounds[(e, j)])
+            sl.append((pinned[(e, j)].data_ptr(), q.nbytes) if pinned else (q.ctypes.data, q.nbytes))
+            dl.append((dst[k].data_ptr(), dst[k].numel()))
+        return ctx.execute_group_h2d(bl, sl, dl, source_pinned=1 if pinned else 0)[1]
+
+    row = {"workload": "C4 MoE: 2 of 8 experts x {gate,up [14336,4096], down [4096,14336]} int8 "
+                       "-> per-row dequant -> f16 (one grouped transfer per step)",
+           "kernel": bounds[(0, 0)].kernel}
+    for pinned in (None, True):
+        held = ({key: torch.from_numpy(pool[key[0]][key[1]][0]).pin_memory() for key in bounds}
+                if pinned else None)
+        for ex in steps[:3]:
+            run(ex, held)
+        ts = []
+        for ex in steps:
+            t = time.perf_counter()
+            tot = run(ex, held)
+            ts.append(time.perf_counter() - t)
+        p50, p95 = float(np.percentile(ts, 50)), float(np.percentile(ts, 95))
+        r = _e2e_row(p50, p95, tot, tot["destination_bytes"], h2d_ceiling, len(steps))
+        r["implementation"] = "hip_relayout_group (6 matrices)"
+        row["e2e_pinned" if pinned else "e2e_pageable"] = r
+        del held
+    del dst
+    b, q = bounds[(0, 0)], pool[0][0][0]
+    return row, ("c4", b, q.nbytes, b.destination_bytes)
+
+
 # ------------------------------------------------------------- headline
 
 HEADLINE_B, HEADLINE_S = 64, 4096  # C5 at its largest shape: 2 GiB f16 in, 1 GiB int8 out
@@ -887,15 +1085,14 @@ def cpu_reference_h2d(torch, blob, symbols, params, src, out_bytes, seconds, thr
                       % (n, el)}
 
 
-def headline(torch, P, args, h2d_ceiling):
+def headline(torch, P, args, h2d_ceiling, inputs):
     """C5 at B=64, S=4096 end to end: one step is one blocking call of the
     reference-shaped dispatch API from a pageable host tensor (fresh output
     allocation, bind, prepare, execute, completion), as the reference times
     its typed H2D rows (bench/results/typed-h2d-221/README.md:31-35)."""
     from sym_amd import workloads as W
     B, S = HEADLINE_B, HEADLINE_S
-    log("generating the C5 %dx%d input" % (B, S))
-    x, sc = W.c5_input(B, S)
+    x, sc = inputs
     blob = W.c5_plan().blob
     plan = P.load_typed_plan(blob)
     syms = {"B": B, "S": S}
@@ -906,12 +1103,12 @@ def headline(torch, P, args, h2d_ceiling):
     stream = torch.cuda.current_stream().cuda_stream
     res = P.Resources(0)
 
-    def step(view=src_view):
+    def step(view=src_view, resources=res, slots=RING_SLOTS):
         out = torch.empty((B, 32, S, 128), dtype=torch.int8, device="cuda")
         bound = P.bind_typed(plan, syms, params)
         req = P.prepare_dispatch(bound, view, device_view(P, out), "h2d")
-        rep = P.execute_dispatch(req, caller_stream=stream, resources=res,
-                                 gather_threads=GATHER_THREADS, n_buffers=RING_SLOTS)
+        rep = P.execute_dispatch(req, caller_stream=stream, resources=resources,
+                                 gather_threads=GATHER_THREADS, n_buffers=slots)
         return out, rep
 
     torch.cuda.synchronize()
@@ -978,6 +1175,27 @@ def headline(torch, P, args, h2d_ceiling):
     res.close()
     torch.cuda.synchronize()
 
+    # reloc_torch's default ring depth (execute_typed_transfer n_buffers=2,
+    # libreloc/python/reloc_torch/dispatch.py:260) on resources of its own,
+    # so that the ring holds exactly two slots
+    res2 = P.Resources(0)
+    for _ in range(3):
+        out, rep2 = step(resources=res2, slots=2)
+    del out
+    ts2 = []
+    torch.cuda.synchronize()
+    t2 = time.perf_counter()
+    for _ in range(max(5, args.steps // 2)):
+        ta = time.perf_counter()
+        out, rep2 = step(resources=res2, slots=2)
+        ts2.append(time.perf_counter() - ta)
+    torch.cuda.synchronize()
+    el2 = time.perf_counter() - t2
+    del out
+    res2.close()
+    torch.cuda.synchronize()
+    log("two ring slots: %.2f ms per step" % (el2 / len(ts2) * 1e3))
+
     log("pinned source p50 %.2f ms" % (q50 * 1e3))
     cpu = cpu_all = None
     if not args.no_cpu:
@@ -1017,9 +1235,21 @@ def headline(torch, P, args, h2d_ceiling):
                  "pinned_source": {"p50_ms": round(q50 * 1e3, 3),
                                    "effective_GBps": round(out_bytes / q50 / 1e9, 2),
                                    "frac": round(prep_rep["wire_bytes"] / q50 / 1e9 / h2d_ceiling, 4),
-                                   "implementation": prep_rep["implementation"]}},
+                                   "implementation": prep_rep["implementation"]},
+                 "two_ring_slots": {"steps": len(ts2), "value": round(out_bytes * len(ts2) / el2 / 1e9, 2),
+                                    "p50_ms": round(float(np.percentile(ts2, 50)) * 1e3, 3),
+                                    "frac": round(rep2["wire_bytes"] * len(ts2) / el2 / 1e9 / h2d_ceiling, 4),
+                                    "host_buffers": rep2["host_buffers"],
+                                    "note": "n_buffers=2, reloc_torch's default ring depth, on "
+                                            "resources of their own"},
+                 "staging": rep["staging"], "host_chunk_bytes": rep["host_chunk_bytes"],
+                 "host_buffers": rep["host_buffers"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": "profiles/traffic.json, committed: FETCH_SIZE + WRITE_SIZE "
+                                       "per dispatch of this launch from two rocprofv3 --pmc runs of "
+                                       "bench.py --traffic-probe --configs c5_e2e (counters need a "
+                                       "profiler run of their own; not measured in this run)",
                      "kernel": "k_permute<2, 1, 6, true> (f16 -> f32 -> int8, [B,S,32,128] -> [B,32,S,128], cached stores)",
                      "launch": "one kernel batch of the upload: %d batch entries [%d,%d,32,128]"
                                % (units, units, S),
@@ -1178,8 +1408,13 @@ def main():
         ctx.close()
         return
 
-    line = headline(torch, P, args, h2d_ceiling)
+    from sym_amd import workloads as W
+    log("generating the C5 %dx%d input" % (HEADLINE_B, HEADLINE_S))
+    inputs = W.c5_input(HEADLINE_B, HEADLINE_S)
+    line = headline(torch, P, args, h2d_ceiling, inputs)
     ctx.close()
+    if not args.no_table:
+        line["configs"] = config_table(torch, P, args, h2d_ceiling, inputs)
     print(json.dumps(line), flush=True)
 
 

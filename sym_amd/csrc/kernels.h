@@ -984,12 +984,6 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
   permute_body<WIN, WOUT, CH, CACHED_ST>(a);
 }
 
-// Chains whose permute fits eight waves without spilling registers: the
-// generic per-stage chain and the dequantizing chains over one-byte
-// sources do not (they spill hundreds of VGPRs under the bound).
-constexpr bool permute_eight_waves(int win, int ch) {
-  return ch != kChainGeneric && !(win == 1 && (ch == kChainDeqF16 || ch == kChainDeq));
-}
 
 // ------------------------------------------------------------ launch
 

@@ -53,6 +53,14 @@ enum ChainCode : int32_t {
   kChainQuant = 7,    // quantize
 };
 
+// Chains whose permute kernel fits eight waves per SIMD (64 VGPRs) without
+// spilling registers: the generic per-stage chain and the dequantizing
+// chains over one-byte sources do not (they spill hundreds of VGPRs under
+// the bound) and run at the occupancy their registers allow.
+constexpr bool permute_eight_waves(int win, int ch) {
+  return ch != kChainGeneric && !(win == 1 && (ch == kChainDeqF16 || ch == kChainDeq));
+}
+
 // Division by a runtime constant for n < 2^32: q = (umulhi(n, m) + n) >> s.
 struct FastDiv {
   uint32_t d, m, s, pad_;
