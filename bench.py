@@ -72,6 +72,8 @@ def parse():
     ap.add_argument("--summarize-stats", metavar="TRACE_DIR",
                     help="per-config kernel durations from a rocprofv3 --kernel-trace run of "
                          "--traffic-probe (its output line saved as TRACE_DIR/probe.json)")
+    ap.add_argument("--summarize-line", metavar="BENCH_LINE_FILE",
+                    help="markdown table of the per-config table (`configs`) of a saved bench line")
     ap.add_argument("--summarize-report", metavar="REPORT_FILE",
                     help="markdown tables (profiles/configs_report.md) from the saved output of "
                          "--report")
@@ -478,9 +480,50 @@ def traffic_for(config):
 CALIBRATION_BYTES = 256 << 20
 
 
+# Launches per config in --traffic-probe: warm-up launches (not counted by
+# the summaries), then timed ones, each config then a copy of its bytes.
+PROBE_WARM, PROBE_LAUNCHES = 20, 100
+
+
+def probe_bound(name):
+    """A config's bound plan and its boundary-0 wire and result bytes, for a
+    device-resident probe (no host input is generated)."""
+    from sym_amd import pyreloc as P
+    from sym_amd import workloads as W
+    rng = np.random.default_rng(SEED)
+    if name.startswith("c5_"):
+        b, s = (int(v) for v in name[3:].split("x"))
+        sc = rng.uniform(0.02, 0.05, 32).astype(np.float32)
+        bound = P.Bound(P.Plan(W.c5_plan().blob), {"B": b, "S": s}, W.param("scale", sc))
+        return bound, b * s * 4096 * 2, b * s * 4096, (2, 1)
+    case = make_case(name)
+    return case.bound, case.wire_bytes, case.out_bytes, (case.win, case.wout)
+
+
+def probe_launches(torch, ctx, bound, wire_bytes, out_bytes, n):
+    """`n` device relayouts back to back over rotating buffer sets larger
+    than the Infinity Cache (every launch reads and writes HBM)."""
+    per = wire_bytes + out_bytes
+    sets = max(2, min(16, int(np.ceil(600e6 / per))))
+    wires = [torch.empty(wire_bytes, dtype=torch.uint8, device="cuda") for _ in range(sets)]
+    outs = [torch.empty(out_bytes, dtype=torch.uint8, device="cuda") for _ in range(sets)]
+    for w in wires:
+        w.random_(0, 256)
+    stream = torch.cuda.Stream()
+    for i in range(n):
+        ctx.relayout_device(bound, wires[i % sets].data_ptr(), outs[i % sets].data_ptr(),
+                            stream=stream.cuda_stream)
+    torch.cuda.synchronize()
+    del wires, outs
+
+
 def traffic_probe(torch, ctx, names):
-    """A plain copy of known size, then 20 launches of each config's kernel
-    over rotating buffer sets; prints which kernel each config launches."""
+    """A plain copy of known size (the PMC calibration), then per config
+    PROBE_WARM + PROBE_LAUNCHES launches of its kernel over rotating buffer
+    sets and a 16-byte copy of the same algorithmic bytes; prints, in that
+    order, which kernel each config launches and how many times, for the
+    summaries of a rocprofv3 run of this probe (_assign)."""
+    from sym_amd import pyreloc as P
     a = torch.empty(CALIBRATION_BYTES, dtype=torch.uint8, device="cuda")
     b = torch.empty_like(a)
     a.random_(0, 256)
@@ -491,25 +534,25 @@ def traffic_probe(torch, ctx, names):
     kernels = {}
     for name in names:
         if name == "c5_e2e":
-            # the headline steps: each chunk's k_permute launch inside the upload
-            from sym_amd import pyreloc as P
+            # the headline steps: each kernel batch's k_permute launch inside
+            # the upload (the summaries keep the full batches, the most
+            # common grid)
             from sym_amd import workloads as W
             x, sc = W.c5_input(HEADLINE_B, HEADLINE_S)
             plan = P.load_typed_plan(W.c5_plan().blob)
             bound = P.bind_typed(plan, {"B": HEADLINE_B, "S": HEADLINE_S}, W.param("scale", sc))
             out = torch.empty(x.size, dtype=torch.int8, device="cuda")
-            for _ in range(3):
+            calls = 3
+            for _ in range(calls):
                 rep = ctx.execute_h2d(bound, x.ctypes.data, x.nbytes, out.data_ptr(), x.size)
-            # the typical launch (the median dispatch): a full batch of
-            # `units` batch entries (the last chunk is a launch of its own)
             units = max(1, min((256 << 20) // (HEADLINE_S * 4096 * 2), HEADLINE_B // 4))
             kernels[name] = {"family": "permute", "win": 2, "wout": 1, "output_bytes": x.size,
                              "algorithmic_bytes": units * HEADLINE_S * 4096 * 3 + sc.nbytes,
-                             "launches_per_call": rep["kernel_launches"]}
+                             "launches_per_call": rep["kernel_launches"],
+                             "dispatches": calls * rep["kernel_launches"]}
             del out, x
             continue
         if name in IX:
-            from sym_amd import pyreloc as P
             b, shape, sd, rd, idx = ix_bound(P, name)
             table = device_table(torch, shape, sd)
             bounds = [b] + [ix_bound(P, name, seed=SEED + s)[0] for s in range(1, IX_SETS)]
@@ -518,29 +561,30 @@ def traffic_probe(torch, ctx, names):
             op, nbi = ix_kernel(name)
             kernels[name] = {"family": "gather", "pattern": "k_gather<%d, %d," % (op, nbi),
                              "output_bytes": b.destination_bytes,
-                             "algorithmic_bytes": ix_alg_bytes(b, sd, rd, len(idx))}
+                             "algorithmic_bytes": ix_alg_bytes(b, sd, rd, len(idx)),
+                             "dispatches": 2 + 20 + 20, "skip": 2}  # gather_rate's launches
             continue
-        case = make_case(name)
-        device_rate(torch, ctx, case.bound, case.wire_bytes, case.out_bytes, 20, 2)
-        bi = case.bound
-        kernels[name] = {"family": case.kernel, "wire_bytes": case.wire_bytes,
-                         "output_bytes": case.out_bytes,
-                         "algorithmic_bytes": case.wire_bytes + case.out_bytes + bi.parameter_bytes,
-                         "win": case.win, "wout": case.wout}
+        bound, wire, out_bytes, (win, wout) = probe_bound(name)
+        probe_launches(torch, ctx, bound, wire, out_bytes, PROBE_WARM + PROBE_LAUNCHES)
+        alg = wire + out_bytes + bound.parameter_bytes
+        copy_bytes = max(16, alg // 2 // 16 * 16)
+        copy = P.measure_copy(0, copy_bytes, 20, 3)
+        kernels[name] = {"family": bound.kernel, "wire_bytes": wire, "output_bytes": out_bytes,
+                         "algorithmic_bytes": alg, "win": win, "wout": wout,
+                         "dispatches": PROBE_WARM + PROBE_LAUNCHES, "skip": PROBE_WARM,
+                         "copy_bytes": copy_bytes, "copy_GBps_events": round(copy, 1)}
     print(json.dumps({"calibration_bytes": CALIBRATION_BYTES, "kernels": kernels}), flush=True)
 
 
 def _pmc_rows(d, counter):
-    """(kernel name, counter value in bytes) per dispatch from a rocprofv3
-    --pmc CSV directory (values are KiB per dispatch)."""
+    """The rows of one counter (values in KiB per dispatch) from a rocprofv3
+    --pmc CSV directory."""
     import csv
     import glob
     rows = []
     for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
         with open(path) as f:
-            for r in csv.DictReader(f):
-                if r.get("Counter_Name") == counter:
-                    rows.append((r["Kernel_Name"], float(r["Counter_Value"]) * 1024.0))
+            rows += [r for r in csv.DictReader(f) if r.get("Counter_Name") == counter]
     return rows
 
 
@@ -697,30 +741,83 @@ def _kernel_pattern(info):
     import re
     if info.get("pattern"):
         return re.compile(re.escape(info["pattern"]))
-    return re.compile(r"k_%s(1p)?<%d, %d" % (info["family"], info["win"], info["wout"]))
+    return re.compile(r"k_%s(1p|8)?<%d, %d" % (info["family"], info["win"], info["wout"]))
+
+
+def _by_dispatch(rows):
+    return sorted(rows, key=lambda r: int(r["Dispatch_Id"]))
+
+
+def _assign(rows, probe):
+    """Each probed config's dispatches, in the probe's order: rows (one per
+    dispatch, in dispatch order) are walked once; a config takes the next
+    `dispatches` rows whose kernel name matches it (the first `skip` of them
+    are warm-up launches), then the run of k_copy16 dispatches of its
+    same-bytes copy that follows. Configs that share one kernel instance
+    (the C5 shapes) are told apart by this order."""
+    cur, out = 0, {}
+    for name, info in probe["kernels"].items():
+        pat, n = _kernel_pattern(info), info.get("dispatches")
+        taken, i = [], cur
+        while i < len(rows) and (n is None or len(taken) < n):
+            if pat.search(rows[i]["Kernel_Name"]):
+                taken.append(rows[i])
+            i += 1
+        copies = []
+        if info.get("copy_bytes"):
+            while i < len(rows) and "k_copy16" not in rows[i]["Kernel_Name"]:
+                i += 1
+            while i < len(rows) and "k_copy16" in rows[i]["Kernel_Name"]:
+                copies.append(rows[i])
+                i += 1
+        cur = i
+        out[name] = (taken[info.get("skip", 0):], copies)
+    return out
+
+
+def _grid(r):
+    return int(r.get("Grid_Size_X") or r.get("Grid_Size"))
+
+
+def _mode_grid(rows):
+    """The most common launch grid (threads) of the rows, and the rows of it."""
+    if not rows:
+        return 0, []
+    grids = [_grid(r) for r in rows]
+    g = max(set(grids), key=grids.count)
+    return g, [r for r in rows if _grid(r) == g]
 
 
 def summarize_stats(d, probe):
     """Per-config kernel durations from a rocprofv3 --kernel-trace run of
     --traffic-probe (its output line saved as d/probe.json): each config's
-    dispatches (matched by kernel name as in summarize_pmc), their mean and
-    median duration, and the algorithmic bytes over the mean as a fraction
-    of 8 TB/s. Prints a markdown table."""
-    rows = [(r["Kernel_Name"], (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
-            for r in _csv_rows(d, "kernel_trace.csv")]
-    lines = ["| config | kernel | dispatches | mean us | median us | algorithmic bytes | "
-             "achieved GB/s | of 8 TB/s |", "|---|---|---:|---:|---:|---:|---:|---:|"]
-    for name, info in probe["kernels"].items():
-        pat = _kernel_pattern(info)
-        us = [t for k, t in rows if pat.search(k)]
-        if not us:
+    timed dispatches (assigned in dispatch order, _assign) at their most
+    common grid, their mean and median duration, the algorithmic bytes over
+    the mean against 8 TB/s, and the 16-byte copy of the same bytes that the
+    probe ran right after them (median duration, the same bytes over it, and
+    the kernel's rate as a fraction of the copy's). Prints a markdown table."""
+    rows = _by_dispatch(_csv_rows(d, "kernel_trace.csv"))
+    us = lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+    lines = ["| config | kernel | grid (threads) | dispatches | mean us | median us | algorithmic "
+             "bytes | achieved GB/s | of 8 TB/s | copy median us | copy GB/s | of copy |",
+             "|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    for name, (krows, crows) in _assign(rows, probe).items():
+        grid, krows = _mode_grid(krows)
+        if not krows:
             continue
-        kernel = next(k for k, _ in rows if pat.search(k)).replace("void relx::(anonymous namespace)::", "")
-        mean = float(np.mean(us))
-        alg = info["algorithmic_bytes"]
-        lines.append("| %s | `%s` | %d | %.2f | %.2f | %d | %.1f | %.3f |" % (
-            name, kernel.split("(")[0], len(us), mean, float(np.median(us)), alg, alg / mean / 1e3,
-            alg / mean / 1e3 / HBM_PEAK_GBS))
+        info = probe["kernels"][name]
+        kernel = krows[0]["Kernel_Name"].replace("void relx::(anonymous namespace)::", "")
+        t = [us(r) for r in krows]
+        mean, alg = float(np.mean(t)), info["algorithmic_bytes"]
+        gbs = alg / mean / 1e3
+        copy = "| | |"
+        if crows:
+            cm = float(np.median([us(r) for r in crows]))
+            cgbs = alg / cm / 1e3
+            copy = "%.2f | %.1f | %.3f |" % (cm, cgbs, gbs / cgbs)
+        lines.append("| %s | `%s` | %d | %d | %.2f | %.2f | %d | %.1f | %.3f | %s" % (
+            name, kernel.split("(")[0], grid, len(t), mean, float(np.median(t)), alg, gbs,
+            gbs / HBM_PEAK_GBS, copy))
     print("\n".join(lines))
 
 
@@ -730,24 +827,27 @@ def summarize_pmc(fetch_dir, write_dir, probe):
     out = {"calibration_bytes": probe["calibration_bytes"], "configs": {}}
     med = {}
     for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
-        rows = _pmc_rows(d, counter)
-        cal = [v for k, v in rows if "copyBuffer" in k and v > probe["calibration_bytes"] / 4]
+        rows = _by_dispatch(_pmc_rows(d, counter))
+        cal = [float(r["Counter_Value"]) * 1024.0 for r in rows if "copyBuffer" in r["Kernel_Name"]
+               and float(r["Counter_Value"]) * 1024.0 > probe["calibration_bytes"] / 4]
         if not cal:
             raise SystemExit("no calibration copy dispatches for %s in %s" % (counter, d))
         factor = probe["calibration_bytes"] / float(np.median(cal))
         out[counter + "_calibration_factor"] = round(factor, 4)
-        for name, info in probe["kernels"].items():
-            pat = _kernel_pattern(info)
-            vals = [v for k, v in rows if pat.search(k)]
-            if vals:
+        for name, (krows, _) in _assign(rows, probe).items():
+            grid, krows = _mode_grid(krows)
+            if krows:
+                vals = [float(r["Counter_Value"]) * 1024.0 for r in krows]
                 med.setdefault(name, {})[counter] = float(np.median(vals)) * factor
-                med[name]["kernel"] = next(k for k, v in rows if pat.search(k))
+                med[name]["kernel"] = krows[0]["Kernel_Name"]
                 med[name]["dispatches"] = len(vals)
+                med[name]["grid"] = grid
     for name, m in med.items():
         if "FETCH_SIZE" in m and "WRITE_SIZE" in m:
             alg = probe["kernels"][name]["algorithmic_bytes"]
             t = m["FETCH_SIZE"] + m["WRITE_SIZE"]
             out["configs"][name] = {"kernel": m["kernel"], "dispatches": m["dispatches"],
+                                    "grid_threads": m["grid"],
                                     "fetch_factor": out["FETCH_SIZE_calibration_factor"],
                                     "write_factor": out["WRITE_SIZE_calibration_factor"],
                                     "fetch_bytes": round(m["FETCH_SIZE"]),
@@ -1269,6 +1369,29 @@ def headline(torch, P, args, h2d_ceiling, inputs):
     }
 
 
+def summarize_line(path):
+    """Markdown tables of the per-config table of a saved bench line (the
+    `configs` key of the default run's JSON line)."""
+    with open(path) as f:
+        d = json.loads([l for l in f.read().splitlines() if l.startswith("{")][-1])
+    t = d["configs"]
+    out = ["Protocol: %s. Pinned H2D ceiling measured in the same run: **%.2f GB/s**." % (
+        t["protocol"], t["pinned_h2d_ceiling_GBps"]), "",
+        "| config | pageable p50 ms | p95 ms | PCIe frac | pinned p50 ms | p95 ms | PCIe frac | "
+        "output GB/s (pinned) | kernel us | of 8 TB/s | same-run copy GB/s | of copy |",
+        "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    for name, r in t["rows"].items():
+        a, b, k = r["e2e_pageable"], r["e2e_pinned"], r["kernel"]
+        out.append("| %s | %.3f | %.3f | %.3f | %.3f | %.3f | %.3f | %.2f | %.2f | %.3f | %.0f | %.3f |" % (
+            name, a["p50_ms"], a["p95_ms"], a["pcie_frac"], b["p50_ms"], b["p95_ms"], b["pcie_frac"],
+            b["effective_GBps"], k["us"], k["hbm_frac"], k["copy_GBps"], k["of_copy"]))
+    lat = t["rows"]["c1"].get("small_n_latency")
+    if lat:
+        out += ["", "C1 small N (latency-bound), end-to-end p50 / p95 us: " + ", ".join(
+            "N=%s: %.1f / %.1f" % (n, v["p50_us"], v["p95_us"]) for n, v in lat.items())]
+    print("\n".join(out))
+
+
 def summarize_report(path):
     """The per-config tables of profiles/configs_report.md from the saved
     output of --report: device-resident kernel rates, end-to-end uploads from
@@ -1319,6 +1442,9 @@ def main():
     args = parse()
     if args.summarize_report:
         summarize_report(args.summarize_report)
+        return
+    if args.summarize_line:
+        summarize_line(args.summarize_line)
         return
     if args.summarize_stats:
         with open(os.path.join(args.summarize_stats, "probe.json")) as f:

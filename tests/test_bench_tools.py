@@ -49,15 +49,16 @@ def test_kernel_pattern(name, info, hit):
 def test_summarize_pmc_scales_by_the_calibration_copy(tmp_path):
     """FETCH_SIZE reads half a copy's bytes on this part: the factor from
     the calibration copy restores them; medians per dispatch."""
-    fields = ["Kernel_Name", "Counter_Name", "Counter_Value"]
+    fields = ["Dispatch_Id", "Grid_Size", "Kernel_Name", "Counter_Name", "Counter_Value"]
     cal = 1 << 20
     for counter, d, cal_kib, kib in (("FETCH_SIZE", "f", cal / 2 / 1024, [100.0, 101.0, 500.0]),
                                      ("WRITE_SIZE", "w", cal / 1024, [50.0, 50.0, 50.0])):
         os.makedirs(tmp_path / d)
-        rows = [{"Kernel_Name": "__amd_rocclr_copyBuffer", "Counter_Name": counter,
-                 "Counter_Value": cal_kib}]
-        rows += [{"Kernel_Name": "void relx::k_permute<2, 1, 6, true>(relx::KArgs)",
-                  "Counter_Name": counter, "Counter_Value": v} for v in kib]
+        rows = [{"Dispatch_Id": 1, "Grid_Size": 4096, "Kernel_Name": "__amd_rocclr_copyBuffer",
+                 "Counter_Name": counter, "Counter_Value": cal_kib}]
+        rows += [{"Dispatch_Id": 2 + i, "Grid_Size": 1024,
+                  "Kernel_Name": "void relx::k_permute8<2, 1, 6, true>(relx::KArgs)",
+                  "Counter_Name": counter, "Counter_Value": v} for i, v in enumerate(kib)]
         write_csv(tmp_path / d / "x_counter_collection.csv", fields, rows)
     probe = {"calibration_bytes": cal, "kernels": {
         "c5": {"family": "permute", "win": 2, "wout": 1, "algorithmic_bytes": 300 * 1024}}}
@@ -66,6 +67,43 @@ def test_summarize_pmc_scales_by_the_calibration_copy(tmp_path):
     c = out["configs"]["c5"]
     assert c["fetch_bytes"] == 2 * 101 * 1024 and c["write_bytes"] == 50 * 1024
     assert c["dispatches"] == 3 and c["traffic_over_algorithmic"] == round(252 / 300, 4)
+    assert c["grid_threads"] == 1024
+
+
+def test_probe_dispatches_are_assigned_in_order(tmp_path, capsys):
+    """Two C5 shapes launch the same kernel instance: the trace is split by
+    dispatch order (each config's warm-up launches dropped, then the copy of
+    its bytes that follows it); kernel rates against 8 TB/s and the copy."""
+    us = 1000
+    rows, d = [], 0
+
+    def add(name, grid, dur):
+        nonlocal d
+        d += 1
+        rows.append({"Dispatch_Id": d, "Kernel_Name": name, "Grid_Size_X": grid,
+                     "Start_Timestamp": 0, "End_Timestamp": int(dur * us)})
+    add("__amd_rocclr_copyBuffer", 4096, 50)
+    for dur in (20, 10, 10, 12):                       # config a: 1 warm-up + 3
+        add("void relx::k_permute8<2, 1, 6, true>(relx::KArgs)", 512, dur)
+    add("__amd_rocclr_fillBufferAligned", 256, 1)      # the copy's buffer fill
+    for dur in (8, 8, 8):
+        add("void relx::k_copy16(...)", 768, dur)
+    for dur in (30, 40, 40, 40):                       # config b: the same kernel, other grid
+        add("void relx::k_permute8<2, 1, 6, false>(relx::KArgs)", 2048, dur)
+    for dur in (36, 36):
+        add("void relx::k_copy16(...)", 3072, dur)
+    write_csv(tmp_path / "p_kernel_trace.csv", list(rows[0]), rows)
+    k = {"family": "permute", "win": 2, "wout": 1, "dispatches": 4, "skip": 1, "copy_bytes": 1}
+    probe = {"kernels": {"a": dict(k, algorithmic_bytes=100000),
+                         "b": dict(k, algorithmic_bytes=400000)}}
+    bench.summarize_stats(str(tmp_path), probe)
+    out = capsys.readouterr().out.splitlines()
+    a = next(l for l in out if l.startswith("| a |")).split("|")
+    b = next(l for l in out if l.startswith("| b |")).split("|")
+    assert a[3].strip() == "512" and a[4].strip() == "3" and float(a[5]) == round(32 / 3, 2)
+    assert float(a[10]) == 8.0 and float(a[12]) == round((100000 / (32 / 3) / 1e3) / (100000 / 8 / 1e3), 3)
+    assert b[3].strip() == "2048" and b[4].strip() == "3" and float(b[5]) == 40.0
+    assert float(b[10]) == 36.0
 
 
 def test_summarize_trace_headline_timeline(tmp_path, capsys):
