@@ -83,6 +83,40 @@ bool have_f16c() {
   return ok;
 }
 
+// A copy into a staging slot with streaming (non-temporal) stores: the slot
+// is read next by the DMA engine, not by this core, and the stores skip the
+// read-for-ownership of every destination line that a plain copy pays.
+// Measured on the box's host (Zen 5, 32 MiB L3), 8 threads: a 32 MiB chunk
+// of a source that is not in cache 430 -> 334 us; 8 MiB equal; a 2 MiB
+// cache-resident chunk 8.6 -> 11.3 us, so only long ranges take it.
+__attribute__((target("avx2"))) void copy_streaming(uint8_t *d, const uint8_t *s, size_t n) {
+  size_t i = 0;
+  while (i < n && (reinterpret_cast<uintptr_t>(d + i) & 31))
+    d[i] = s[i], ++i;
+  for (; i + 128 <= n; i += 128) {
+    const __m256i a = _mm256_loadu_si256(reinterpret_cast<const __m256i *>(s + i));
+    const __m256i b = _mm256_loadu_si256(reinterpret_cast<const __m256i *>(s + i + 32));
+    const __m256i c = _mm256_loadu_si256(reinterpret_cast<const __m256i *>(s + i + 64));
+    const __m256i e = _mm256_loadu_si256(reinterpret_cast<const __m256i *>(s + i + 96));
+    _mm256_stream_si256(reinterpret_cast<__m256i *>(d + i), a);
+    _mm256_stream_si256(reinterpret_cast<__m256i *>(d + i + 32), b);
+    _mm256_stream_si256(reinterpret_cast<__m256i *>(d + i + 64), c);
+    _mm256_stream_si256(reinterpret_cast<__m256i *>(d + i + 96), e);
+  }
+  for (; i < n; ++i)
+    d[i] = s[i];
+  _mm_sfence(); // the streaming stores are visible before the slot's copy is issued
+}
+
+bool have_avx2() {
+  static const bool ok = __builtin_cpu_supports("avx2");
+  return ok;
+}
+
+#ifndef RELX_STREAMING_STAGE_BYTES
+#define RELX_STREAMING_STAGE_BYTES (size_t{2} << 20)
+#endif
+
 } // namespace
 
 void host_transform(const Prepared &p, uint32_t k, uint32_t src_width, const void *src,
@@ -90,7 +124,13 @@ void host_transform(const Prepared &p, uint32_t k, uint32_t src_width, const voi
   const uint8_t *s = static_cast<const uint8_t *>(src);
   uint8_t *d = static_cast<uint8_t *>(dst);
   if (k == 0) {
-    std::memcpy(d + e0 * src_width, s + e0 * src_width, static_cast<size_t>(e1 - e0) * src_width);
+    const size_t n = static_cast<size_t>(e1 - e0) * src_width;
+    // a worker's range of at least RELX_STREAMING_STAGE_BYTES (a chunk of
+    // 16 MiB and more over 8 workers) streams its stores
+    if (n >= RELX_STREAMING_STAGE_BYTES && have_avx2())
+      copy_streaming(d + e0 * src_width, s + e0 * src_width, n);
+    else
+      std::memcpy(d + e0 * src_width, s + e0 * src_width, n);
     return;
   }
   if (k == 1 && p.stages[0].op == kOpF32toF16 && have_f16c()) {
