@@ -1350,7 +1350,7 @@ def headline(torch, P, args, h2d_ceiling, inputs):
                                        "per dispatch of this launch from two rocprofv3 --pmc runs of "
                                        "bench.py --traffic-probe --configs c5_e2e (counters need a "
                                        "profiler run of their own; not measured in this run)",
-                     "kernel": "k_permute<2, 1, 6, true> (f16 -> f32 -> int8, [B,S,32,128] -> [B,32,S,128], cached stores)",
+                     "kernel": "k_permute8<2, 1, 6, true> (f16 -> f32 -> int8, [B,S,32,128] -> [B,32,S,128], eight waves per SIMD, cached stores)",
                      "launch": "one kernel batch of the upload: %d batch entries [%d,%d,32,128]"
                                % (units, units, S),
                      "kernel_ms_per_launch_events": round(kernel_ms, 5),

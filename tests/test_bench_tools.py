@@ -35,6 +35,8 @@ def test_union_of_intervals():
      {"family": "permute", "win": 2, "wout": 1}, True),
     ("void relx::(anonymous namespace)::k_permute<2, 1, 6, false>(relx::KArgs)",
      {"family": "permute", "win": 2, "wout": 1}, True),
+    ("void relx::(anonymous namespace)::k_permute8<2, 1, 6, true>(relx::KArgs)",
+     {"family": "permute", "win": 2, "wout": 1}, True),
     ("void relx::(anonymous namespace)::k_interleave1p<4, 2, 4, 2>(unsigned char const*)",
      {"family": "interleave", "win": 4, "wout": 2}, True),
     ("void relx::(anonymous namespace)::k_transpose<4, 4, 1>(relx::KArgs)",
