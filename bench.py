@@ -296,11 +296,22 @@ def ix_config(torch, ctx, P, name, args, h2d_ceiling):
 
 # ----------------------------------------------------------- measurements
 
+# Bytes the rotating buffer sets of a device-rate measurement span: eight
+# times the MI355X's 256 MB Infinity Cache (MALL). With fewer, a launch
+# rewrites result lines still held there from the previous pass, which never
+# reach HBM -- cached stores then look faster than they are (C5 8x4096 over
+# two sets: 65.9 us cached, 72.8 us streaming; over eight: 75.2 and 73.4).
+ROTATE_BYTES = 2 << 30
+
+
 def device_rate(torch, ctx, bound, wire_bytes, out_bytes, steps, warmup, sets=None):
-    """K back-to-back device relayouts over rotating buffer sets. Returns
-    (ms_per_step over the bracketed region, mean per-launch kernel ms)."""
+    """K back-to-back device relayouts over rotating buffer sets spanning
+    ROTATE_BYTES, at least one pass over every set in each timed region.
+    Returns (ms_per_step over the bracketed region, mean per-launch kernel
+    ms)."""
     per = wire_bytes + out_bytes
-    sets = sets or max(2, min(16, int(np.ceil(600e6 / per))))
+    sets = sets or max(2, -(-ROTATE_BYTES // per))
+    steps = max(steps, sets)
     wires = [torch.empty(wire_bytes, dtype=torch.uint8, device="cuda") for _ in range(sets)]
     outs = [torch.empty(out_bytes, dtype=torch.uint8, device="cuda") for _ in range(sets)]
     for w in wires:
@@ -331,7 +342,7 @@ def device_rate(torch, ctx, bound, wire_bytes, out_bytes, steps, warmup, sets=No
     torch.cuda.synchronize()
     ms_step = t0.elapsed_time(t1) / steps
     # per-launch durations on the launch stream
-    n = min(steps, 400)
+    n = min(steps, max(400, sets))
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
     for i in range(n):
         ev[i][0].record(stream)
@@ -500,11 +511,13 @@ def probe_bound(name):
     return case.bound, case.wire_bytes, case.out_bytes, (case.win, case.wout)
 
 
-def probe_launches(torch, ctx, bound, wire_bytes, out_bytes, n):
-    """`n` device relayouts back to back over rotating buffer sets larger
-    than the Infinity Cache (every launch reads and writes HBM)."""
+def probe_launches(torch, ctx, bound, wire_bytes, out_bytes, warm, n):
+    """`warm` + `n` device relayouts back to back over rotating buffer sets
+    spanning ROTATE_BYTES (every launch reads and writes HBM), `n` raised to
+    one pass over the sets; returns the launches made."""
     per = wire_bytes + out_bytes
-    sets = max(2, min(16, int(np.ceil(600e6 / per))))
+    sets = max(2, -(-ROTATE_BYTES // per))
+    n = warm + max(n, sets)
     wires = [torch.empty(wire_bytes, dtype=torch.uint8, device="cuda") for _ in range(sets)]
     outs = [torch.empty(out_bytes, dtype=torch.uint8, device="cuda") for _ in range(sets)]
     for w in wires:
@@ -515,6 +528,7 @@ def probe_launches(torch, ctx, bound, wire_bytes, out_bytes, n):
                             stream=stream.cuda_stream)
     torch.cuda.synchronize()
     del wires, outs
+    return n
 
 
 def traffic_probe(torch, ctx, names):
@@ -565,13 +579,13 @@ def traffic_probe(torch, ctx, names):
                              "dispatches": 2 + 20 + 20, "skip": 2}  # gather_rate's launches
             continue
         bound, wire, out_bytes, (win, wout) = probe_bound(name)
-        probe_launches(torch, ctx, bound, wire, out_bytes, PROBE_WARM + PROBE_LAUNCHES)
+        launched = probe_launches(torch, ctx, bound, wire, out_bytes, PROBE_WARM, PROBE_LAUNCHES)
         alg = wire + out_bytes + bound.parameter_bytes
         copy_bytes = max(16, alg // 2 // 16 * 16)
         copy = P.measure_copy(0, copy_bytes, 20, 3)
         kernels[name] = {"family": bound.kernel, "wire_bytes": wire, "output_bytes": out_bytes,
                          "algorithmic_bytes": alg, "win": win, "wout": wout,
-                         "dispatches": PROBE_WARM + PROBE_LAUNCHES, "skip": PROBE_WARM,
+                         "dispatches": launched, "skip": PROBE_WARM,
                          "copy_bytes": copy_bytes, "copy_GBps_events": round(copy, 1)}
     print(json.dumps({"calibration_bytes": CALIBRATION_BYTES, "kernels": kernels}), flush=True)
 
@@ -1350,7 +1364,7 @@ def headline(torch, P, args, h2d_ceiling, inputs):
                                        "per dispatch of this launch from two rocprofv3 --pmc runs of "
                                        "bench.py --traffic-probe --configs c5_e2e (counters need a "
                                        "profiler run of their own; not measured in this run)",
-                     "kernel": "k_permute8<2, 1, 6, true> (f16 -> f32 -> int8, [B,S,32,128] -> [B,32,S,128], eight waves per SIMD, cached stores)",
+                     "kernel": "k_permute8<2, 1, 6, true> (f16 -> f32 -> int8, [B,S,32,128] -> [B,32,S,128], eight waves per SIMD, direct body, streaming stores)",
                      "launch": "one kernel batch of the upload: %d batch entries [%d,%d,32,128]"
                                % (units, units, S),
                      "kernel_ms_per_launch_events": round(kernel_ms, 5),

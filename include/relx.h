@@ -171,6 +171,11 @@ typedef struct relx_bound_info {
   int64_t row_elements;
   int64_t table_bytes;
   int64_t index_count;
+  /* permute programs: 1 when every launch of the whole box (the launches of
+   * relx_relayout_device) runs the direct body, whose divisions are shifts
+   * and whose vectors take stage parameters from their own channel
+   * coordinate; 0 otherwise */
+  int permute_direct;
 } relx_bound_info;
 
 int relx_bound_query(const relx_bound *bound, relx_bound_info *out);
@@ -526,7 +531,8 @@ double relx_measure_d2h(int device, size_t bytes, int iters, int rounds);
 
 /* Measured HBM copy ceiling (GB/s of bytes read + written): a 16-byte vector
  * copy kernel of `bytes` (the stream kernel's access shape) over buffer pairs
- * rotated past the Infinity Cache, `iters` copies, best of `rounds`. The
+ * spanning at least 2 GiB (eight times the Infinity Cache), `iters` copies
+ * but at least one per pair, best of `rounds`. The
  * device-side counterpart of relx_measure_h2d; the reference measures its
  * copy kernel the same way (copyF32Vec4Kernel, libreloc/cuda/CudaKernels.cu:30-36).
  * Returns -1 on failure. */

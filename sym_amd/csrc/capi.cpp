@@ -355,6 +355,13 @@ int relx_bound_query(const relx_bound *bound, relx_bound_info *out) {
   try {
     const relx::DeviceProgram &dp = const_cast<relx::BoundHandle &>(bound->h).program(0);
     std::snprintf(out->kernel, sizeof(out->kernel), "%s", dp.kernel);
+    if (dp.family == relx::kFamPermute) {
+      const std::vector<relx::KArgs> ls = relx::axis_launches(dp, -1, 0, 0);
+      out->permute_direct = ls.empty() ? 0 : 1;
+      for (const relx::KArgs &a : ls)
+        if (!a.p_direct)
+          out->permute_direct = 0;
+    }
     if (!b.typed)
       out->source_bytes = dp.wire_elems * L.element_size;
   } catch (...) {

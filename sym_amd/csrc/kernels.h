@@ -868,59 +868,70 @@ __global__ __launch_bounds__(kBlock) void k_interleave1p(const uint8_t *src, int
 // ------------------------------------------------------------- permute
 
 // Destination axes [batch..., c, m, e] from a source holding (m, c, e)
-// contiguously. A block takes T consecutive m (one contiguous T*C*E source
-// run), applies the stages on the way into LDS, which it fills in
-// destination order [c][t][e], then writes C contiguous runs of T*E
-// elements. Reads are whole source rows, writes whole destination runs.
-// CACHED_ST: the runs are stored through the caches instead of streaming
-// (permute_cached_stores).
-template <int WIN, int WOUT, int CH, bool CACHED_ST>
+// contiguously. A block takes T consecutive m of a group of G consecutive c
+// (T source runs of G*E elements, C*E apart), applies the stages on the way
+// into LDS, which it fills in destination order [c][t][e], then writes G
+// contiguous runs of T*E elements. The blocks of one group come before the
+// next group's, so the blocks resident at once write G planes of the result.
+template <int WIN, int WOUT, int CH>
 __device__ __forceinline__ void permute_body(const KArgs &a) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int VI = 16 / WIN, BO = VI * WOUT;
   constexpr int U = 4; // source vectors in flight per thread
   constexpr bool NTL = RELX_NT_LOAD(kFamPermute, WIN, WOUT, 1);
-  constexpr bool NTS = !CACHED_ST && RELX_NT_STORE(kFamPermute, WIN, WOUT, 1);
+  constexpr bool NTS = RELX_NT_STORE(kFamPermute, WIN, WOUT, 1);
   asm volatile("" ::"s"(a.src), "s"(a.dst), "s"(a.work), "s"(a.sbase), "s"(a.dbase), "s"(a.p_t),
                "s"(a.p_lds), "s"(a.p_dsc));
   hot(a.p_tiles);
+  hot(a.p_cgt);
   hot(a.p_ce);
+  hot(a.p_ge);
   hot(a.p_e);
   hot(a.p_run);
+  asm volatile("" ::"s"(a.p_g));
   hot_levels<kBatchLevels>(a);
   hot_chain<CH>(a);
   const uint32_t t = blockIdx.x;
   if (t >= a.work)
     return;
-  const uint32_t batch = fdiv(t, a.p_tiles);
-  const uint32_t m0 = (t - batch * a.p_tiles.d) * a.p_t;
+  // group of G channels (slowest), then batch entry and m-tile
+  const uint32_t cg = fdiv(t, a.p_cgt);
+  const uint32_t t2 = t - cg * a.p_cgt.d;
+  const uint32_t batch = fdiv(t2, a.p_tiles);
+  const uint32_t m0 = (t2 - batch * a.p_tiles.d) * a.p_t;
   int64_t sbase = a.sbase, dbase = a.dbase;
   decompose<kBatchLevels>(a.lv, batch, sbase, dbase); // permutes carry no pads
-  const uint32_t CE = a.p_ce.d, E = a.p_e.d;
-  const uint8_t *src = a.src + (sbase + static_cast<int64_t>(m0) * CE) * WIN;
-  const uint32_t nvec = a.p_t * CE / VI;
+  const uint32_t CE = a.p_ce.d, GE = a.p_ge.d, E = a.p_e.d, c0 = cg * a.p_g;
+  // the block's T row parts of GE elements, CE apart
+  const vec4 *src = reinterpret_cast<const vec4 *>(
+      a.src + (sbase + static_cast<int64_t>(m0) * CE + static_cast<int64_t>(c0) * E) * WIN);
+  const uint32_t gap = (CE - GE) / VI; // vectors between two row parts
+  const uint32_t nvec = a.p_t * GE / VI;
   for (uint32_t v0 = threadIdx.x; v0 < nvec; v0 += kBlock * U) {
     vec4 in[U];
+    // each vector's place: (t, c, e) in the block and its dense result offset
+    uint32_t tt[U], rem[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t v = v0 + u * kBlock < nvec ? v0 + u * kBlock : v0;
+      tt[u] = fdiv(v * VI, a.p_ge); // v * VI: element offset in the row parts
+      rem[u] = v * VI - tt[u] * GE;
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const uint32_t v = v0 + u * kBlock;
       if (v < nvec)
-        in[u] = ld16<NTL>(reinterpret_cast<const vec4 *>(src) + v);
+        in[u] = ld16<NTL>(src + v + tt[u] * gap);
     }
-    // each vector's place: (t, c, e) in the block and its dense result offset
     uint32_t lds_off[U];
     int64_t ro[U];
     VecParams par[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint32_t v = v0 + u * kBlock < nvec ? v0 + u * kBlock : v0;
-      const uint32_t off = v * VI; // element offset in the block's source run
-      const uint32_t tt = fdiv(off, a.p_ce);
-      const uint32_t rem = off - tt * CE;
-      const uint32_t c = fdiv(rem, a.p_e);
-      const uint32_t e = rem - c * E;
-      lds_off[u] = ((c * a.p_t + tt) * E + e) * WOUT;
-      ro[u] = dbase + c * a.p_dsc + static_cast<int64_t>(m0 + tt) * E + e;
+      const uint32_t cl = fdiv(rem[u], a.p_e);
+      const uint32_t e = rem[u] - cl * E;
+      lds_off[u] = ((cl * a.p_t + tt[u]) * E + e) * WOUT;
+      ro[u] = dbase + (c0 + cl) * a.p_dsc + static_cast<int64_t>(m0 + tt[u]) * E + e;
       par[u] = fetch_params<CH>(a, ro[u]);
     }
     // one body per vector with a compile-time index, so `in` stays in
@@ -955,35 +966,163 @@ __device__ __forceinline__ void permute_body(const KArgs &a) {
   }
   __syncthreads();
   const uint32_t nout = a.p_lds / 16, run = a.p_run.d;
-  uint8_t *dst = a.dst + (dbase + static_cast<int64_t>(m0) * E) * WOUT;
+  uint8_t *dst = a.dst + (dbase + static_cast<int64_t>(c0) * a.p_dsc + static_cast<int64_t>(m0) * E) * WOUT;
   for (uint32_t w = threadIdx.x; w < nout; w += kBlock) {
-    const uint32_t c = fdiv(w, a.p_run);
-    const uint32_t j = w - c * run;
+    const uint32_t cl = fdiv(w, a.p_run);
+    const uint32_t j = w - cl * run;
     const vec4 val = reinterpret_cast<const vec4 *>(lds)[w];
-    st16<NTS>(reinterpret_cast<vec4 *>(dst + c * a.p_dsc * WOUT) + j, val);
+    st16<NTS>(reinterpret_cast<vec4 *>(dst + cl * a.p_dsc * WOUT) + j, val);
   }
 }
 
-template <int WIN, int WOUT, int CH, bool CACHED_ST>
+// Stage parameters of a direct launch's vector: entry `ch` of the chain's
+// parameter stage.
+template <int CH>
+__device__ __forceinline__ VecParams direct_params(const PermArgs &a, uint32_t ch) {
+  VecParams p{0.0f, 0};
+  if constexpr (chain_param_stage(CH) >= 0) {
+    p.sc = a.pf[a.scale_off + ch];
+    if constexpr (CH == kChainDeqF16 || CH == kChainDeq)
+      p.zp = a.pi[a.zp_off + (a.zp_per_ch ? ch : 0u)];
+  }
+  return p;
+}
+
+// The chain over one vector whose parameters are constant across it.
+template <int CH, int V>
+__device__ __forceinline__ void chain_vec_direct(uint32_t (&v)[V], const VecParams &p) {
+#pragma unroll
+  for (int e = 0; e < V; ++e) {
+    if constexpr (CH == kChainF32F16)
+      v[e] = op_f32_f16(v[e]);
+    else if constexpr (CH == kChainF16F32)
+      v[e] = op_f16_f32(v[e]);
+    else if constexpr (CH == kChainDeqF16)
+      v[e] = op_f32_f16(op_dequant(v[e], p.sc, p.zp));
+    else if constexpr (CH == kChainDeq)
+      v[e] = op_dequant(v[e], p.sc, p.zp);
+    else if constexpr (CH == kChainF16Quant)
+      v[e] = quant_value(op_f16_f32_value(v[e]), p.sc);
+    else if constexpr (CH == kChainQuant)
+      v[e] = op_quant(v[e], p.sc);
+  }
+}
+
+// The permute of a direct launch: the same blocks, tile and store order from
+// PermArgs, with shifts and masks for the divisions inside a block, the batch
+// entry's offset as one multiply, and a vector's parameters by its channel.
+template <int WIN, int WOUT, int CH>
+__device__ __forceinline__ void permute_direct_body(const PermArgs &a) {
+  static_assert(CH != kChainGeneric, "direct launches run compile-time chains");
+  extern __shared__ __align__(16) uint8_t lds[];
+  constexpr int VI = 16 / WIN, BO = VI * WOUT;
+  constexpr int U = 2; // source vectors in flight per thread
+  constexpr bool NTL = RELX_NT_LOAD(kFamPermute, WIN, WOUT, 1);
+  constexpr bool NTS = RELX_NT_STORE(kFamPermute, WIN, WOUT, 1);
+  // every argument named at entry: their scalar loads issue in one round
+  asm volatile("" ::"s"(a.src), "s"(a.dst), "s"(a.pf), "s"(a.sbase), "s"(a.dbase), "s"(a.dsc),
+               "s"(a.work), "s"(a.cgt_d), "s"(a.cgt_m), "s"(a.cgt_s), "s"(a.tiles_d),
+               "s"(a.tiles_m), "s"(a.tiles_s));
+  asm volatile("" ::"s"(a.t), "s"(a.g), "s"(a.ge_s), "s"(a.e_s), "s"(a.run_s), "s"(a.ce),
+               "s"(a.bss), "s"(a.bds), "s"(a.nout), "s"(a.cmask), "s"(a.scale_off));
+  if constexpr (CH == kChainDeqF16 || CH == kChainDeq)
+    asm volatile("" ::"s"(a.pi), "s"(a.zp_off), "s"(a.zp_per_ch));
+  const uint32_t t = blockIdx.x;
+  if (t >= a.work)
+    return;
+  const uint32_t cg = fdiv(t, FastDiv{a.cgt_d, a.cgt_m, a.cgt_s, 0});
+  const uint32_t t2 = t - cg * a.cgt_d;
+  const uint32_t b = fdiv(t2, FastDiv{a.tiles_d, a.tiles_m, a.tiles_s, 0});
+  const uint32_t m0 = (t2 - b * a.tiles_d) * a.t, c0 = cg * a.g;
+  const uint32_t GE = 1u << a.ge_s, E = 1u << a.e_s;
+  const vec4 *src = reinterpret_cast<const vec4 *>(
+      a.src + (a.sbase + static_cast<int64_t>(b) * a.bss + static_cast<int64_t>(m0) * a.ce +
+               static_cast<int64_t>(c0) * E) * WIN);
+  const uint32_t gap = (a.ce - GE) / VI; // vectors between two row parts
+  const uint32_t nvec = (a.t << a.ge_s) / VI;
+  for (uint32_t v0 = threadIdx.x; v0 < nvec; v0 += kBlock * U) {
+    uint32_t tt[U], rem[U];
+    vec4 in[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t v = v0 + u * kBlock < nvec ? v0 + u * kBlock : v0;
+      tt[u] = (v * VI) >> a.ge_s;
+      rem[u] = (v * VI) & (GE - 1);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t v = v0 + u * kBlock;
+      if (v < nvec)
+        in[u] = ld16<NTL>(src + v + tt[u] * gap);
+    }
+    uint32_t lds_off[U];
+    VecParams par[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t cl = rem[u] >> a.e_s, e = rem[u] & (E - 1);
+      lds_off[u] = ((cl * a.t + tt[u]) * E + e) * WOUT;
+      par[u] = direct_params<CH>(a, (c0 + cl) & a.cmask);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (v0 + u * kBlock >= nvec)
+        break;
+      uint32_t x[VI];
+      unpack<WIN, VI>(&in[u], x);
+      chain_vec_direct<CH, VI>(x, par[u]);
+      vec4 o[(BO + 15) / 16];
+      o[0] = vec4{0u, 0u, 0u, 0u};
+      pack<WOUT, VI>(x, o);
+      uint8_t *dstl = lds + lds_off[u];
+      if constexpr (BO >= 16) {
+#pragma unroll
+        for (int j = 0; j < BO / 16; ++j)
+          reinterpret_cast<vec4 *>(dstl)[j] = o[j];
+      } else if constexpr (BO == 8) {
+        *reinterpret_cast<vec2 *>(dstl) = vec2{o[0].x, o[0].y};
+      } else {
+        *reinterpret_cast<uint32_t *>(dstl) = o[0].x;
+      }
+    }
+  }
+  __syncthreads();
+  uint8_t *dst = a.dst + (a.dbase + static_cast<int64_t>(b) * a.bds + static_cast<int64_t>(c0) * a.dsc +
+                          static_cast<int64_t>(m0) * E) * WOUT;
+  const uint32_t rmask = (1u << a.run_s) - 1;
+  for (uint32_t w = threadIdx.x; w < a.nout; w += kBlock) {
+    const vec4 val = reinterpret_cast<const vec4 *>(lds)[w];
+    st16<NTS>(reinterpret_cast<vec4 *>(dst + static_cast<int64_t>(w >> a.run_s) * a.dsc * WOUT) +
+                  (w & rmask),
+              val);
+  }
+}
+
+template <int WIN, int WOUT, int CH>
 __global__ __launch_bounds__(kBlock) void k_permute(KArgs a) {
-  permute_body<WIN, WOUT, CH, CACHED_ST>(a);
+  permute_body<WIN, WOUT, CH>(a);
 }
 
 // The same kernel at eight waves per SIMD (at most 64 VGPRs): 256 CUs then
 // hold 2048 blocks of four waves at once, and the power-of-two block counts
-// of activation shapes (2048 at [1,4096,32,128], 4096 at [8,1024,..], 16384
-// at [8,4096,..]) run as whole rounds, instead of ending on a round of 256
-// blocks, one per CU, too few to keep HBM busy. The f16 -> int8 chain needs
-// 69 VGPRs without the bound, which leaves seven waves. Measured on the
-// MI355X, two alternating passes: 1x4096 11.45 -> 11.21 us, 8x1024 19.1 ->
-// 18.85 us, 8x4096 66.1 -> 65.25 us, 64x1024 125.4 -> 124.5 us; no shape
-// slower.
-template <int WIN, int WOUT, int CH, bool CACHED_ST>
+// of activation shapes run as whole rounds, instead of ending on a round of
+// 256 blocks, one per CU, too few to keep HBM busy. The f16 -> int8 chain
+// needs 69 VGPRs without the bound, which leaves seven waves.
+template <int WIN, int WOUT, int CH>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_permute8(
     KArgs a) {
-  permute_body<WIN, WOUT, CH, CACHED_ST>(a);
+  permute_body<WIN, WOUT, CH>(a);
 }
 
+template <int WIN, int WOUT, int CH>
+__global__ __launch_bounds__(kBlock) void k_permute_direct(PermArgs a) {
+  permute_direct_body<WIN, WOUT, CH>(a);
+}
+
+template <int WIN, int WOUT, int CH>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_permute_direct8(
+    PermArgs a) {
+  permute_direct_body<WIN, WOUT, CH>(a);
+}
 
 // ------------------------------------------------------------ launch
 
@@ -1056,37 +1195,60 @@ hipError_t interleave_cp(const KArgs &a, hipStream_t s) {
   }
 }
 
-#ifndef RELX_PERMUTE_CACHED_STORES
-#define RELX_PERMUTE_CACHED_STORES 1
-#endif
-// A permute launch stores its runs through the caches when it writes at most
-// 128 MiB into planes (destination runs of one c) 512 KiB or more apart, and
-// streams them otherwise. Measured on the MI355X over 23 C5 shapes, kernel
-// time with cached against streaming stores: 2.7-7.9% faster with planes of
-// 512 KiB and more up to 128 MiB of result (8x4096, the headline upload's
-// kernel batch: 70.8 -> 65.2 us), within 1.6% either way for shorter planes
-// at 128 MiB, and 1.6-5.6% slower past 128 MiB or for shorter planes below.
-inline bool permute_cached_stores(const KArgs &a, int wout) {
-  return RELX_PERMUTE_CACHED_STORES &&
-         static_cast<int64_t>(a.work) * a.p_lds <= (int64_t{128} << 20) &&
-         a.p_dsc * wout >= (int64_t{512} << 10);
+// A direct launch's PermArgs (KArgs::p_direct; the host has proven the shifts,
+// the channel entries and a single batch level).
+inline PermArgs permute_direct_args(const KArgs &a) {
+  PermArgs p{};
+  p.src = a.src;
+  p.dst = a.dst;
+  p.pf = a.pf;
+  p.pi = a.pi;
+  p.sbase = a.sbase;
+  p.dbase = a.dbase;
+  p.dsc = a.p_dsc;
+  p.work = a.work;
+  p.cgt_d = a.p_cgt.d;
+  p.cgt_m = a.p_cgt.m;
+  p.cgt_s = a.p_cgt.s;
+  p.tiles_d = a.p_tiles.d;
+  p.tiles_m = a.p_tiles.m;
+  p.tiles_s = a.p_tiles.s;
+  p.t = a.p_t;
+  p.g = a.p_g;
+  p.ge_s = a.p_ge.s;
+  p.e_s = a.p_e.s;
+  p.run_s = a.p_run.s;
+  p.ce = a.p_ce.d;
+  p.bss = a.lv[kBatchLevels - 1].ss;
+  p.bds = a.lv[kBatchLevels - 1].ds;
+  p.nout = a.p_lds / 16;
+  p.cmask = a.p_cmask;
+  const int k = chain_param_stage(a.chain_code);
+  if (k >= 0) {
+    p.scale_off = a.chain.st[k].scale_off;
+    p.zp_off = a.chain.st[k].zp_off;
+    p.zp_per_ch = a.chain.st[k].zp_per_ch;
+  }
+  return p;
 }
 
 template <int WIN, int WOUT, int CH>
 hipError_t permute_launch(const KArgs &a, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(a.work)), block(kBlock);
-  const bool cached = permute_cached_stores(a, WOUT);
-  if constexpr (permute_eight_waves(WIN, CH)) {
-    if (cached)
-      hipLaunchKernelGGL((k_permute8<WIN, WOUT, CH, true>), grid, block, a.p_lds, s, a);
-    else
-      hipLaunchKernelGGL((k_permute8<WIN, WOUT, CH, false>), grid, block, a.p_lds, s, a);
-  } else {
-    if (cached)
-      hipLaunchKernelGGL((k_permute<WIN, WOUT, CH, true>), grid, block, a.p_lds, s, a);
-    else
-      hipLaunchKernelGGL((k_permute<WIN, WOUT, CH, false>), grid, block, a.p_lds, s, a);
+  if constexpr (CH != kChainGeneric) {
+    if (a.p_direct) {
+      const PermArgs p = permute_direct_args(a);
+      if constexpr (permute_eight_waves(WIN, CH))
+        hipLaunchKernelGGL((k_permute_direct8<WIN, WOUT, CH>), grid, block, a.p_lds, s, p);
+      else
+        hipLaunchKernelGGL((k_permute_direct<WIN, WOUT, CH>), grid, block, a.p_lds, s, p);
+      return hipGetLastError();
+    }
   }
+  if constexpr (permute_eight_waves(WIN, CH))
+    hipLaunchKernelGGL((k_permute8<WIN, WOUT, CH>), grid, block, a.p_lds, s, a);
+  else
+    hipLaunchKernelGGL((k_permute<WIN, WOUT, CH>), grid, block, a.p_lds, s, a);
   return hipGetLastError();
 }
 

@@ -16,16 +16,22 @@
 
 #include "index.h"
 
+// Rows of m per permute block: at most this many source bytes over all C.
 #ifndef RELX_PERMUTE_SOURCE_BYTES
-#define RELX_PERMUTE_SOURCE_BYTES 16384
+#define RELX_PERMUTE_SOURCE_BYTES 8192
+#endif
+// A permute block reads G of the C channels of each source row, at most this
+// many bytes of the row (G halves from C while it is more), and the blocks run
+// group by group: the resident blocks then write the result planes of one
+// group, not all C. Measured on the MI355X over buffers spanning 2.4 GB, C5's
+// [8,4096,32,128] f16 -> int8 launch: 74.1 us with all 32 heads per block
+// (2 rows), 68.2 us with 16 (2 rows of 4 KiB), 66.3 us with 16 and one row
+// per block (RELX_PERMUTE_SOURCE_BYTES), against 65.2 us for a 16-byte copy
+// of the same bytes; [64,4096,..] 572 -> 498 us.
+#ifndef RELX_PERMUTE_GROUP_BYTES
+#define RELX_PERMUTE_GROUP_BYTES 4096
 #endif
 
-namespace {
-// gfx950 as built for (MI355X): compute units, and LDS bytes per CU; a
-// block of four waves at eight waves per SIMD leaves room for 8 per CU.
-constexpr int64_t kResidentCUs = 256;
-constexpr int64_t kLdsPerCU = 160 * 1024;
-} // namespace
 
 namespace relx {
 
@@ -445,36 +451,26 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
               C > 1 && M > 1;
     for (int i = 0; i < c; ++i)
       ok = ok && a.ss[i] % VI == 0;
-    // T rows of m per block: about 16 KiB of source, an LDS tile of at most
-    // 32 KiB, T dividing M
+    // G channels per block (RELX_PERMUTE_GROUP_BYTES)
+    int64_t G = C;
+    while (G % 2 == 0 && G * E * win > RELX_PERMUTE_GROUP_BYTES)
+      G /= 2;
+    // T rows of m per block: at most RELX_PERMUTE_SOURCE_BYTES of source over
+    // all C (at least one row), an LDS tile of at most 32 KiB, T dividing M
     int64_t T = 0;
     if (ok) {
       T = 1;
       while (T * 2 <= M && M % (T * 2) == 0 && T * 2 * C * E * win <= RELX_PERMUTE_SOURCE_BYTES &&
-             T * 2 * C * E * wout <= 32768)
+             T * 2 * G * E * wout <= 32768)
         T *= 2;
-      ok = T * C * E * wout <= 32768;
-      // Twice the rows per block (up to twice the source bytes) when that
-      // makes the whole box exactly one round of resident blocks: measured
-      // on C5 at [8,1024,..] and [64,128,..] (8192 rows: 2048 blocks of 4
-      // rows), 19.1 -> 18.7 and 19.0 -> 18.35 us, where 2 rounds of 2-row
-      // blocks leave the second round's stores to drain alone. Shapes whose
-      // block count is far from one round keep the default (8x4096: 65.8 us
-      // against 69.0 us with 4-row blocks).
-      int64_t rows = M;
-      for (int i = 0; i < c; ++i)
-        rows *= a.vext[i];
-      const int64_t T2 = T * 2, lds2 = T2 * C * E * wout;
-      if (ok && permute_eight_waves(static_cast<int>(win), chain_code) && M % T2 == 0 &&
-          T2 * C * E * win <= 2 * RELX_PERMUTE_SOURCE_BYTES && lds2 <= 32768 &&
-          rows / T2 == kResidentCUs * std::min<int64_t>(8, kLdsPerCU / lds2))
-        T = T2;
+      ok = T * G * E * wout <= 32768;
     }
     if (ok && channels_ok(VI)) {
       family = kFamPermute;
       a.vec = VI;
       a.p_t = static_cast<uint32_t>(T);
-      a.p_lds = static_cast<uint32_t>(T * C * E * wout);
+      a.p_g = static_cast<uint32_t>(G);
+      a.p_lds = static_cast<uint32_t>(T * G * E * wout);
     }
   }
   if (family == kFamGeneric && widths_ok && dense && !needs_expr) {
@@ -610,7 +606,9 @@ int64_t box_work(const DeviceProgram &dp, const Box &b) {
       e = 1;
     else if (dp.family == kFamPermute && i == r - 2)
       e /= a.p_t;
-    else if (dp.family == kFamPermute && i > r - 4)
+    else if (dp.family == kFamPermute && i == r - 3)
+      e /= a.p_g;
+    else if (dp.family == kFamPermute && i > r - 3)
       e = 1;
     n *= e;
   }
@@ -747,6 +745,44 @@ KArgs edge_args(const DeviceProgram &dp, const Box &b) {
   return a;
 }
 
+bool pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+
+// A permute launch runs the direct body when its divisions are shifts (G*E,
+// E and the 16-byte vectors of a run are powers of two, so make_div gives
+// m = 1 and s = log2 d), its batch entries lie along one level (the outer
+// levels are unit levels) and the parameter stage, if any, takes a vector's
+// entry from the block's own c coordinate. For a stage per channel along c
+// (rs = M*E, re = C) at result offset o = D + c*M*E + m*E + e, with m < M,
+// e < E and D the offset of the block's batch entry, (o / (M*E)) mod C = c
+// exactly when D is a multiple of C*M*E: every batch level's destination
+// stride is, and the launch origin is one plus an offset inside a plane
+// (below M*E; a launch may start at any m). A per-tensor stage takes entry 0.
+bool permute_direct(KArgs &a, int64_t C, int64_t M, int64_t E) {
+  a.p_cmask = 0;
+  if (a.chain_code == kChainGeneric || !pow2(a.p_ge.d) || !pow2(a.p_e.d) || !pow2(a.p_run.d))
+    return false;
+  // the direct kernel takes a batch entry's offsets from the innermost level
+  for (int j = 0; j + 1 < kBatchLevels; ++j)
+    if (a.lv[j].div.d != 1 || a.lv[j].vcnt != 1)
+      return false;
+  const int k = chain_param_stage(a.chain_code);
+  if (k < 0)
+    return true;
+  const DevStage &s = a.chain.st[k];
+  if (s.vec != 0)
+    return false;
+  if (s.mode == kChanNone)
+    return true;
+  const int64_t plane = C * M * E;
+  if (s.mode != kChanDim || s.ch_rs != M * E || s.ch_re != C || a.dbase % plane >= M * E)
+    return false;
+  for (int j = 0; j < kBatchLevels; ++j)
+    if (a.lv[j].div.d > 1 && a.lv[j].ds % plane != 0)
+      return false;
+  a.p_cmask = ~0u;
+  return true;
+}
+
 KArgs launch_args(const DeviceProgram &dp, const Box &b) {
   KArgs a = dp.base;
   const int r = a.rank;
@@ -809,10 +845,13 @@ KArgs launch_args(const DeviceProgram &dp, const Box &b) {
       a.lv[kBatchLevels - n + j] = axis_level(a, b, idx[j], 1);
     const int64_t E = a.vext[r - 1], C = a.vext[r - 3], M = a.vext[r - 2], T = a.p_t;
     a.p_tiles = make_div(b.ext[r - 2] / T);
+    a.p_cgt = make_div(work / (C / a.p_g));
     a.p_ce = make_div(C * E);
+    a.p_ge = make_div(int64_t{a.p_g} * E);
     a.p_e = make_div(E);
     a.p_run = make_div(T * E * a.wout / 16);
     a.p_dsc = M * E;
+    a.p_direct = permute_direct(a, C, M, E) ? 1 : 0;
     break;
   }
   case kFamInterleave:
@@ -1092,27 +1131,58 @@ void verify_launch(const DeviceProgram &dp_in, const KArgs &a) {
   case kFamPermute: {
     if (a.work64 > (int64_t{1} << 22) || a.work != a.work64)
       bad_launch(dp, "more blocks than one launch takes");
-    const int64_t CE = a.p_ce.d, E = a.p_e.d, T = a.p_t, C = CE / E;
+    const int64_t CE = a.p_ce.d, E = a.p_e.d, T = a.p_t, C = CE / E, G = a.p_g, GE = a.p_ge.d;
     const int VI = 16 / win;
-    if (a.p_lds != T * CE * wout || a.p_lds > 32768 || int64_t{a.p_run.d} * 16 != T * E * wout ||
-        a.vec != VI || CE % VI != 0 || (E * wout) % 16 != 0)
+    if (G < 1 || C % G != 0 || GE != G * E || a.p_lds != T * GE * wout || a.p_lds > 32768 ||
+        int64_t{a.p_run.d} * 16 != T * E * wout || a.vec != VI || GE % VI != 0 ||
+        (E * wout) % 16 != 0 || int64_t{a.p_cgt.d} * (C / G) != a.work64)
       bad_launch(dp, "block geometry disagrees with the kernel");
+    // a direct launch replaces each division by a shift and mask, and each
+    // vector's parameter entry by c & p_cmask
+    const int pk = chain_param_stage(a.chain_code);
+    if (a.p_direct) {
+      for (const FastDiv *f : {&a.p_ge, &a.p_e, &a.p_run})
+        if (!pow2(f->d) || f->m != 1 || (uint64_t{1} << f->s) != f->d)
+          bad_launch(dp, "a direct permute divides by a number that is not a power of two");
+      if (a.chain_code == kChainGeneric || (pk >= 0 && a.chain.st[pk].vec != 0) ||
+          (a.p_cmask != 0 && a.p_cmask != ~0u))
+        bad_launch(dp, "a direct permute with a chain it cannot run");
+      for (int j = 0; j + 1 < kBatchLevels; ++j)
+        if (a.lv[j].div.d != 1 || a.lv[j].vcnt != 1 || a.lv[j].ss != 0 || a.lv[j].ds != 0)
+          bad_launch(dp, "a direct permute over more than one batch level");
+      if (a.lv[kBatchLevels - 1].div.d > 1 &&
+          (int64_t{a.lv[kBatchLevels - 1].ss} * (a.lv[kBatchLevels - 1].div.d - 1) >= kMaxLaunchWork ||
+           int64_t{a.lv[kBatchLevels - 1].ds} * (a.lv[kBatchLevels - 1].div.d - 1) >= kMaxLaunchWork))
+        bad_launch(dp, "a direct permute's batch offsets leave 32 bits");
+    }
     for (uint32_t t = 0; t < a.work; ++t) {
-      const uint32_t batch = fdiv(t, a.p_tiles);
-      const int64_t m0 = int64_t{t - batch * a.p_tiles.d} * T;
+      // the kernel's own decomposition: group, then batch entry and m-tile
+      const uint32_t cg = fdiv(t, a.p_cgt);
+      const uint32_t t2 = t - cg * a.p_cgt.d;
+      const uint32_t batch = fdiv(t2, a.p_tiles);
+      const int64_t m0 = int64_t{t2 - batch * a.p_tiles.d} * T;
       int64_t sbase = a.sbase, dbase = a.dbase;
       if (decompose_rt(kBatchLevels, a.lv, batch, sbase, dbase))
         bad_launch(dp, "a permute block reaches a pad");
-      ck.src_run(sbase + m0 * CE, T * CE, false);
-      if (((sbase + m0 * CE) * win) % 16 != 0)
-        bad_launch(dp, "unaligned source rows");
-      for (int64_t c = 0; c < C; ++c) {
+      for (int64_t tt = 0; tt < T; ++tt) {
+        const int64_t so = sbase + (m0 + tt) * CE + int64_t{cg} * GE;
+        ck.src_run(so, GE, false);
+        if ((so * win) % 16 != 0)
+          bad_launch(dp, "unaligned source rows");
+      }
+      for (int64_t cl = 0; cl < G; ++cl) {
+        const int64_t c = int64_t{cg} * G + cl;
         ck.dst_run(dbase + c * a.p_dsc + m0 * E, T * E, false);
         if (((dbase + c * a.p_dsc + m0 * E) * wout) % 16 != 0)
           bad_launch(dp, "unaligned destination runs");
         for (int64_t tt = 0; tt < T; ++tt)
-          for (int64_t e = 0; e < E; e += VI)
-            ck.channels(dbase + c * a.p_dsc + (m0 + tt) * E + e, VI);
+          for (int64_t e = 0; e < E; e += VI) {
+            const int64_t o = dbase + c * a.p_dsc + (m0 + tt) * E + e;
+            ck.channels(o, VI);
+            if (a.p_direct && pk >= 0 &&
+                chan_of(a.chain.st[pk], o) != (static_cast<uint32_t>(c) & a.p_cmask))
+              bad_launch(dp, "a direct permute reads another parameter entry");
+          }
       }
     }
     break;

@@ -61,6 +61,13 @@ constexpr bool permute_eight_waves(int win, int ch) {
   return ch != kChainGeneric && !(win == 1 && (ch == kChainDeqF16 || ch == kChainDeq));
 }
 
+// The one stage of a compile-time chain that reads parameters (-1: none).
+constexpr int chain_param_stage(int ch) {
+  return ch == kChainDeqF16 || ch == kChainDeq || ch == kChainQuant ? 0
+         : ch == kChainF16Quant                                     ? 1
+                                                                    : -1;
+}
+
 // Division by a runtime constant for n < 2^32: q = (umulhi(n, m) + n) >> s.
 struct FastDiv {
   uint32_t d, m, s, pad_;
@@ -172,11 +179,19 @@ struct KArgs {
   int64_t i_ssc;        // plane stride (source stride of c)
   int32_t i_loc, i_vc;  // leading pad and valid extent of c
   // permute: destination axes [batch..., c, m, e]; the source holds (m, c, e)
-  // contiguously (rows of C*E per m). A block takes T consecutive m.
+  // contiguously (rows of C*E per m). A block takes T consecutive m of one
+  // group of G consecutive c; blocks run group by group (the group is the
+  // slowest index: cg = t / p_cgt).
   FastDiv p_tiles;      // m-tiles in the box
+  FastDiv p_cgt;        // blocks per group: the box's batch entries x m-tiles
   FastDiv p_ce, p_e;    // C*E and E (source row and inner extents)
+  FastDiv p_ge;         // G*E (a block's part of a source row)
   FastDiv p_run;        // 16-byte output vectors per (c, tile) run: T*E*wout/16
-  uint32_t p_t, p_lds;  // T, LDS bytes per block (T*C*E*wout)
+  uint32_t p_t, p_lds;  // T, LDS bytes per block (T*G*E*wout)
+  uint32_t p_g, p_pad2_; // G
+  // direct launches (p_direct): a vector's parameter entry is c & p_cmask
+  // (~0: the stage is per channel along c; 0: per tensor)
+  uint32_t p_cmask, p_pad_;
   int64_t p_dsc;        // destination stride of c (M*E)
   Chain chain;
   // ---- generic kernel and host bookkeeping (coalesced destination axes)
@@ -190,6 +205,8 @@ struct KArgs {
   int32_t res_rank;
   int32_t edge_box;  // 1: a box of a fast-family program at its unaligned edge,
                      // run by the generic kernel
+  int32_t p_direct;  // permute: C*E, E and the run are powers of two and the
+                     // parameter stage's channel is c or 0 (permute_direct)
   int64_t work64;    // generic: elements of the box
   uint64_t fill64;
   int64_t pext[kMaxRank]; // padded extents
@@ -201,6 +218,32 @@ struct KArgs {
   int64_t box_ext[kMaxRank];
   int64_t rs[kMaxRank]; // result strides and extents (channel expressions)
   int64_t re[kMaxRank];
+};
+
+// Arguments of a direct permute launch (KArgs::p_direct): only the fields its
+// blocks read, 33 dwords that a block fetches in one round of scalar loads.
+// (Built from KArgs, whose 650 bytes the general kernel fetches in three
+// dependent rounds, spilling scalar registers, before its first data load;
+// with blocks of 8 KiB that start delay costs C5 [8,4096,32,128] 20%.) The
+// launch's batch entries lie along one level: entry b starts b * bss source
+// and b * bds result elements past the launch origin.
+struct PermArgs {
+  const uint8_t *src;
+  uint8_t *dst;
+  const float *pf;
+  const int32_t *pi;
+  int64_t sbase, dbase;               // element offsets of the launch origin
+  int64_t dsc;                        // result stride of c (M*E)
+  uint32_t work;                      // blocks
+  uint32_t cgt_d, cgt_m, cgt_s;       // blocks per channel group (FastDiv)
+  uint32_t tiles_d, tiles_m, tiles_s; // m-tiles per batch entry (FastDiv)
+  uint32_t t, g;                      // rows and channels per block
+  uint32_t ge_s, e_s, run_s;          // log2 of G*E, E and a run's 16-byte vectors
+  uint32_t ce;                        // C*E, a source row
+  uint32_t bss, bds;                  // element strides of a batch entry
+  uint32_t nout;                      // 16-byte vectors a block stores
+  uint32_t cmask;                     // a vector's parameter entry: c & cmask
+  uint32_t scale_off, zp_off, zp_per_ch;
 };
 
 // Row gather of an indexed plan (index_select along axis 0, at most one cast):

@@ -1583,9 +1583,12 @@ double measure_device_copy(int device, size_t bytes, int iters, int rounds) {
   if (n16 == 0 || n16 >= (size_t{1} << 31))
     throw Error("invalid_argument", "copy size must be 16 B to 32 GiB");
   bytes = n16 * 16;
-  // Rotate buffer pairs whose total exceeds the 256 MB Infinity Cache, so
-  // every copy reads and writes HBM.
-  const size_t sets = std::max<size_t>(2, std::min<size_t>(16, (size_t{600} << 20) / (2 * bytes) + 1));
+  // Rotate buffer pairs spanning at least 2 GiB, eight times the 256 MB
+  // Infinity Cache, and make each timed round at least one pass over them, so
+  // every copy reads and writes HBM (a destination still held in the cache
+  // from an earlier pass would absorb the rewrite).
+  const size_t sets = std::max<size_t>(2, ((size_t{2} << 30) + 2 * bytes - 1) / (2 * bytes));
+  iters = std::max(iters, static_cast<int>(sets));
   std::vector<void *> src(sets, nullptr), dst(sets, nullptr);
   hipStream_t s = nullptr;
   hipEvent_t e0 = nullptr, e1 = nullptr;

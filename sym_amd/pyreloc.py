@@ -324,6 +324,12 @@ class Bound:
     def kernel(self):
         return self.info.kernel.decode()
 
+    @property
+    def permute_direct(self):
+        """True when every whole-box launch of a permute program runs the
+        direct body (shift indexing, parameters by channel coordinate)."""
+        return bool(self.info.permute_direct)
+
     def bytes_at(self, boundary):
         return self.info.bytes_at[boundary]
 

@@ -18,6 +18,7 @@ from sym_amd import encoder as EN
 from sym_amd import pyreloc as P
 from sym_amd import workloads as W
 from tests import golden_io as G
+from tests import permute_cases as PC
 from tests.test_encoder import small_cases
 
 pytestmark = pytest.mark.gpu
@@ -347,6 +348,45 @@ def test_c5_activation_quant(ctx, B, S):
         for b0 in range(0, B, step):
             picks = list(range(b0, min(B, b0 + step)))
             assert np.array_equal(got[picks], _c5_expected(x, s, picks)), picks
+
+
+@pytest.mark.parametrize("case", PC.cases(), ids=[c[0] for c in PC.cases()])
+def test_permute_bodies(ctx, case):
+    """Block permutes through the direct body (shift indexing, parameters by
+    head) and the general one, each against the oracle: uploaded with every
+    stage on the device, with a 64 KiB chunk schedule, and device-resident."""
+    name, blob, x, direct = case
+    want = (O.run_typed(blob, {}, {}, x).tobytes() if P.Plan(blob).typed else
+            O.execute_layout(O.bind(O.decode_plan(blob), {}), x.tobytes()))
+    for opts in ({"host_stages": 0}, {"host_stages": 0, "chunk_bytes": 1 << 16}):
+        out, rep, b = run_h2d(ctx, blob, {}, {}, x, "permute " + name, **opts)
+        assert b.kernel == "permute" and b.permute_direct == direct
+        assert out.tobytes() == want, opts
+    xd = torch.from_numpy(x.view(np.uint8).reshape(-1).copy()).cuda()
+    dev = torch.empty(len(want), dtype=torch.uint8, device="cuda")
+    ctx.relayout_device(b, xd.data_ptr(), dev.data_ptr())
+    torch.cuda.synchronize()
+    assert dev.cpu().numpy().tobytes() == want
+
+
+@pytest.mark.parametrize("B,S", [(1, 65536), (64, 4096)])
+def test_c5_device_resident(ctx, B, S):
+    """Device-resident C5 boxes of 256 MiB and 1 GiB of result, one direct
+    launch each (relx_relayout_device), checked against the oracle in
+    sequence slices."""
+    x, sc = W.c5_input(B, S, seed=B * 7919 + S)
+    b = P.Bound(P.Plan(W.c5_plan().blob), {"B": B, "S": S}, W.param("scale", sc))
+    assert b.permute_direct
+    say("c5 device-resident B=%d S=%d" % (B, S))
+    xd = torch.from_numpy(x.view(np.uint8).reshape(-1)).cuda()
+    dev = torch.empty(B * S * 4096, dtype=torch.int8, device="cuda")
+    ctx.relayout_device(b, xd.data_ptr(), dev.data_ptr())
+    torch.cuda.synchronize()
+    del xd
+    got = dev.cpu().numpy().reshape(B, 32, S, 128)
+    step = max(1, 8388608 // (B * 4096))
+    for s0 in range(0, S, step):
+        assert np.array_equal(got[:, :, s0:s0 + step], _c5_expected(x[:, s0:s0 + step], sc)), s0
 
 
 # -------------------------------------------------------- value sweeps

@@ -12,6 +12,7 @@ import pytest
 from sym_amd import pyreloc as P
 from sym_amd import workloads as W
 from tests import golden_io as G
+from tests import permute_cases as PC
 
 CHUNKS = [0, 1 << 16, 3 << 20]
 
@@ -74,5 +75,32 @@ def test_c4_launches(rows, cols):
 def test_c5_launches(bs, seq):
     b = P.Bound(P.Plan(W.c5_plan().blob), {"B": bs, "S": seq},
                 W.param("scale", np.ones(32, np.float32)))
+    # per-head scales along c, C*E = 4096 and E = 128: the direct body, whose
+    # parameter entries the verifier compares with the stage's channel map
+    # on every vector
+    assert b.kernel == "permute" and b.permute_direct
     big = bs * seq >= 64 * 1024
     _check(b, [0, 1], chunks=[0] if big else CHUNKS)
+
+
+@pytest.mark.parametrize("bs,seq", [(1, 4096), (1, 65536), (64, 4096)])
+def test_permute_direct_chunked(bs, seq):
+    """C5 uploads in chunks: one batch entry splits along its sequence axis,
+    so launches start inside a plane of the result; every launch verified,
+    direct ones against the stage's channel map on every vector."""
+    b = P.Bound(P.Plan(W.c5_plan().blob), {"B": bs, "S": seq},
+                W.param("scale", np.ones(32, np.float32)))
+    assert b.permute_direct
+    assert P.verify_launches(b, 0, 1 << 20 if bs == 1 else 64 << 20) > 2
+
+
+@pytest.mark.parametrize("case", PC.cases(), ids=[c[0] for c in PC.cases()])
+def test_permute_bodies(case):
+    """Which permute body each plan gets, and every launch of either body
+    verified (a direct launch's parameter entry against the stage's channel
+    map on every vector)."""
+    name, blob, x, direct = case
+    b = P.Bound(P.Plan(blob), {}, {})
+    assert b.kernel == "permute", name
+    assert b.permute_direct == direct, name
+    _check(b, range(len(b.footprints())))
