@@ -35,8 +35,12 @@ def test_union_of_intervals():
      {"family": "permute", "win": 2, "wout": 1}, True),
     ("void relx::(anonymous namespace)::k_permute<2, 1, 6, false>(relx::KArgs)",
      {"family": "permute", "win": 2, "wout": 1}, True),
-    ("void relx::(anonymous namespace)::k_permute8<2, 1, 6, true>(relx::KArgs)",
+    ("void relx::(anonymous namespace)::k_permute8<2, 1, 6>(relx::KArgs)",
      {"family": "permute", "win": 2, "wout": 1}, True),
+    ("void relx::(anonymous namespace)::k_permute_direct8<2, 1, 6>(relx::PermArgs)",
+     {"family": "permute", "win": 2, "wout": 1}, True),
+    ("void relx::(anonymous namespace)::k_permute_direct<1, 2, 4>(relx::PermArgs)",
+     {"family": "permute", "win": 2, "wout": 1}, False),
     ("void relx::(anonymous namespace)::k_interleave1p<4, 2, 4, 2>(unsigned char const*)",
      {"family": "interleave", "win": 4, "wout": 2}, True),
     ("void relx::(anonymous namespace)::k_transpose<4, 4, 1>(relx::KArgs)",
@@ -59,7 +63,7 @@ def test_summarize_pmc_scales_by_the_calibration_copy(tmp_path):
         rows = [{"Dispatch_Id": 1, "Grid_Size": 4096, "Kernel_Name": "__amd_rocclr_copyBuffer",
                  "Counter_Name": counter, "Counter_Value": cal_kib}]
         rows += [{"Dispatch_Id": 2 + i, "Grid_Size": 1024,
-                  "Kernel_Name": "void relx::k_permute8<2, 1, 6, true>(relx::KArgs)",
+                  "Kernel_Name": "void relx::k_permute_direct8<2, 1, 6>(relx::PermArgs)",
                   "Counter_Name": counter, "Counter_Value": v} for i, v in enumerate(kib)]
         write_csv(tmp_path / d / "x_counter_collection.csv", fields, rows)
     probe = {"calibration_bytes": cal, "kernels": {
@@ -86,7 +90,7 @@ def test_probe_dispatches_are_assigned_in_order(tmp_path, capsys):
                      "Start_Timestamp": 0, "End_Timestamp": int(dur * us)})
     add("__amd_rocclr_copyBuffer", 4096, 50)
     for dur in (20, 10, 10, 12):                       # config a: 1 warm-up + 3
-        add("void relx::k_permute8<2, 1, 6, true>(relx::KArgs)", 512, dur)
+        add("void relx::k_permute_direct8<2, 1, 6>(relx::PermArgs)", 512, dur)
     add("__amd_rocclr_fillBufferAligned", 256, 1)      # the copy's buffer fill
     for dur in (8, 8, 8):
         add("void relx::k_copy16(...)", 768, dur)
@@ -124,9 +128,9 @@ def test_summarize_trace_headline_timeline(tmp_path, capsys):
                {"Direction": "MEMORY_COPY_HOST_TO_DEVICE", "Start_Timestamp": 35 * us,
                 "End_Timestamp": 70 * us}])
     write_csv(tmp_path / "t_kernel_trace.csv", ["Kernel_Name", "Start_Timestamp", "End_Timestamp"],
-              [{"Kernel_Name": "k_permute<2, 1, 6, true>", "Start_Timestamp": 30 * us,
+              [{"Kernel_Name": "k_permute_direct8<2, 1, 6>", "Start_Timestamp": 30 * us,
                 "End_Timestamp": 40 * us},
-               {"Kernel_Name": "k_permute<2, 1, 6, true>", "Start_Timestamp": 70 * us,
+               {"Kernel_Name": "k_permute_direct8<2, 1, 6>", "Start_Timestamp": 70 * us,
                 "End_Timestamp": 75 * us}])
     bench.summarize_trace(str(tmp_path))
     row = [l for l in capsys.readouterr().out.splitlines() if l.startswith("| 0 |")][0]
