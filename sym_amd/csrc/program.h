@@ -205,8 +205,9 @@ struct KArgs {
   int32_t res_rank;
   int32_t edge_box;  // 1: a box of a fast-family program at its unaligned edge,
                      // run by the generic kernel
-  int32_t p_direct;  // permute: C*E, E and the run are powers of two and the
-                     // parameter stage's channel is c or 0 (permute_direct)
+  int32_t p_direct;  // permute: G*E, E and the run are powers of two, one
+                     // batch level, and the parameter stage's channel is c
+                     // or 0 (permute_direct)
   int64_t work64;    // generic: elements of the box
   uint64_t fill64;
   int64_t pext[kMaxRank]; // padded extents
@@ -221,10 +222,11 @@ struct KArgs {
 };
 
 // Arguments of a direct permute launch (KArgs::p_direct): only the fields its
-// blocks read, 33 dwords that a block fetches in one round of scalar loads.
-// (Built from KArgs, whose 650 bytes the general kernel fetches in three
-// dependent rounds, spilling scalar registers, before its first data load;
-// with blocks of 8 KiB that start delay costs C5 [8,4096,32,128] 20%.) The
+// blocks read, 34 dwords that a block fetches in one round of scalar loads.
+// (Built from KArgs, 2,024 bytes, whose fields the general kernel reads from
+// its first 656 in three dependent rounds, spilling scalar registers, before
+// its first data load; with blocks of 4-8 KiB of source that start costs C5
+// [8,4096,32,128] 20%.) The
 // launch's batch entries lie along one level: entry b starts b * bss source
 // and b * bds result elements past the launch origin.
 struct PermArgs {
