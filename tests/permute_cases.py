@@ -62,3 +62,47 @@ def cases(B=2, S=64):
     add("f16 quant per head, D = 96", 32, 96, "float16",
         [EN.Cast("float32", "exact"), EN.Quantize(_per(32, rng), axis=1)], False)
     return out
+
+
+def _chain(rng, dtype, shape):
+    """Stages after the [B,S,H,D] -> [B,H,S,D] transpose: one of the chains
+    the permute runs, a parameter stage per tensor or along a random axis."""
+    axis = [None, 0, 1, 2, 3][int(rng.integers(5))]
+    n = 1 if axis is None else shape[(0, 2, 1, 3)[axis]]
+    rank = 0 if axis is None else 1
+    sc = EN.InlineParam(tuple(float(v) for v in rng.uniform(0.004, 0.05, n)), "float32", rank)
+    zp = EN.InlineParam(tuple(int(v) for v in rng.integers(-9, 10, n)), "int32", rank)
+    if dtype == "float16":
+        return [[], [EN.Cast("float32", "exact")],
+                [EN.Cast("float32", "exact"), EN.Quantize(sc, axis=axis)]][int(rng.integers(3))]
+    if dtype == "float32":
+        return [[EN.Cast("float16")], [EN.Quantize(sc, axis=axis)]][int(rng.integers(2))]
+    if dtype == "bfloat16":
+        return [EN.Cast("float32", "exact")]
+    return [[EN.Dequantize(sc, zero_point=zp, axis=axis)],
+            [EN.Dequantize(sc, zero_point=zp, axis=axis), EN.Cast("float16")]][int(rng.integers(2))]
+
+
+def random_cases(n, seed=7):
+    """(name, plan blob, source array) for n random block permutes of
+    [B, S, H, D] -> [B, H, S, D] with a random chain; shapes small enough for
+    the oracle, H and D powers of two or not."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        dtype = ["float16", "float32", "int8", "bfloat16"][int(rng.integers(4))]
+        shape = (int(rng.integers(1, 4)), int(rng.choice([2, 8, 12, 16, 40, 64])),
+                 int(rng.choice([2, 3, 4, 6, 8, 16, 24, 32])), int(rng.choice([16, 32, 48, 64, 96, 128])))
+        ops = [EN.Transpose((0, 2, 1, 3))] + _chain(rng, dtype, shape)
+        try:
+            plan = EN.encode(list(shape), dtype, ops)
+        except EN.EncodeError:
+            continue
+        if dtype == "int8":
+            x = rng.integers(-128, 128, shape, dtype=np.int8)
+        elif dtype == "bfloat16":
+            x = (rng.integers(0, 1 << 16, shape, dtype=np.uint32)).astype(np.uint16)
+        else:
+            x = (rng.standard_normal(shape) * 3).astype(dtype)
+        out.append(("%s %s %s" % (dtype, shape, [type(o).__name__ for o in ops[1:]]), plan.blob, x))
+    return out

@@ -369,6 +369,27 @@ def test_permute_bodies(ctx, case):
     assert dev.cpu().numpy().tobytes() == want
 
 
+def test_random_permutes(ctx):
+    """The 200 random block permutes of the launch tests against the oracle:
+    uploaded with every stage on the device (default and 4 KiB chunks) and
+    device-resident."""
+    direct = 0
+    for i, (name, blob, x) in enumerate(PC.random_cases(200)):
+        want = (O.run_typed(blob, {}, {}, x).tobytes() if P.Plan(blob).typed else
+                O.execute_layout(O.bind(O.decode_plan(blob), {}), x.tobytes()))
+        for chunk in (0, 4096):
+            out, rep, b = run_h2d(ctx, blob, {}, {}, x, "random permute %d %s" % (i, name),
+                                  host_stages=0, chunk_bytes=chunk)
+            assert out.tobytes() == want, (i, name, chunk)
+        direct += b.permute_direct
+        xd = torch.from_numpy(np.ascontiguousarray(x).view(np.uint8).reshape(-1).copy()).cuda()
+        dev = torch.empty(len(want), dtype=torch.uint8, device="cuda")
+        ctx.relayout_device(b, xd.data_ptr(), dev.data_ptr())
+        torch.cuda.synchronize()
+        assert dev.cpu().numpy().tobytes() == want, (i, name, "device")
+    assert 0 < direct < 200
+
+
 @pytest.mark.parametrize("B,S", [(1, 65536), (64, 4096)])
 def test_c5_device_resident(ctx, B, S):
     """Device-resident C5 boxes of 256 MiB and 1 GiB of result, one direct

@@ -104,3 +104,18 @@ def test_permute_bodies(case):
     assert b.kernel == "permute", name
     assert b.permute_direct == direct, name
     _check(b, range(len(b.footprints())))
+
+
+def test_random_permutes():
+    """200 random block permutes (tests/permute_cases.random_cases: shapes
+    with and without power-of-two heads and head dims, every chain the
+    permute runs, parameters per tensor or along any axis): both kernels
+    taken, every launch verified at every wire boundary and three chunk
+    sizes."""
+    kinds = set()
+    for name, blob, x in PC.random_cases(200):
+        b = P.Bound(P.Plan(blob), {}, {})
+        assert b.kernel == "permute", name
+        kinds.add(b.permute_direct)
+        _check(b, range(len(b.footprints())), chunks=[0, 4096, 1 << 16])
+    assert kinds == {True, False}
