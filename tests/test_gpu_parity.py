@@ -371,8 +371,9 @@ def test_permute_bodies(ctx, case):
 
 def test_random_permutes(ctx):
     """The 200 random block permutes of the launch tests against the oracle:
-    uploaded with every stage on the device (default and 4 KiB chunks) and
-    device-resident."""
+    uploaded with every stage on the device (default and 4 KiB chunks),
+    device-resident, and device -> host into pageable memory (default and
+    4 KiB chunks, alternately)."""
     direct = 0
     for i, (name, blob, x) in enumerate(PC.random_cases(200)):
         want = (O.run_typed(blob, {}, {}, x).tobytes() if P.Plan(blob).typed else
@@ -387,6 +388,11 @@ def test_random_permutes(ctx):
         ctx.relayout_device(b, xd.data_ptr(), dev.data_ptr())
         torch.cuda.synchronize()
         assert dev.cpu().numpy().tobytes() == want, (i, name, "device")
+        # device -> host: the permute into the device result, copied out in chunks
+        host = np.full(len(want), 0xA5, np.uint8)
+        ctx.execute_d2h(b, xd.data_ptr(), xd.numel(), host.ctypes.data, len(want),
+                        chunk_bytes=4096 if i % 2 else 0, source_pinned=0)
+        assert host.tobytes() == want, (i, name, "d2h")
     assert 0 < direct < 200
 
 
