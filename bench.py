@@ -14,7 +14,7 @@ written.
 * `pcie`: the same steps in wire bytes against the measured pinned H2D
   ceiling, plus the pinned-source (direct DMA) rate.
 * `roofline`: the dominant kernel, the permute over one kernel batch of the
-  upload (8 batch entries), run back to back on one stream over buffers
+  upload (16 batch entries), run back to back on one stream over buffers
   spanning 2 GiB; algorithmic bytes per launch over its mean duration (two
   events bracketing the timed launches, over their count; the mean of an
   event pair per launch, which adds the events' own cost to each launch,
@@ -251,7 +251,7 @@ def ix_config(torch, ctx, P, name, args, h2d_ceiling):
                       "output_GBps": round(out_bytes / ms_step / 1e6, 1),
                       "algorithmic_bytes": alg, "achieved_GBps": round(alg / ms_step / 1e6, 1),
                       "hbm_frac": round(alg / ms_step / 1e6 / HBM_PEAK_GBS, 4),
-                      "traffic": traffic_for(name)}}
+                      "traffic": traffic_for(name, alg)}}
     # upload from a host table a quarter the size (same selected rows)
     rows = max(shape[0] // 4, 1)
     hb, hshape, _, _, hidx = ix_bound(P, name, rows=rows)
@@ -304,6 +304,15 @@ def ix_config(torch, ctx, P, name, args, h2d_ceiling):
 # reach HBM -- cached stores then look faster than they are (C5 8x4096 over
 # two sets: 65.9 us cached, 72.8 us streaming; over eight: 75.2 and 73.4).
 ROTATE_BYTES = 2 << 30
+# the library's kernel-batch rule (kKernelBatchBytes, runtime.h): a launch
+# takes whole chunks up to this much wire, at most a quarter of the call's
+KERNEL_BATCH_BYTES = 512 << 20
+
+
+def batch_units(B, S):
+    """Batch entries per full kernel batch of the C5 [B, S] upload in
+    chunks of one entry (S*4096 f16 elements)."""
+    return max(1, min(KERNEL_BATCH_BYTES // (S * 4096 * 2), B // 4))
 
 
 def device_rate(torch, ctx, bound, wire_bytes, out_bytes, steps, warmup, sets=None):
@@ -477,15 +486,18 @@ def cpu_baseline(case, seconds, threads):
                       % (n, case.name.upper(), case.out_bytes, el)}
 
 
-def traffic_for(config):
+def traffic_for(config, algorithmic_bytes=None):
     """HBM bytes per launch of the config's kernel from the committed PMC
-    summary (profiles/traffic.json), or None."""
+    summary (profiles/traffic.json), or None; None too when the summary's
+    launch moved other algorithmic bytes than the one measured now."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
         entry = json.load(f).get("configs", {}).get(config)
-    return None if entry is None else entry["traffic_bytes"]
+    if entry is None or (algorithmic_bytes is not None and entry["algorithmic_bytes"] != algorithmic_bytes):
+        return None
+    return entry["traffic_bytes"]
 
 
 # Calibration copy of the traffic probe: one device-to-device copy of this
@@ -561,7 +573,7 @@ def traffic_probe(torch, ctx, names):
             calls = 3
             for _ in range(calls):
                 rep = ctx.execute_h2d(bound, x.ctypes.data, x.nbytes, out.data_ptr(), x.size)
-            units = max(1, min((256 << 20) // (HEADLINE_S * 4096 * 2), HEADLINE_B // 4))
+            units = batch_units(HEADLINE_B, HEADLINE_S)
             kernels[name] = {"family": "permute", "win": 2, "wout": 1, "output_bytes": x.size,
                              "algorithmic_bytes": units * HEADLINE_S * 4096 * 3 + sc.nbytes,
                              "launches_per_call": rep["kernel_launches"],
@@ -1254,14 +1266,15 @@ def headline(torch, P, args, h2d_ceiling, inputs):
     p50, p95 = float(np.percentile(ts, 50)), float(np.percentile(ts, 95))
 
     # The dominant kernel: k_permute, one launch per kernel batch of the
-    # upload. A batch takes whole batch entries (the chunks) up to 256 MiB of
+    # upload. A batch takes whole batch entries (the chunks) up to 512 MiB of
     # wire, at most a quarter of the call, and the last chunk is a batch of
     # its own. The roofline takes the full batch's launch, the same box over
-    # B' entries, back to back on one stream with an event pair per launch.
+    # B' entries, back to back on one stream between two events (an event
+    # pair per launch, which adds the events' cost, is reported beside it).
     # The launches inside the steps are timed by event pairs on their copy
     # stream, which also count the wait from the batch's last copy to the
     # kernel's start.
-    units = max(1, min((256 << 20) // (S * 4096 * 2), B // 4))
+    units = batch_units(B, S)
     launches_per_call = kt["launches"] // max(1, kt["calls"])
     expected = -(-(B - 1) // units) + 1 if units > 1 else B
     assert launches_per_call == expected, (B, units, launches_per_call)
@@ -1320,7 +1333,7 @@ def headline(torch, P, args, h2d_ceiling, inputs):
         cores = len(os.sched_getaffinity(0))
         cpu_all = (cpu_reference_h2d(torch, blob, syms, params, x, out_bytes, args.cpu_seconds,
                                      cores) if cores != 8 else cpu)
-    traffic = traffic_for("c5_e2e")
+    traffic = traffic_for("c5_e2e", alg_per_launch)
     return {
         "metric": METRIC,
         "value": round(value, 2),

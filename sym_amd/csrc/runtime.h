@@ -117,14 +117,14 @@ ChunkPlan chunk_plan(const DeviceProgram &dp, uint32_t src_width, int64_t chunk_
 
 // The kernel launches of an upload each cover a batch of landed chunks. A
 // launch streams at the HBM rate only from a few hundred MB up (C5's
-// permute: 50 MB per launch at 51% of peak, 400 MB at 70%), while a chunk's
-// copy takes far longer than its share of the kernel, so a batch takes
-// chunks until it holds kKernelBatchBytes of wire. A member keeps at least
-// four batches, so that the last one, which runs after the last copy,
-// stays short.
+// permute on cold HBM: 50 MB per launch at 0.61 of peak, 403 MB at 0.78,
+// 805 MB at 0.80), while a chunk's copy takes far longer than its share of
+// the kernel, so a batch takes chunks until it holds kKernelBatchBytes of
+// wire. A member keeps at least four batches, so that the last one, which
+// runs after the last copy, stays short.
 // The last chunk is a batch of its own when batches take several chunks:
 // its kernel is what runs after the last copy lands.
-constexpr int64_t kKernelBatchBytes = int64_t{256} << 20;
+constexpr int64_t kKernelBatchBytes = int64_t{512} << 20;
 struct KernelBatches {
   int64_t units, per; // chunk-axis units, units per batch (whole chunks)
   int64_t last;       // first unit of the last chunk when it is a batch of its own, else units
