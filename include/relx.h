@@ -176,6 +176,10 @@ typedef struct relx_bound_info {
    * and whose vectors take stage parameters from their own channel
    * coordinate; 0 otherwise */
   int permute_direct;
+  /* transpose programs: the q width (source-contiguous axis) of the tile
+   * kernel's tiles, 128 for one-byte sources whose q extent is a multiple of
+   * 128, else 64; 0 for the other kernel families */
+  int transpose_tile_q;
 } relx_bound_info;
 
 int relx_bound_query(const relx_bound *bound, relx_bound_info *out);

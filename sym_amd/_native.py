@@ -55,7 +55,8 @@ class relx_bound_info(ctypes.Structure):
                 ("wire_bytes_at", ctypes.c_int64 * (RELX_MAX_STAGES + 1)),
                 ("indexed", ctypes.c_int), ("table_rows", ctypes.c_int64),
                 ("row_elements", ctypes.c_int64), ("table_bytes", ctypes.c_int64),
-                ("index_count", ctypes.c_int64), ("permute_direct", ctypes.c_int)]
+                ("index_count", ctypes.c_int64), ("permute_direct", ctypes.c_int),
+                ("transpose_tile_q", ctypes.c_int)]
 
 
 class relx_ctx_stats(ctypes.Structure):

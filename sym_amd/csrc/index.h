@@ -64,11 +64,14 @@ __host__ __device__ __forceinline__ uint32_t xcd_tile(uint32_t b, uint32_t n) {
 // Tile t of a transpose launch -> (q-tile, c-tile, batch index). Within a
 // batch element's plane of nq x nc tiles, whole groups of g q-tiles come
 // first (q fastest, then c), then the partial group of the remaining q-tiles.
+// With t_skew, q-tile tq takes c-tile (c + tq) mod nc at step c, so the
+// blocks in flight, which share c while q runs fastest, write their
+// destination rows at different column offsets.
 __host__ __device__ __forceinline__ void tile_of(const KArgs &a, uint32_t t, uint32_t &tq,
                                                  uint32_t &tc, uint32_t &batch) {
   batch = fdiv(t, a.t_plane);
   const uint32_t tp = t - batch * a.t_plane.d;
-  const uint32_t nc = a.t_group.d / a.t_g.d;
+  const uint32_t nc = a.t_nc.d;
   if (tp < a.t_full * nc) {
     const uint32_t grp = fdiv(tp, a.t_group);
     const uint32_t r = tp - grp * a.t_group.d;
@@ -80,6 +83,10 @@ __host__ __device__ __forceinline__ void tile_of(const KArgs &a, uint32_t t, uin
     const uint32_t c = fdiv(r, a.t_tail);
     tq = a.t_full + (r - c * a.t_tail.d);
     tc = c;
+  }
+  if (a.t_skew) {
+    const uint32_t x = tc + (tq - fdiv(tq, a.t_nc) * nc); // < 2 nc
+    tc = x >= nc ? x - nc : x;
   }
 }
 

@@ -617,24 +617,27 @@ __global__ __launch_bounds__(kBlock) void k_stream(KArgs a) {
 // ------------------------------------------------------------- transpose
 
 constexpr int kTile = 64;
-constexpr int kPitch = kTile + 1;
 
-// One 64x64 tile per block: [c][q] source rows (q contiguous) into LDS,
-// out as [q][c] destination rows (c contiguous). Stages run on the way out.
-template <int WIN, int WOUT, int CH>
+// One tile of 64 c by TQ q per block (TQ = 64, or 128 for one-byte sources,
+// KArgs::t_wq): [c][q] source rows (q contiguous) into LDS, out as [q][c]
+// destination rows (c contiguous). Stages run on the way out.
+template <int WIN, int WOUT, int CH, int TQ>
 __global__ __launch_bounds__(kBlock) void k_transpose(KArgs a) {
+  constexpr int kPitch = TQ + 1;
   __shared__ uint32_t tile[kTile * kPitch]; // [c][q]
   constexpr int VI = 16 / WIN, VO = 16 / WOUT;
-  constexpr int VPRI = kTile / VI, VPRO = kTile / VO;
-  constexpr int NI = kTile * VPRI / kBlock, NO = kTile * VPRO / kBlock;
+  constexpr int VPRI = TQ / VI, VPRO = kTile / VO;
+  constexpr int NI = kTile * VPRI / kBlock, NO = TQ * VPRO / kBlock;
+  static_assert(NI * kBlock == kTile * VPRI && NO * kBlock == TQ * VPRO, "whole tiles per block");
   constexpr bool NTL = RELX_NT_LOAD(kFamTranspose, WIN, WOUT, 1);
   constexpr bool NTS = RELX_NT_STORE(kFamTranspose, WIN, WOUT, 1);
   asm volatile("" ::"s"(a.src), "s"(a.dst), "s"(a.work), "s"(a.sbase), "s"(a.dbase), "s"(a.t_full),
-               "s"(a.t_xcd), "s"(a.t_ssc), "s"(a.t_dsq), "s"(gridDim.x));
+               "s"(a.t_xcd), "s"(a.t_skew), "s"(a.t_ssc), "s"(a.t_dsq), "s"(gridDim.x));
   hot(a.t_plane);
   hot(a.t_group);
   hot(a.t_g);
   hot(a.t_tail);
+  hot(a.t_nc);
   hot_levels<kBatchLevels>(a);
   hot_chain<CH>(a);
   const uint32_t t = a.t_xcd ? xcd_tile(blockIdx.x, gridDim.x) : blockIdx.x;
@@ -644,7 +647,7 @@ __global__ __launch_bounds__(kBlock) void k_transpose(KArgs a) {
   tile_of(a, t, tq, tc, r2);
   int64_t sbase = a.sbase, dbase = a.dbase;
   decompose<kBatchLevels>(a.lv, r2, sbase, dbase); // transposes carry no pads
-  const int64_t q0 = static_cast<int64_t>(tq) * kTile, c0 = static_cast<int64_t>(tc) * kTile;
+  const int64_t q0 = static_cast<int64_t>(tq) * TQ, c0 = static_cast<int64_t>(tc) * kTile;
   // load: source rows c (stride t_ssc), contiguous q; all loads in flight
   // before the first LDS write
   vec4 in[NI];
@@ -1159,8 +1162,15 @@ hipError_t stream_launch(const KArgs &a, hipStream_t s) {
 
 template <int WIN, int WOUT, int CH>
 hipError_t transpose_launch(const KArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL((k_transpose<WIN, WOUT, CH>), dim3(static_cast<unsigned>(a.work)),
-                     dim3(kBlock), 0, s, a);
+  const dim3 grid(static_cast<unsigned>(a.work)), block(kBlock);
+  if (a.t_wq == 128) {
+    if constexpr (WIN == 1)
+      hipLaunchKernelGGL((k_transpose<WIN, WOUT, CH, 128>), grid, block, 0, s, a);
+    else
+      return hipErrorInvalidValue;
+  } else {
+    hipLaunchKernelGGL((k_transpose<WIN, WOUT, CH, kTile>), grid, block, 0, s, a);
+  }
   return hipGetLastError();
 }
 

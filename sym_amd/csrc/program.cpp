@@ -513,6 +513,9 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
           family = kFamTranspose;
           dp->qa = qa;
           dp->ca = r - 1;
+          // one-byte sources take tiles 128 q wide when q allows it: each
+          // tile row then reads a whole 128-byte line
+          a.t_wq = win == 1 && a.vext[qa] % 128 == 0 ? 128 : 64;
         }
       }
     }
@@ -563,7 +566,7 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
         if (family == kFamStream && ax == r - 1)
           dp->chunk_align = V;
         else if (family == kFamTranspose && (ax == dp->qa || ax == dp->ca))
-          dp->chunk_align = 64;
+          dp->chunk_align = ax == dp->qa ? a.t_wq : 64;
         else if (family == kFamInterleave && ax == r - 2)
           dp->chunk_align = a.vec;
         // an interleave launch writes every channel of its pixels, so its
@@ -599,7 +602,7 @@ int64_t box_work(const DeviceProgram &dp, const Box &b) {
     if (dp.family == kFamStream && i == r - 1)
       e /= a.vec;
     else if (dp.family == kFamTranspose && (i == dp.qa || i == dp.ca))
-      e /= 64;
+      e /= i == dp.qa ? a.t_wq : 64;
     else if (dp.family == kFamInterleave && i == r - 2)
       e /= a.vec;
     else if (dp.family == kFamInterleave && i == r - 1)
@@ -621,7 +624,7 @@ int64_t split_align(const DeviceProgram &dp, int i) {
   if (dp.family == kFamStream && i == r - 1)
     return dp.base.vec;
   if (dp.family == kFamTranspose && (i == dp.qa || i == dp.ca))
-    return 64;
+    return i == dp.qa ? dp.base.t_wq : 64;
   if (dp.family == kFamInterleave && i == r - 2)
     return dp.base.vec;
   if (dp.family == kFamInterleave && i == r - 1)
@@ -823,16 +826,24 @@ KArgs launch_args(const DeviceProgram &dp, const Box &b) {
   case kFamTranspose:
     batch(dp.qa, dp.ca);
     {
-      const int64_t nq = b.ext[dp.qa] / 64, nc = b.ext[dp.ca] / 64;
-      const bool bytes = a.win == 1;
+      // orders (measured on C3's int8 -> f16 transpose, 8 KiB result rows):
+      // 128-wide tiles q fastest with each q-tile's c-tiles rotated, so the
+      // blocks in flight write their rows at different column offsets
+      // (30.0 -> 27.1 us); 64-wide one-byte tiles q fastest, grouped by XCD
+      // so that the two halves of each source line meet in one L2; wider
+      // elements in groups of kTileGroup q-tiles
+      const int64_t nq = b.ext[dp.qa] / a.t_wq, nc = b.ext[dp.ca] / 64;
+      const bool bytes = a.win == 1, wide = a.t_wq == 128;
       const int64_t g = bytes ? nq : std::min<int64_t>(kTileGroup, nq);
       const int64_t full = nq / g * g;
       a.t_plane = make_div(nq * nc);
       a.t_group = make_div(g * nc);
       a.t_g = make_div(g);
       a.t_tail = make_div(nq - full > 0 ? nq - full : 1);
+      a.t_nc = make_div(nc);
       a.t_full = static_cast<uint32_t>(full);
-      a.t_xcd = bytes ? 1u : 0u;
+      a.t_xcd = bytes && !wide ? 1u : 0u;
+      a.t_skew = wide ? 1u : 0u;
     }
     a.t_ssc = a.ss[dp.ca];
     a.t_dsq = a.ds[dp.qa];
@@ -913,8 +924,8 @@ std::vector<KArgs> prefix_launches(const DeviceProgram &dp, const int64_t *fixed
   // A transpose box whose q or c extent is not a multiple of the tile: the
   // whole tiles go to the tile kernel, the strips past them (the q strip
   // over the whole c range, the c strip beside the whole q tiles) to the
-  // element-wise kernel. Box starts on those axes are multiples of 64
-  // (chunks and splits keep the tile alignment).
+  // element-wise kernel. Box starts on those axes are multiples of the tile
+  // (64, t_wq along q: chunks and splits keep the tile alignment).
   std::vector<Box> edges;
   if (dp.family == kFamStream && a.rank == 1 && b.ext[0] % a.vec != 0) {
     // the tail of a single contiguous axis (box starts are multiples of V)
@@ -927,7 +938,8 @@ std::vector<KArgs> prefix_launches(const DeviceProgram &dp, const int64_t *fixed
   }
   if (dp.family == kFamTranspose) {
     const int q = dp.qa, c = dp.ca;
-    const int64_t mq = b.ext[q] / 64 * 64, mc = b.ext[c] / 64 * 64;
+    const int64_t wq = a.t_wq;
+    const int64_t mq = b.ext[q] / wq * wq, mc = b.ext[c] / 64 * 64;
     if (mq < b.ext[q]) {
       Box e = b;
       e.lo[q] = b.lo[q] + mq;
@@ -1068,6 +1080,10 @@ void verify_launch(const DeviceProgram &dp_in, const KArgs &a) {
     if (a.work64 > (int64_t{1} << 22) || a.work != a.work64)
       bad_launch(dp, "more tiles than one launch takes");
     const int VO = 16 / wout;
+    const int64_t TQ = a.t_wq;
+    if (!(TQ == 64 || (TQ == 128 && win == 1)) || a.t_nc.d != a.t_group.d / a.t_g.d ||
+        (a.t_skew && a.t_xcd))
+      bad_launch(dp, "tile geometry disagrees with the kernel");
     std::vector<bool> seen(a.work, false); // the order must be a bijection
     for (uint32_t blk = 0; blk < a.work; ++blk) { // grid = one block per tile
       const uint32_t t = a.t_xcd ? xcd_tile(blk, a.work) : blk;
@@ -1085,18 +1101,24 @@ void verify_launch(const DeviceProgram &dp_in, const KArgs &a) {
       int64_t sbase = a.sbase, dbase = a.dbase;
       if (decompose_rt(kBatchLevels, a.lv, r2, sbase, dbase))
         bad_launch(dp, "a transpose tile reaches a pad");
-      const int64_t q0 = int64_t{tq} * 64, c0 = int64_t{tc} * 64;
-      for (int row = 0; row < 64; row += 63) {
-        // a tile row moves as 16-byte vectors
-        const int64_t so = sbase + (c0 + row) * a.t_ssc + q0, d = dbase + (q0 + row) * a.t_dsq + c0;
-        ck.src_run(so, 64, false);
+      const int64_t q0 = int64_t{tq} * TQ, c0 = int64_t{tc} * 64;
+      // a tile row moves as 16-byte vectors: 64 source rows of TQ elements,
+      // TQ destination rows of 64
+      for (int64_t row = 0; row < 64; row += 63) {
+        const int64_t so = sbase + (c0 + row) * a.t_ssc + q0;
+        ck.src_run(so, TQ, false);
+        if ((so * win) % 16 != 0)
+          bad_launch(dp, "a tile row is not 16-byte aligned");
+      }
+      for (int64_t row = 0; row < TQ; row += TQ - 1) {
+        const int64_t d = dbase + (q0 + row) * a.t_dsq + c0;
         ck.dst_run(d, 64, false);
-        if ((so * win) % 16 != 0 || (d * wout) % 16 != 0)
+        if ((d * wout) % 16 != 0)
           bad_launch(dp, "a tile row is not 16-byte aligned");
       }
       if ((a.t_ssc * win) % 16 != 0 || (a.t_dsq * wout) % 16 != 0)
         bad_launch(dp, "row strides break 16-byte alignment");
-      for (int row = 0; row < 64; ++row)
+      for (int64_t row = 0; row < TQ; ++row)
         for (int cv = 0; cv < 64; cv += VO)
           ck.channels(dbase + (q0 + row) * a.t_dsq + c0 + cv, VO);
     }

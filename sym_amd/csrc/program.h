@@ -127,9 +127,11 @@ constexpr int interleave_pixels(int win, int wout, int cp) {
 // Transpose tiles are visited in groups of this many q-tiles (destination
 // rows), c-tiles within a group: the blocks in flight write long runs of
 // few destination rows and read runs of kTileGroup tile rows. One-byte
-// sources (a tile row is half a 128-byte line, the other half belongs to the
-// next q-tile) instead walk q fastest with each XCD on a contiguous run, so
-// both halves of a line meet in one L2.
+// sources take tiles 128 q wide (a whole 128-byte line per tile row) when q
+// is a multiple of 128, walked q fastest with each q-tile's c-tiles rotated
+// by its index; otherwise 64-wide tiles (a tile row is half a line, the
+// other half belongs to the next q-tile) walk q fastest with each XCD on a
+// contiguous run, so both halves of a line meet in one L2.
 #ifndef RELX_TILE_GROUP
 #define RELX_TILE_GROUP 16
 #endif
@@ -166,13 +168,15 @@ struct KArgs {
   uint32_t fill;      // pad fill bits (fast families move elements of at most 4 bytes)
   int64_t sbase, dbase; // element offsets of the box origin (source: of its valid origin)
   Level lv[kMaxRank];   // stream: box axes (innermost in vectors); 2-D families: batch axes
-  // transpose: tiles along the source-inner axis q (destination rows) and
-  // the destination-inner axis c, visited in groups of g q-tiles (see
-  // tile_of): plane = nq * nc tiles, group = g * nc tiles, g, tail = the
-  // q-tiles of the last, partial group
-  FastDiv t_plane, t_group, t_g, t_tail;
+  // transpose: tiles of t_wq q by 64 c along the source-inner axis q
+  // (destination rows) and the destination-inner axis c, visited in groups
+  // of g q-tiles (see tile_of): plane = nq * nc tiles, group = g * nc tiles,
+  // g, tail = the q-tiles of the last, partial group, nc = c-tiles
+  FastDiv t_plane, t_group, t_g, t_tail, t_nc;
   uint32_t t_full; // q-tiles in whole groups
   uint32_t t_xcd;  // 1: each XCD takes a contiguous run of the order
+  uint32_t t_wq;   // q-tile width: 64, or 128 for one-byte sources
+  uint32_t t_skew; // 1: q-tile tq visits its c-tiles rotated by tq (mod nc)
   int64_t t_ssc, t_dsq; // source stride of c, destination stride of q
   // interleave: pixel groups along the source-contiguous axis p; channel axis c
   FastDiv i_ng;

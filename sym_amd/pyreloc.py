@@ -330,6 +330,13 @@ class Bound:
         direct body (shift indexing, parameters by channel coordinate)."""
         return bool(self.info.permute_direct)
 
+    @property
+    def transpose_tile_q(self):
+        """q width of a transpose program's tiles (128 for one-byte sources
+        whose source-contiguous extent allows it, else 64; 0 for other
+        kernel families)."""
+        return self.info.transpose_tile_q
+
     def bytes_at(self, boundary):
         return self.info.bytes_at[boundary]
 

@@ -29,6 +29,31 @@ def test_library_exports_every_header_symbol():
     assert set(declared) == set(N.SIGNATURES), "ctypes table and header disagree"
 
 
+def test_struct_layouts_match_the_header(tmp_path):
+    """Every ctypes mirror of a relx_* struct has the size and field offsets
+    that the C compiler gives include/relx.h."""
+    import subprocess
+    structs = [(n, c) for n, c in sorted(vars(N).items())
+               if isinstance(c, type) and issubclass(c, ctypes.Structure) and n.startswith("relx_")]
+    assert len(structs) >= 8
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "relx.h"', "int main(void) {"]
+    for n, c in structs:
+        lines.append('  printf("%s %%zu\\n", sizeof(%s));' % (n, n))
+        for f in c._fields_:
+            lines.append('  printf("%s.%s %%zu\\n", offsetof(%s, %s));' % (n, f[0], n, f[0]))
+    lines.append("  return 0;\n}")
+    (tmp_path / "layout.c").write_text("\n".join(lines) + "\n")
+    exe = str(tmp_path / "layout")
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), "-o", exe, str(tmp_path / "layout.c")],
+                   check=True, capture_output=True)
+    got = dict(line.split() for line in subprocess.run([exe], check=True, capture_output=True,
+                                                       text=True).stdout.splitlines())
+    for n, c in structs:
+        assert int(got[n]) == ctypes.sizeof(c), n
+        for f in c._fields_:
+            assert int(got[n + "." + f[0]]) == getattr(c, f[0]).offset, (n, f[0])
+
+
 def test_version_and_wire_version():
     assert "librelx" in P.version()
     blob = bytes.fromhex(G.goldens()["layout_v0"]["kIdentityHex"])

@@ -59,8 +59,36 @@ def test_c2_launches(n):
 def test_c3_launches():
     b = P.Bound(P.Plan(W.c3_plan().blob), {"s0": 4096, "s1": 11008},
                 W.param("scale", np.ones(11008, np.float32)))
-    assert b.kernel == "transpose"
+    # 11008 = 86 x 128: one-byte source rows read as whole 128-byte lines
+    assert b.kernel == "transpose" and b.transpose_tile_q == 128
     _check(b, [0])
+
+
+@pytest.mark.parametrize("rows,cols,tile_q", [(4096, 11008, 128), (256, 4032, 64), (192, 4160, 64),
+                                              (4000, 11008, 128), (128, 128, 128), (64, 64, 64),
+                                              (100, 300, 128)])
+def test_transpose_tile_width(rows, cols, tile_q):
+    """One-byte transposes take tiles 128 q wide when the source-contiguous
+    extent is a multiple of 128 (edge strips element-wise), else 64; the
+    verifier walks the rotated tile order of the wide tiles (a bijection onto
+    the plane) at several chunk sizes, so chunk boundaries along c and q
+    keep the tile alignment."""
+    b = P.Bound(P.Plan(W.c3_plan().blob), {"s0": rows, "s1": cols},
+                W.param("scale", np.ones(cols, np.float32)))
+    if cols % 16:
+        assert b.kernel != "transpose"
+        return
+    assert b.kernel == "transpose" and b.transpose_tile_q == tile_q
+    _check(b, [0, 1, 2], chunks=[0, 1 << 12, 1 << 16, 3 << 20])
+
+
+def test_transpose_tile_width_wider_elements():
+    """Sources of two and four bytes keep 64-wide tiles."""
+    b = P.Bound(P.Plan(W.c1_plan().blob), {"s0": 64 * 4096})
+    assert b.kernel == "transpose" and b.transpose_tile_q == 64
+    b = P.Bound(P.Plan(W.c4_plan().blob), {"s0": 512, "s1": 256},
+                W.param("scale", np.ones(512, np.float32)))
+    assert b.transpose_tile_q == 0
 
 
 @pytest.mark.parametrize("rows,cols", [(14336, 4096), (4096, 14336)])
