@@ -269,9 +269,10 @@ struct DeviceGuard {
 #define RELX_ZERO_COPY_BYTES (1 << 20)
 #endif
 constexpr int kChunkEvents = 32; // device-to-host kernel events, reused round robin
-// Staged chunks of a two-slot ring's default schedule from which the chunks
-// double (see execute_members).
-constexpr int64_t kTwoSlotDoubleChunks = 64;
+// Staged chunks of a two-slot ring's default schedule from which the ring
+// takes the pinned bytes of two slots of twice the chunk as four slots of
+// the chunk (see execute_members).
+constexpr int64_t kTwoSlotSplitChunks = 64;
 
 // A call's status flag, which the element-wise kernels set (pinned host
 // memory). A slot is cleared when a call takes it, kStatusSlots calls after
@@ -751,7 +752,7 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
   // byte ranges of the table, multiples of 256 bytes).
   size_t max_slot = 0;
   std::vector<ChunkPlan> plans;
-  const int nslots = opt.n_buffers > 0 ? opt.n_buffers : 3;
+  int nslots = opt.n_buffers > 0 ? opt.n_buffers : 3;
   for (Member &m : ms) {
     const DeviceProgram &dp = *m.dp;
     ChunkPlan p{};
@@ -772,14 +773,16 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
       m.zero_copy = !sc && !m.direct && p.units <= p.per_chunk &&
                     dp.wire_bytes <= static_cast<int64_t>(RELX_ZERO_COPY_BYTES);
       // A two-slot ring stages chunk j only once the copy of chunk j - 2 has
-      // landed, so each chunk pays a slot turnaround. With many chunks the
-      // default size doubles: C5 [64,4096] from a pageable source, 64 -> 32
-      // chunks, 94.7-94.9% -> 96.0-97.0% of the PCIe ceiling; calls with
-      // fewer chunks lose overlap to larger ones (C5 [8,4096]: 8 -> 4 chunks,
-      // 92% -> 89-91%).
-      if (!m.direct && opt.chunk_bytes <= 0 && nslots == 2 &&
-          (p.units + p.per_chunk - 1) / p.per_chunk >= kTwoSlotDoubleChunks)
-        p.per_chunk = std::min(p.units, 2 * p.per_chunk);
+      // landed, so each chunk pays a slot turnaround, and the copy engines
+      // idle whenever a staging outlasts the other slot's copy. With many
+      // chunks the ring takes the pinned bytes of two slots of twice the
+      // default chunk, as four slots of the chunk. C5 [64,4096] from a
+      // pageable source: two slots of 32 MiB 94.7-94.9% of the PCIe
+      // ceiling, two of 64 MiB 95.9-96.5%, four of 32 MiB 98.5-98.7% (three
+      // 98.7-99.4%). Calls with fewer chunks keep their two slots.
+      if (!m.direct && opt.chunk_bytes <= 0 && opt.n_buffers == 2 &&
+          (p.units + p.per_chunk - 1) / p.per_chunk >= kTwoSlotSplitChunks)
+        nslots = 4;
     }
     if (!m.direct)
       max_slot = std::max(max_slot, static_cast<size_t>(p.per_chunk * p.unit_wire));
