@@ -1172,9 +1172,8 @@ HEADLINE_B, HEADLINE_S = 64, 4096  # C5 at its largest shape: 2 GiB f16 in, 1 Gi
 # Staging of the headline's pageable source: the 8 worker threads the
 # reference's typed transfers use (reloc_torch execute_typed_transfer passes
 # the template's threads, 8), and this library's 3-slot pinned ring (measured
-# 98.7-99.4% of the PCIe ceiling on C5 64x4096; reloc_torch's 2 slots, which
-# the library lays out as four slots of half the pinned bytes each for a
-# call of this many chunks, 98.5-98.7%).
+# 98.7-99.4% of the PCIe ceiling on C5 64x4096; with the chunks left to the
+# library, reloc_torch's 2 slots run as 3 as well).
 GATHER_THREADS, RING_SLOTS = 8, 3
 
 
@@ -1372,9 +1371,8 @@ def headline(torch, P, args, h2d_ceiling, inputs):
                                     "frac": round(rep2["wire_bytes"] * len(ts2) / el2 / 1e9 / h2d_ceiling, 4),
                                     "host_buffers": rep2["host_buffers"],
                                     "note": "n_buffers=2, reloc_torch's default ring depth, on "
-                                            "resources of their own (a call of 64 or more staged "
-                                            "chunks lays the two slots' pinned bytes out as four "
-                                            "slots)"},
+                                            "resources of their own (with the chunks left to the "
+                                            "library a ring has at least three slots)"},
                  "staging": rep["staging"], "host_chunk_bytes": rep["host_chunk_bytes"],
                  "host_buffers": rep["host_buffers"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,

@@ -224,7 +224,8 @@ int relx_ctx_stats_get(const relx_ctx *ctx, relx_ctx_stats *out);
 /* Per-call options (reference TransferOptions,
  * libreloc/include/reloc/Transfer.h:121-155). Zeroed = defaults. */
 typedef struct relx_options {
-  int n_buffers;        /* pinned ring slots (default 3) */
+  int n_buffers;        /* pinned ring slots: 0 = 3; with chunk_bytes 0 (the
+                         * library's chunks) at least 3, else exactly this many */
   int64_t chunk_bytes;  /* wire bytes per chunk (0 = schedule picks) */
   int host_stages;      /* leading per-tensor cast stages the host applies
                            while staging (-1 = auto: the leading narrowing

@@ -269,10 +269,6 @@ struct DeviceGuard {
 #define RELX_ZERO_COPY_BYTES (1 << 20)
 #endif
 constexpr int kChunkEvents = 32; // device-to-host kernel events, reused round robin
-// Staged chunks of a two-slot ring's default schedule from which the ring
-// takes the pinned bytes of two slots of twice the chunk as four slots of
-// the chunk (see execute_members).
-constexpr int64_t kTwoSlotSplitChunks = 64;
 
 // A call's status flag, which the element-wise kernels set (pinned host
 // memory). A slot is cleared when a call takes it, kStatusSlots calls after
@@ -752,7 +748,17 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
   // byte ranges of the table, multiples of 256 bytes).
   size_t max_slot = 0;
   std::vector<ChunkPlan> plans;
-  int nslots = opt.n_buffers > 0 ? opt.n_buffers : 3;
+  // Ring slots. With the chunks left to the library (chunk_bytes unset) the
+  // depth is the library's too, n_buffers counting as a minimum: a ring of
+  // two slots stages chunk j only once the copy of chunk j - 2 has landed,
+  // and the copy engines idle whenever a staging outlasts the other slot's
+  // copy. Pageable sources, p50 of raw calls, two slots -> three: C1 0.83-0.88
+  // -> 0.91-0.92 of the PCIe ceiling, C2 0.71-0.72 -> 0.76-0.77, C5 [8,1024]
+  // 0.83-0.88 -> 0.92, [8,4096] 0.91-0.92 -> 0.94-0.95, [64,4096] 0.96 ->
+  // 0.99. A caller's chunk_bytes keeps the slots it asks for.
+  const int nslots = opt.n_buffers <= 0 ? 3
+                     : opt.chunk_bytes > 0 ? opt.n_buffers
+                                           : std::max(opt.n_buffers, 3);
   for (Member &m : ms) {
     const DeviceProgram &dp = *m.dp;
     ChunkPlan p{};
@@ -772,17 +778,6 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
       // measured faster than staging it for a zero-copy read).
       m.zero_copy = !sc && !m.direct && p.units <= p.per_chunk &&
                     dp.wire_bytes <= static_cast<int64_t>(RELX_ZERO_COPY_BYTES);
-      // A two-slot ring stages chunk j only once the copy of chunk j - 2 has
-      // landed, so each chunk pays a slot turnaround, and the copy engines
-      // idle whenever a staging outlasts the other slot's copy. With many
-      // chunks the ring takes the pinned bytes of two slots of twice the
-      // default chunk, as four slots of the chunk. C5 [64,4096] from a
-      // pageable source: two slots of 32 MiB 94.7-94.9% of the PCIe
-      // ceiling, two of 64 MiB 95.9-96.5%, four of 32 MiB 98.5-98.7% (three
-      // 98.7-99.4%). Calls with fewer chunks keep their two slots.
-      if (!m.direct && opt.chunk_bytes <= 0 && opt.n_buffers == 2 &&
-          (p.units + p.per_chunk - 1) / p.per_chunk >= kTwoSlotSplitChunks)
-        nslots = 4;
     }
     if (!m.direct)
       max_slot = std::max(max_slot, static_cast<size_t>(p.per_chunk * p.unit_wire));
@@ -1160,9 +1155,12 @@ void execute_d2h(Context &ctx, BoundHandle &h, const void *src, size_t src_bytes
   const int64_t row = axis < 0 ? plan.copy_bytes : plan.row, per = axis < 0 ? 1 : plan.per;
   const KArgs &a = dp.base;
   const int64_t total_chunks = plan.outer * ((units + per - 1) / per);
-  // ring slots: n_buffers, at most one per chunk
-  const int nslots = static_cast<int>(
-      std::min<int64_t>(opt.n_buffers > 0 ? opt.n_buffers : 3, total_chunks));
+  // ring slots, at most one per chunk: n_buffers, at least three when the
+  // library picks the chunks (as for uploads)
+  const int asked = opt.n_buffers <= 0 ? 3
+                    : opt.chunk_bytes > 0 ? opt.n_buffers
+                                          : std::max(opt.n_buffers, 3);
+  const int nslots = static_cast<int>(std::min<int64_t>(asked, total_chunks));
   const int ns = call_streams(opt);
   const bool ring_new =
       !pinned && ensure_ring(ctx, nslots, static_cast<size_t>(std::min(per * row, out_bytes)));
