@@ -823,7 +823,8 @@ def summarize_stats(d, probe):
     common grid, their mean and median duration, the algorithmic bytes over
     the mean against 8 TB/s, and the 16-byte copy of the same bytes that the
     probe ran right after them (median duration, the same bytes over it, and
-    the kernel's rate as a fraction of the copy's). Prints a markdown table."""
+    the kernel's rate as a fraction of the copy's; of its two forms, one
+    and two vectors per lane, the faster). Prints a markdown table."""
     rows = _by_dispatch(_csv_rows(d, "kernel_trace.csv"))
     us = lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
     lines = ["| config | kernel | grid (threads) | dispatches | mean us | median us | algorithmic "
@@ -840,7 +841,12 @@ def summarize_stats(d, probe):
         gbs = alg / mean / 1e3
         copy = "| | |"
         if crows:
-            cm = float(np.median([us(r) for r in crows]))
+            # the copy runs in two forms (one and two vectors per lane): the
+            # faster form's median
+            forms = {}
+            for r in crows:
+                forms.setdefault(r["Kernel_Name"], []).append(us(r))
+            cm = min(float(np.median(v)) for v in forms.values())
             cgbs = alg / cm / 1e3
             copy = "%.2f | %.1f | %.3f |" % (cm, cgbs, gbs / cgbs)
         lines.append("| %s | `%s` | %d | %d | %.2f | %.2f | %d | %.1f | %.3f | %s" % (
@@ -1395,7 +1401,7 @@ def headline(torch, P, args, h2d_ceiling, inputs):
                                      "kernel_ms_per_call_events": round(kt["ms"] / max(1, kt["calls"]), 4),
                                      "achieved": round(pipeline_gbs, 1)},
                      "copy_ceiling": {"GBps": round(copy_gbs, 1), "bytes": alg_per_launch,
-                                      "kernel": "16-byte vector copy of the same bytes",
+                                      "kernel": "16-byte vector copy of the same bytes, the faster of one and two vectors per lane",
                                       "frac": round(achieved / copy_gbs, 4)}},
         "cpu_baseline": cpu,
         "cpu_baseline_all_cores": cpu_all,

@@ -535,7 +535,8 @@ double relx_measure_h2d(int device, size_t bytes, int iters, int rounds);
 double relx_measure_d2h(int device, size_t bytes, int iters, int rounds);
 
 /* Measured HBM copy ceiling (GB/s of bytes read + written): a 16-byte vector
- * copy kernel of `bytes` (the stream kernel's access shape) over buffer pairs
+ * copy kernel of `bytes` (wave-contiguous vectors streamed past the caches,
+ * one and then two per lane, the faster form counting) over buffer pairs
  * spanning at least 2 GiB (eight times the Infinity Cache), `iters` copies
  * but at least one per pair, best of `rounds`. The
  * device-side counterpart of relx_measure_h2d; the reference measures its

@@ -1588,7 +1588,7 @@ double measure_copy(int device, size_t bytes, int iters, int rounds, bool d2h) {
   return best;
 }
 
-hipError_t copy16_launch(const void *src, void *dst, uint32_t n16, hipStream_t s);
+hipError_t copy16_launch(const void *src, void *dst, uint32_t n16, int items, hipStream_t s);
 
 double measure_device_copy(int device, size_t bytes, int iters, int rounds) {
   DeviceGuard guard(device);
@@ -1627,19 +1627,24 @@ double measure_device_copy(int device, size_t bytes, int iters, int rounds) {
     HIPCHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
     HIPCHECK(hipEventCreate(&e0));
     HIPCHECK(hipEventCreate(&e1));
-    for (size_t i = 0; i < 2 * sets; ++i)
-      HIPCHECK(copy16_launch(src[i % sets], dst[i % sets], static_cast<uint32_t>(n16), s));
-    HIPCHECK(hipStreamSynchronize(s));
-    for (int r = 0; r < rounds; ++r) {
-      HIPCHECK(hipEventRecord(e0, s));
-      for (int i = 0; i < iters; ++i)
-        HIPCHECK(copy16_launch(src[static_cast<size_t>(i) % sets], dst[static_cast<size_t>(i) % sets],
-                               static_cast<uint32_t>(n16), s));
-      HIPCHECK(hipEventRecord(e1, s));
-      HIPCHECK(hipEventSynchronize(e1));
-      float ms = 0.0f;
-      HIPCHECK(hipEventElapsedTime(&ms, e0, e1));
-      best = std::max(best, 2.0 * static_cast<double>(bytes) * iters / (ms * 1e-3) / 1e9);
+    // both forms of the copy (one and two vectors per lane), the faster one
+    // counts: one is faster from about 128 MB up, two below
+    for (int items = 1; items <= 2; ++items) {
+      for (size_t i = 0; i < 2 * sets; ++i)
+        HIPCHECK(copy16_launch(src[i % sets], dst[i % sets], static_cast<uint32_t>(n16), items, s));
+      HIPCHECK(hipStreamSynchronize(s));
+      for (int r = 0; r < rounds; ++r) {
+        HIPCHECK(hipEventRecord(e0, s));
+        for (int i = 0; i < iters; ++i)
+          HIPCHECK(copy16_launch(src[static_cast<size_t>(i) % sets],
+                                 dst[static_cast<size_t>(i) % sets], static_cast<uint32_t>(n16),
+                                 items, s));
+        HIPCHECK(hipEventRecord(e1, s));
+        HIPCHECK(hipEventSynchronize(e1));
+        float ms = 0.0f;
+        HIPCHECK(hipEventElapsedTime(&ms, e0, e1));
+        best = std::max(best, 2.0 * static_cast<double>(bytes) * iters / (ms * 1e-3) / 1e9);
+      }
     }
   } catch (...) {
     release();

@@ -893,7 +893,7 @@ hipError_t gather_launch(const GatherArgs &a, int op, int nbi, int iw, bool nt, 
       }));
 }
 
-hipError_t copy16_launch(const void *src, void *dst, uint32_t n16, hipStream_t s) {
+hipError_t copy16_launch(const void *src, void *dst, uint32_t n16, int /*items*/, hipStream_t s) {
   const uintptr_t sp = reinterpret_cast<uintptr_t>(src), dp = reinterpret_cast<uintptr_t>(dst);
   const size_t n = static_cast<size_t>(n16) * 16;
   std::lock_guard<std::mutex> g(g_mu);

@@ -96,8 +96,10 @@ def test_probe_dispatches_are_assigned_in_order(tmp_path, capsys):
         add("void relx::k_copy16(...)", 768, dur)
     for dur in (30, 40, 40, 40):                       # config b: the same kernel, other grid
         add("void relx::k_permute8<2, 1, 6, false>(relx::KArgs)", 2048, dur)
-    for dur in (36, 36):
-        add("void relx::k_copy16(...)", 3072, dur)
+    for dur in (36, 36):                               # the copy's two forms: the faster counts
+        add("void relx::k_copy16<1>(...)", 3072, dur)
+    for dur in (44, 44):
+        add("void relx::k_copy16<2>(...)", 1536, dur)
     write_csv(tmp_path / "p_kernel_trace.csv", list(rows[0]), rows)
     k = {"family": "permute", "win": 2, "wout": 1, "dispatches": 4, "skip": 1, "copy_bytes": 1}
     probe = {"kernels": {"a": dict(k, algorithmic_bytes=100000),
