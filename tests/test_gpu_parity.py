@@ -19,6 +19,7 @@ from sym_amd import pyreloc as P
 from sym_amd import workloads as W
 from tests import golden_io as G
 from tests import permute_cases as PC
+from tests import transpose_cases as TC
 from tests.test_encoder import small_cases
 
 pytestmark = pytest.mark.gpu
@@ -394,6 +395,33 @@ def test_random_permutes(ctx):
                         chunk_bytes=4096 if i % 2 else 0, source_pinned=0)
         assert host.tobytes() == want, (i, name, "d2h")
     assert 0 < direct < 200
+
+
+def test_random_one_byte_transposes(ctx):
+    """The 120 random one-byte transposes of the launch tests (128-wide tiles
+    in the rotated order, 64-wide tiles, edge strips, element-wise ones)
+    against the oracle: uploaded with every stage on the device (default and
+    4 KiB chunks), device-resident, and device -> host into pageable memory
+    (default and 4 KiB chunks, alternately)."""
+    wide = 0
+    for i, (name, blob, x, width) in enumerate(TC.random_cases(120)):
+        want = (O.run_typed(blob, {}, {}, x).tobytes() if P.Plan(blob).typed else
+                O.execute_layout(O.bind(O.decode_plan(blob), {}), x.tobytes()))
+        for chunk in (0, 4096):
+            out, rep, b = run_h2d(ctx, blob, {}, {}, x, "random transpose %d %s" % (i, name),
+                                  host_stages=0, chunk_bytes=chunk)
+            assert out.tobytes() == want, (i, name, chunk)
+        wide += b.transpose_tile_q == 128
+        xd = torch.from_numpy(np.ascontiguousarray(x).view(np.uint8).reshape(-1).copy()).cuda()
+        dev = torch.empty(len(want), dtype=torch.uint8, device="cuda")
+        ctx.relayout_device(b, xd.data_ptr(), dev.data_ptr())
+        torch.cuda.synchronize()
+        assert dev.cpu().numpy().tobytes() == want, (i, name, "device")
+        host = np.full(len(want), 0xA5, np.uint8)
+        ctx.execute_d2h(b, xd.data_ptr(), xd.numel(), host.ctypes.data, len(want),
+                        chunk_bytes=4096 if i % 2 else 0, source_pinned=0)
+        assert host.tobytes() == want, (i, name, "d2h")
+    assert wide > 40
 
 
 @pytest.mark.parametrize("B,S", [(1, 65536), (64, 4096)])

@@ -13,6 +13,7 @@ from sym_amd import pyreloc as P
 from sym_amd import workloads as W
 from tests import golden_io as G
 from tests import permute_cases as PC
+from tests import transpose_cases as TC
 
 CHUNKS = [0, 1 << 16, 3 << 20]
 
@@ -80,6 +81,21 @@ def test_transpose_tile_width(rows, cols, tile_q):
         return
     assert b.kernel == "transpose" and b.transpose_tile_q == tile_q
     _check(b, [0, 1, 2], chunks=[0, 1 << 12, 1 << 16, 3 << 20])
+
+
+def test_random_one_byte_transposes():
+    """120 random one-byte transposes (layout, dequantize, dequantize + f16;
+    batched or not; edge strips): each transpose program takes the tile
+    width its q extent allows, and every launch is verified at several
+    chunk sizes."""
+    kinds = set()
+    for name, blob, x, width in TC.random_cases(120):
+        b = P.Bound(P.Plan(blob), {}, {})
+        if b.kernel == "transpose":
+            assert b.transpose_tile_q == width, name
+        kinds.add((b.kernel, b.transpose_tile_q))
+        _check(b, [0], chunks=[0, 4096, 1 << 16])
+    assert kinds == {("transpose", 128), ("transpose", 64), ("generic", 0)}
 
 
 def test_transpose_tile_width_wider_elements():
