@@ -765,11 +765,12 @@ def summarize_trace(d):
 def _kernel_pattern(info):
     """The kernel names a probed config launches: the gather instance it
     names, or its family at its element widths (the one-level interleave,
-    k_interleave1p, and the permute's eight-wave and direct forms included)."""
+    k_interleave1p, the permute's eight-wave and direct forms and the
+    transpose's byte-tile forms included)."""
     import re
     if info.get("pattern"):
         return re.compile(re.escape(info["pattern"]))
-    return re.compile(r"k_%s(1p|8|_direct8?)?<%d, %d" % (info["family"], info["win"], info["wout"]))
+    return re.compile(r"k_%s(1p|8|_direct8?|_b8?)?<%d, %d" % (info["family"], info["win"], info["wout"]))
 
 
 def _by_dispatch(rows):

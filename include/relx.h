@@ -178,8 +178,11 @@ typedef struct relx_bound_info {
   int permute_direct;
   /* transpose programs: the q width (source-contiguous axis) of the tile
    * kernel's tiles, 128 for one-byte sources whose q extent is a multiple of
-   * 128, else 64; 0 for the other kernel families */
+   * 128, else 64; and their c width (destination-contiguous axis), 128 for
+   * four-byte results when q and c both are multiples of 128 (tiles kept in
+   * LDS as bytes), else 64; 0 for the other kernel families */
   int transpose_tile_q;
+  int transpose_tile_c;
 } relx_bound_info;
 
 int relx_bound_query(const relx_bound *bound, relx_bound_info *out);

@@ -355,8 +355,10 @@ int relx_bound_query(const relx_bound *bound, relx_bound_info *out) {
   try {
     const relx::DeviceProgram &dp = const_cast<relx::BoundHandle &>(bound->h).program(0);
     std::snprintf(out->kernel, sizeof(out->kernel), "%s", dp.kernel);
-    if (dp.family == relx::kFamTranspose)
+    if (dp.family == relx::kFamTranspose) {
       out->transpose_tile_q = static_cast<int>(dp.base.t_wq);
+      out->transpose_tile_c = static_cast<int>(dp.base.t_wc);
+    }
     if (dp.family == relx::kFamPermute) {
       const std::vector<relx::KArgs> ls = relx::axis_launches(dp, -1, 0, 0);
       out->permute_direct = ls.empty() ? 0 : 1;

@@ -694,6 +694,126 @@ __global__ __launch_bounds__(kBlock) void k_transpose(KArgs a) {
   }
 }
 
+// One-byte sources with four-byte results whose q and c extents are
+// multiples of 128 (KArgs::t_wc 128): a tile of 128 c by 128 q per block,
+// kept in LDS as bytes already transposed ([q][c], a 16-byte source segment
+// of row c written to column c of 16 rows), and stored in units of one
+// 64-element chunk of one result row: a wave's store instruction covers
+// 64 / L rows of one chunk (L = lanes per chunk), the block's four waves
+// alternate the row's two chunks, so each block writes 512-byte runs of its
+// 128 result rows. int8 [4096, 11008] dequantized to f32 and transposed:
+// 49.7 -> 41.3 us against the 64 c x 128 q word tile; the same tile for
+// f16 results ran 27.8 against 27.9 us and for int8 results 24.2 against
+// 23.4 us, so those keep the word tile. The body is written for any result
+// width.
+template <int WIN, int WOUT, int CH>
+__device__ __forceinline__ void transpose_b_body(const KArgs &a) {
+  static_assert(WIN == 1, "byte tiles hold one-byte source elements");
+  constexpr int TC = 128, TQ = 128;
+  constexpr int PAD = WOUT == 1 ? 16 : 8, P = TC + PAD; // LDS reads of VO bytes stay aligned
+  __shared__ __align__(16) uint8_t tile[TQ * P];        // [q][c]
+  constexpr int VPRI = TQ / 16, NI = TC * VPRI / kBlock;
+  constexpr int VO = 16 / WOUT;          // result elements (source bytes) per 16-byte store
+  constexpr int L = kTile / VO;          // lanes per 64-element chunk of a row
+  constexpr int RPI = 64 / L;            // rows per store instruction
+  constexpr int NCH = TC / kTile;        // chunks per tile row
+  constexpr int NW = kBlock / 64;
+  constexpr int NO = TQ * NCH / (RPI * NW);
+  static_assert(NI * kBlock == TC * VPRI && NO * RPI * NW == TQ * NCH, "whole tiles per block");
+  // the tile reads whole source lines: streaming loads (41.3 against 41.8
+  // us cached)
+  constexpr bool NTL = true;
+  constexpr bool NTS = RELX_NT_STORE(kFamTranspose, 1, WOUT, 1);
+  asm volatile("" ::"s"(a.src), "s"(a.dst), "s"(a.work), "s"(a.sbase), "s"(a.dbase), "s"(a.t_full),
+               "s"(a.t_xcd), "s"(a.t_skew), "s"(a.t_ssc), "s"(a.t_dsq), "s"(gridDim.x));
+  hot(a.t_plane);
+  hot(a.t_group);
+  hot(a.t_g);
+  hot(a.t_tail);
+  hot(a.t_nc);
+  hot_levels<kBatchLevels>(a);
+  hot_chain<CH>(a);
+  const uint32_t t = blockIdx.x;
+  if (t >= a.work)
+    return;
+  uint32_t tq, tc, r2;
+  tile_of(a, t, tq, tc, r2);
+  int64_t sbase = a.sbase, dbase = a.dbase;
+  decompose<kBatchLevels>(a.lv, r2, sbase, dbase); // transposes carry no pads
+  const int64_t q0 = static_cast<int64_t>(tq) * TQ, c0 = static_cast<int64_t>(tc) * TC;
+  vec4 in[NI];
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    const int vid = threadIdx.x + j * kBlock;
+    const int row = vid / VPRI, cv = vid % VPRI;
+    in[j] = ld16<NTL>(reinterpret_cast<const vec4 *>(a.src + sbase + (c0 + row) * a.t_ssc + q0 + cv * 16));
+  }
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, k = lane / L, v = lane % L;
+  // store j of this lane: tile row and chunk, result offset (recomputed after
+  // the barrier rather than held across it, which would cost the kernel half
+  // its waves)
+  auto unit = [&](int j, int &row, int &ch) {
+    const int ins = j * NW + wv;
+    ch = ins % NCH;
+    row = (ins / NCH) * RPI + k;
+  };
+  const int64_t drow = dbase + q0 * a.t_dsq + c0 + v * VO;
+  VecParams par[NO];
+#pragma unroll
+  for (int j = 0; j < NO; ++j) {
+    int row, ch;
+    unit(j, row, ch);
+    par[j] = fetch_params<CH>(a, drow + row * a.t_dsq + ch * kTile);
+  }
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    const int vid = threadIdx.x + j * kBlock;
+    const int row = vid / VPRI, cv = vid % VPRI;
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      tile[(cv * 16 + e) * P + row] = static_cast<uint8_t>(in[j][e >> 2] >> ((e & 3) * 8));
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < NO; ++j) {
+    int row, ch;
+    unit(j, row, ch);
+    const uint8_t *tp = tile + row * P + ch * kTile + v * VO;
+    const int64_t dof = drow + row * a.t_dsq + ch * kTile;
+    vec4 w = {0u, 0u, 0u, 0u};
+    if constexpr (VO == 16) {
+      w = *reinterpret_cast<const vec4 *>(tp);
+    } else if constexpr (VO == 8) {
+      const uint2 b = *reinterpret_cast<const uint2 *>(tp);
+      w.x = b.x;
+      w.y = b.y;
+    } else {
+      w.x = *reinterpret_cast<const uint32_t *>(tp);
+    }
+    uint32_t val[VO];
+    unpack<1, VO>(&w, val);
+    chain_vec_p<CH, VO>(a, val, dof, par[j]);
+    vec4 out;
+    pack<WOUT, VO>(val, &out);
+    st16<NTS>(reinterpret_cast<vec4 *>(a.dst + dof * WOUT), out);
+  }
+}
+
+template <int WIN, int WOUT, int CH>
+__global__ __launch_bounds__(kBlock) void k_transpose_b(KArgs a) {
+  transpose_b_body<WIN, WOUT, CH>(a);
+}
+
+// The compile-time chains at eight waves per SIMD (at most 64 VGPRs, no
+// spill; unbounded, int8 -> f16 dequantization takes 70 and seven waves,
+// and int8 -> f32 measured 42.3 against 41.8 us). The generic per-stage
+// chain would spill under the bound and keeps the kernel above.
+template <int WIN, int WOUT, int CH>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_transpose_b8(
+    KArgs a) {
+  transpose_b_body<WIN, WOUT, CH>(a);
+}
+
 // ------------------------------------------------------------ interleave
 
 // Axes: [batch..., P, C] with C (padded to CP) innermost in the destination
@@ -1163,7 +1283,14 @@ hipError_t stream_launch(const KArgs &a, hipStream_t s) {
 template <int WIN, int WOUT, int CH>
 hipError_t transpose_launch(const KArgs &a, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(a.work)), block(kBlock);
-  if (a.t_wq == 128) {
+  if (a.t_wc == 128) {
+    if constexpr (WIN == 1 && WOUT == 4 && CH != kChainGeneric)
+      hipLaunchKernelGGL((k_transpose_b8<WIN, WOUT, CH>), grid, block, 0, s, a);
+    else if constexpr (WIN == 1 && WOUT == 4)
+      hipLaunchKernelGGL((k_transpose_b<WIN, WOUT, CH>), grid, block, 0, s, a);
+    else
+      return hipErrorInvalidValue;
+  } else if (a.t_wq == 128) {
     if constexpr (WIN == 1)
       hipLaunchKernelGGL((k_transpose<WIN, WOUT, CH, 128>), grid, block, 0, s, a);
     else

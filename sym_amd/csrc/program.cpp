@@ -513,9 +513,11 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
           family = kFamTranspose;
           dp->qa = qa;
           dp->ca = r - 1;
-          // one-byte sources take tiles 128 q wide when q allows it: each
-          // tile row then reads a whole 128-byte line
+          // one-byte sources take tiles 128 q wide when q allows it (each
+          // tile row then reads a whole 128-byte line); with four-byte
+          // results, 128 c wide too, kept in LDS as bytes, when c allows it
           a.t_wq = win == 1 && a.vext[qa] % 128 == 0 ? 128 : 64;
+          a.t_wc = a.t_wq == 128 && wout == 4 && a.vext[r - 1] % 128 == 0 ? 128 : 64;
         }
       }
     }
@@ -566,7 +568,7 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
         if (family == kFamStream && ax == r - 1)
           dp->chunk_align = V;
         else if (family == kFamTranspose && (ax == dp->qa || ax == dp->ca))
-          dp->chunk_align = ax == dp->qa ? a.t_wq : 64;
+          dp->chunk_align = ax == dp->qa ? a.t_wq : a.t_wc;
         else if (family == kFamInterleave && ax == r - 2)
           dp->chunk_align = a.vec;
         // an interleave launch writes every channel of its pixels, so its
@@ -602,7 +604,7 @@ int64_t box_work(const DeviceProgram &dp, const Box &b) {
     if (dp.family == kFamStream && i == r - 1)
       e /= a.vec;
     else if (dp.family == kFamTranspose && (i == dp.qa || i == dp.ca))
-      e /= i == dp.qa ? a.t_wq : 64;
+      e /= i == dp.qa ? a.t_wq : a.t_wc;
     else if (dp.family == kFamInterleave && i == r - 2)
       e /= a.vec;
     else if (dp.family == kFamInterleave && i == r - 1)
@@ -624,7 +626,7 @@ int64_t split_align(const DeviceProgram &dp, int i) {
   if (dp.family == kFamStream && i == r - 1)
     return dp.base.vec;
   if (dp.family == kFamTranspose && (i == dp.qa || i == dp.ca))
-    return i == dp.qa ? dp.base.t_wq : 64;
+    return i == dp.qa ? dp.base.t_wq : dp.base.t_wc;
   if (dp.family == kFamInterleave && i == r - 2)
     return dp.base.vec;
   if (dp.family == kFamInterleave && i == r - 1)
@@ -832,7 +834,7 @@ KArgs launch_args(const DeviceProgram &dp, const Box &b) {
       // (30.0 -> 27.1 us); 64-wide one-byte tiles q fastest, grouped by XCD
       // so that the two halves of each source line meet in one L2; wider
       // elements in groups of kTileGroup q-tiles
-      const int64_t nq = b.ext[dp.qa] / a.t_wq, nc = b.ext[dp.ca] / 64;
+      const int64_t nq = b.ext[dp.qa] / a.t_wq, nc = b.ext[dp.ca] / a.t_wc;
       const bool bytes = a.win == 1, wide = a.t_wq == 128;
       const int64_t g = bytes ? nq : std::min<int64_t>(kTileGroup, nq);
       const int64_t full = nq / g * g;
@@ -925,7 +927,7 @@ std::vector<KArgs> prefix_launches(const DeviceProgram &dp, const int64_t *fixed
   // whole tiles go to the tile kernel, the strips past them (the q strip
   // over the whole c range, the c strip beside the whole q tiles) to the
   // element-wise kernel. Box starts on those axes are multiples of the tile
-  // (64, t_wq along q: chunks and splits keep the tile alignment).
+  // (t_wq along q, t_wc along c: chunks and splits keep the tile alignment).
   std::vector<Box> edges;
   if (dp.family == kFamStream && a.rank == 1 && b.ext[0] % a.vec != 0) {
     // the tail of a single contiguous axis (box starts are multiples of V)
@@ -938,8 +940,8 @@ std::vector<KArgs> prefix_launches(const DeviceProgram &dp, const int64_t *fixed
   }
   if (dp.family == kFamTranspose) {
     const int q = dp.qa, c = dp.ca;
-    const int64_t wq = a.t_wq;
-    const int64_t mq = b.ext[q] / wq * wq, mc = b.ext[c] / 64 * 64;
+    const int64_t wq = a.t_wq, wc = a.t_wc;
+    const int64_t mq = b.ext[q] / wq * wq, mc = b.ext[c] / wc * wc;
     if (mq < b.ext[q]) {
       Box e = b;
       e.lo[q] = b.lo[q] + mq;
@@ -1080,9 +1082,9 @@ void verify_launch(const DeviceProgram &dp_in, const KArgs &a) {
     if (a.work64 > (int64_t{1} << 22) || a.work != a.work64)
       bad_launch(dp, "more tiles than one launch takes");
     const int VO = 16 / wout;
-    const int64_t TQ = a.t_wq;
-    if (!(TQ == 64 || (TQ == 128 && win == 1)) || a.t_nc.d != a.t_group.d / a.t_g.d ||
-        (a.t_skew && a.t_xcd))
+    const int64_t TQ = a.t_wq, TC = a.t_wc;
+    if (!(TQ == 64 || (TQ == 128 && win == 1)) || !(TC == 64 || (TC == 128 && TQ == 128)) ||
+        a.t_nc.d != a.t_group.d / a.t_g.d || (a.t_skew && a.t_xcd) || (TC == 128 && a.t_xcd))
       bad_launch(dp, "tile geometry disagrees with the kernel");
     std::vector<bool> seen(a.work, false); // the order must be a bijection
     for (uint32_t blk = 0; blk < a.work; ++blk) { // grid = one block per tile
@@ -1101,10 +1103,10 @@ void verify_launch(const DeviceProgram &dp_in, const KArgs &a) {
       int64_t sbase = a.sbase, dbase = a.dbase;
       if (decompose_rt(kBatchLevels, a.lv, r2, sbase, dbase))
         bad_launch(dp, "a transpose tile reaches a pad");
-      const int64_t q0 = int64_t{tq} * TQ, c0 = int64_t{tc} * 64;
-      // a tile row moves as 16-byte vectors: 64 source rows of TQ elements,
-      // TQ destination rows of 64
-      for (int64_t row = 0; row < 64; row += 63) {
+      const int64_t q0 = int64_t{tq} * TQ, c0 = int64_t{tc} * TC;
+      // a tile row moves as 16-byte vectors: TC source rows of TQ elements,
+      // TQ destination rows of TC
+      for (int64_t row = 0; row < TC; row += TC - 1) {
         const int64_t so = sbase + (c0 + row) * a.t_ssc + q0;
         ck.src_run(so, TQ, false);
         if ((so * win) % 16 != 0)
@@ -1112,14 +1114,14 @@ void verify_launch(const DeviceProgram &dp_in, const KArgs &a) {
       }
       for (int64_t row = 0; row < TQ; row += TQ - 1) {
         const int64_t d = dbase + (q0 + row) * a.t_dsq + c0;
-        ck.dst_run(d, 64, false);
+        ck.dst_run(d, TC, false);
         if ((d * wout) % 16 != 0)
           bad_launch(dp, "a tile row is not 16-byte aligned");
       }
       if ((a.t_ssc * win) % 16 != 0 || (a.t_dsq * wout) % 16 != 0)
         bad_launch(dp, "row strides break 16-byte alignment");
       for (int64_t row = 0; row < TQ; ++row)
-        for (int cv = 0; cv < 64; cv += VO)
+        for (int64_t cv = 0; cv < TC; cv += VO)
           ck.channels(dbase + (q0 + row) * a.t_dsq + c0 + cv, VO);
     }
     break;

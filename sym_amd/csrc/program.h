@@ -168,14 +168,18 @@ struct KArgs {
   uint32_t fill;      // pad fill bits (fast families move elements of at most 4 bytes)
   int64_t sbase, dbase; // element offsets of the box origin (source: of its valid origin)
   Level lv[kMaxRank];   // stream: box axes (innermost in vectors); 2-D families: batch axes
-  // transpose: tiles of t_wq q by 64 c along the source-inner axis q
+  // transpose: tiles of t_wq q by t_wc c along the source-inner axis q
   // (destination rows) and the destination-inner axis c, visited in groups
   // of g q-tiles (see tile_of): plane = nq * nc tiles, group = g * nc tiles,
   // g, tail = the q-tiles of the last, partial group, nc = c-tiles
   FastDiv t_plane, t_group, t_g, t_tail, t_nc;
   uint32_t t_full; // q-tiles in whole groups
   uint32_t t_xcd;  // 1: each XCD takes a contiguous run of the order
-  uint32_t t_wq;   // q-tile width: 64, or 128 for one-byte sources
+  // q-tile width (64, or 128 for one-byte sources) and c-tile width (64, or
+  // 128 for one-byte sources with four-byte results: byte tiles), read on
+  // the host only; 16 bits each keep the fields the kernels read where they
+  // were
+  uint16_t t_wq, t_wc;
   uint32_t t_skew; // 1: q-tile tq visits its c-tiles rotated by tq (mod nc)
   int64_t t_ssc, t_dsq; // source stride of c, destination stride of q
   // interleave: pixel groups along the source-contiguous axis p; channel axis c

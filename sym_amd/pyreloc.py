@@ -337,6 +337,13 @@ class Bound:
         kernel families)."""
         return self.info.transpose_tile_q
 
+    @property
+    def transpose_tile_c(self):
+        """c width of a transpose program's tiles (128 for a one-byte source
+        with four-byte results whose q and c extents allow it, else 64; 0
+        for other kernel families)."""
+        return self.info.transpose_tile_c
+
     def bytes_at(self, boundary):
         return self.info.bytes_at[boundary]
 

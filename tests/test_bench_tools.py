@@ -45,6 +45,10 @@ def test_union_of_intervals():
      {"family": "interleave", "win": 4, "wout": 2}, True),
     ("void relx::(anonymous namespace)::k_transpose<4, 4, 1>(relx::KArgs)",
      {"family": "transpose", "win": 1, "wout": 2}, False),
+    ("void relx::(anonymous namespace)::k_transpose_b8<1, 2, 4>(relx::KArgs)",
+     {"family": "transpose", "win": 1, "wout": 2}, True),
+    ("void relx::(anonymous namespace)::k_transpose<1, 2, 4, 128>(relx::KArgs)",
+     {"family": "transpose", "win": 1, "wout": 2}, True),
     ("void relx::(anonymous namespace)::k_gather<1, 16, 4, true>(relx::GatherArgs)",
      {"pattern": "k_gather<1, 16, 4, true>"}, True),
 ])

@@ -398,12 +398,13 @@ def test_random_permutes(ctx):
 
 
 def test_random_one_byte_transposes(ctx):
-    """The 120 random one-byte transposes of the launch tests (128-wide tiles
-    in the rotated order, 64-wide tiles, edge strips, element-wise ones)
+    """The 120 random one-byte transposes of the launch tests (128 x 128 byte
+    tiles and 64 c x 128 q tiles in the rotated order, 64-wide tiles, edge
+    strips, element-wise ones)
     against the oracle: uploaded with every stage on the device (default and
     4 KiB chunks), device-resident, and device -> host into pageable memory
     (default and 4 KiB chunks, alternately)."""
-    wide = 0
+    wide = byte_tiles = 0
     for i, (name, blob, x, width) in enumerate(TC.random_cases(120)):
         want = (O.run_typed(blob, {}, {}, x).tobytes() if P.Plan(blob).typed else
                 O.execute_layout(O.bind(O.decode_plan(blob), {}), x.tobytes()))
@@ -412,6 +413,7 @@ def test_random_one_byte_transposes(ctx):
                                   host_stages=0, chunk_bytes=chunk)
             assert out.tobytes() == want, (i, name, chunk)
         wide += b.transpose_tile_q == 128
+        byte_tiles += b.transpose_tile_c == 128
         xd = torch.from_numpy(np.ascontiguousarray(x).view(np.uint8).reshape(-1).copy()).cuda()
         dev = torch.empty(len(want), dtype=torch.uint8, device="cuda")
         ctx.relayout_device(b, xd.data_ptr(), dev.data_ptr())
@@ -421,7 +423,7 @@ def test_random_one_byte_transposes(ctx):
         ctx.execute_d2h(b, xd.data_ptr(), xd.numel(), host.ctypes.data, len(want),
                         chunk_bytes=4096 if i % 2 else 0, source_pinned=0)
         assert host.tobytes() == want, (i, name, "d2h")
-    assert wide > 40
+    assert wide > 40 and byte_tiles >= 5
 
 
 @pytest.mark.parametrize("B,S", [(1, 65536), (64, 4096)])

@@ -9,6 +9,7 @@ several chunk sizes."""
 import numpy as np
 import pytest
 
+from sym_amd import encoder as EN
 from sym_amd import pyreloc as P
 from sym_amd import workloads as W
 from tests import golden_io as G
@@ -61,26 +62,33 @@ def test_c3_launches():
     b = P.Bound(P.Plan(W.c3_plan().blob), {"s0": 4096, "s1": 11008},
                 W.param("scale", np.ones(11008, np.float32)))
     # 11008 = 86 x 128: one-byte source rows read as whole 128-byte lines
-    assert b.kernel == "transpose" and b.transpose_tile_q == 128
+    assert b.kernel == "transpose" and (b.transpose_tile_q, b.transpose_tile_c) == (128, 64)
     _check(b, [0])
 
 
-@pytest.mark.parametrize("rows,cols,tile_q", [(4096, 11008, 128), (256, 4032, 64), (192, 4160, 64),
-                                              (4000, 11008, 128), (128, 128, 128), (64, 64, 64),
-                                              (100, 300, 128)])
-def test_transpose_tile_width(rows, cols, tile_q):
+@pytest.mark.parametrize("f32", [False, True])
+@pytest.mark.parametrize("rows,cols,tile_q,tile_c", [(4096, 11008, 128, 128), (256, 4032, 64, 64),
+                                                     (192, 4160, 64, 64), (4000, 11008, 128, 64),
+                                                     (128, 128, 128, 128), (64, 64, 64, 64),
+                                                     (192, 256, 128, 64), (100, 300, 128, 64)])
+def test_transpose_tile_width(rows, cols, tile_q, tile_c, f32):
     """One-byte transposes take tiles 128 q wide when the source-contiguous
-    extent is a multiple of 128 (edge strips element-wise), else 64; the
+    extent is a multiple of 128 (edge strips element-wise), else 64, and
+    with f32 results 128 c wide byte tiles when the c extent is a multiple
+    of 128 too; the
     verifier walks the rotated tile order of the wide tiles (a bijection onto
     the plane) at several chunk sizes, so chunk boundaries along c and q
     keep the tile alignment."""
-    b = P.Bound(P.Plan(W.c3_plan().blob), {"s0": rows, "s1": cols},
-                W.param("scale", np.ones(cols, np.float32)))
+    scale = EN.BindingParam("scale", "float32", ("s1",))
+    ops = [EN.Dequantize(scale, axis=1)] + ([] if f32 else [EN.Cast("float16")])
+    plan = EN.encode(["s0", "s1"], "int8", ops + [EN.Transpose((1, 0))])
+    b = P.Bound(P.Plan(plan.blob), {"s0": rows, "s1": cols}, W.param("scale", np.ones(cols, np.float32)))
     if cols % 16:
         assert b.kernel != "transpose"
         return
-    assert b.kernel == "transpose" and b.transpose_tile_q == tile_q
-    _check(b, [0, 1, 2], chunks=[0, 1 << 12, 1 << 16, 3 << 20])
+    want_c = tile_c if f32 else 64
+    assert b.kernel == "transpose" and (b.transpose_tile_q, b.transpose_tile_c) == (tile_q, want_c)
+    _check(b, range(len(b.footprints())), chunks=[0, 1 << 12, 1 << 16, 3 << 20])
 
 
 def test_random_one_byte_transposes():
@@ -92,16 +100,17 @@ def test_random_one_byte_transposes():
     for name, blob, x, width in TC.random_cases(120):
         b = P.Bound(P.Plan(blob), {}, {})
         if b.kernel == "transpose":
-            assert b.transpose_tile_q == width, name
-        kinds.add((b.kernel, b.transpose_tile_q))
+            assert (b.transpose_tile_q, b.transpose_tile_c) == width, name
+        kinds.add((b.kernel, b.transpose_tile_q, b.transpose_tile_c))
         _check(b, [0], chunks=[0, 4096, 1 << 16])
-    assert kinds == {("transpose", 128), ("transpose", 64), ("generic", 0)}
+    assert kinds == {("transpose", 128, 128), ("transpose", 128, 64), ("transpose", 64, 64),
+                     ("generic", 0, 0)}
 
 
 def test_transpose_tile_width_wider_elements():
     """Sources of two and four bytes keep 64-wide tiles."""
     b = P.Bound(P.Plan(W.c1_plan().blob), {"s0": 64 * 4096})
-    assert b.kernel == "transpose" and b.transpose_tile_q == 64
+    assert b.kernel == "transpose" and (b.transpose_tile_q, b.transpose_tile_c) == (64, 64)
     b = P.Bound(P.Plan(W.c4_plan().blob), {"s0": 512, "s1": 256},
                 W.param("scale", np.ones(512, np.float32)))
     assert b.transpose_tile_q == 0

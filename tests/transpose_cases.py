@@ -2,9 +2,9 @@
 [B, Q, R]) with the value chains the transpose kernel runs: layout only,
 dequantize (per tensor or along an axis, with zero points), and
 dequantize then cast to f16. Source-contiguous extents Q that are multiples
-of 128 take tiles 128 q wide in the rotated order, others 64-wide tiles; R
-extents that are not multiples of 64 leave an edge strip to the element-wise
-kernel (R = 100 also breaks the 16-byte row alignment of one- and two-byte
+of 128 take tiles 128 q wide in the rotated order (with f32 results, 128 c
+wide byte tiles when R is a multiple of 128 too), others 64-wide tiles; R extents that are
+not multiples of the tile leave an edge strip to the element-wise kernel (R = 100 also breaks the 16-byte row alignment of one- and two-byte
 results, which then run element-wise throughout). Used by the CPU launch checks (every launch verified, the tile width
 asserted) and by the GPU parity test against the oracle.
 """
@@ -13,7 +13,7 @@ import numpy as np
 from sym_amd import encoder as EN
 
 QS = (64, 128, 192, 256, 384, 1152)
-RS = (64, 100, 128, 160, 320)
+RS = (64, 100, 128, 160, 256, 320)
 
 
 def _chain(rng, shape):
@@ -33,8 +33,8 @@ def _chain(rng, shape):
 
 
 def random_cases(n, seed=11):
-    """(name, plan blob, source array, expected q-tile width) for n random
-    one-byte transposes."""
+    """(name, plan blob, source array, expected (q, c) tile widths) for n
+    random one-byte transposes."""
     rng = np.random.default_rng(seed)
     out = []
     while len(out) < n:
@@ -49,6 +49,7 @@ def random_cases(n, seed=11):
         except EN.EncodeError:
             continue
         x = rng.integers(-128, 128, shape, dtype=np.int8)
-        width = 128 if q % 128 == 0 else 64
+        f32 = [type(o).__name__ for o in ops] == ["Dequantize"]
+        width = (128 if q % 128 == 0 else 64, 128 if q % 128 == 0 and r % 128 == 0 and f32 else 64)
         out.append(("int8 %s %s" % (shape, [type(o).__name__ for o in ops]), plan.blob, x, width))
     return out
