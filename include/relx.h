@@ -179,10 +179,14 @@ typedef struct relx_bound_info {
   /* transpose programs: the q width (source-contiguous axis) of the tile
    * kernel's tiles, 128 for one-byte sources whose q extent is a multiple of
    * 128, else 64; and their c width (destination-contiguous axis), 128 for
-   * four-byte results when q and c both are multiples of 128 (tiles kept in
-   * LDS as bytes), else 64; 0 for the other kernel families */
+   * two- and four-byte results when q and c both are multiples of 128 (tiles
+   * kept in LDS as bytes), else 64; 0 for the other kernel families */
   int transpose_tile_q;
   int transpose_tile_c;
+  /* transpose programs: 1 when every launch of the whole box indexes the
+   * parameters of its dequantize -> f16 chain by destination row (one
+   * channel per row, proven per launch), else 0 */
+  int transpose_row_params;
 } relx_bound_info;
 
 int relx_bound_query(const relx_bound *bound, relx_bound_info *out);

@@ -56,7 +56,8 @@ class relx_bound_info(ctypes.Structure):
                 ("indexed", ctypes.c_int), ("table_rows", ctypes.c_int64),
                 ("row_elements", ctypes.c_int64), ("table_bytes", ctypes.c_int64),
                 ("index_count", ctypes.c_int64), ("permute_direct", ctypes.c_int),
-                ("transpose_tile_q", ctypes.c_int), ("transpose_tile_c", ctypes.c_int)]
+                ("transpose_tile_q", ctypes.c_int), ("transpose_tile_c", ctypes.c_int),
+                ("transpose_row_params", ctypes.c_int)]
 
 
 class relx_ctx_stats(ctypes.Structure):

@@ -358,6 +358,14 @@ int relx_bound_query(const relx_bound *bound, relx_bound_info *out) {
     if (dp.family == relx::kFamTranspose) {
       out->transpose_tile_q = static_cast<int>(dp.base.t_wq);
       out->transpose_tile_c = static_cast<int>(dp.base.t_wc);
+      const std::vector<relx::KArgs> ls = relx::axis_launches(dp, -1, 0, 0);
+      int tiles = 0, rows = 0;
+      for (const relx::KArgs &a : ls)
+        if (!a.edge_box) {
+          ++tiles;
+          rows += (a.t_flags & relx::kTileRowChannel) ? 1 : 0;
+        }
+      out->transpose_row_params = tiles > 0 && rows == tiles ? 1 : 0;
     }
     if (dp.family == relx::kFamPermute) {
       const std::vector<relx::KArgs> ls = relx::axis_launches(dp, -1, 0, 0);

@@ -64,7 +64,7 @@ __host__ __device__ __forceinline__ uint32_t xcd_tile(uint32_t b, uint32_t n) {
 // Tile t of a transpose launch -> (q-tile, c-tile, batch index). Within a
 // batch element's plane of nq x nc tiles, whole groups of g q-tiles come
 // first (q fastest, then c), then the partial group of the remaining q-tiles.
-// With t_skew, q-tile tq takes c-tile (c + tq) mod nc at step c, so the
+// With kTileSkew, q-tile tq takes c-tile (c + tq) mod nc at step c, so the
 // blocks in flight, which share c while q runs fastest, write their
 // destination rows at different column offsets.
 __host__ __device__ __forceinline__ void tile_of(const KArgs &a, uint32_t t, uint32_t &tq,
@@ -84,7 +84,7 @@ __host__ __device__ __forceinline__ void tile_of(const KArgs &a, uint32_t t, uin
     tq = a.t_full + (r - c * a.t_tail.d);
     tc = c;
   }
-  if (a.t_skew) {
+  if (a.t_flags & kTileSkew) {
     const uint32_t x = tc + (tq - fdiv(tq, a.t_nc) * nc); // < 2 nc
     tc = x >= nc ? x - nc : x;
   }

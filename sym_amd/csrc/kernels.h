@@ -632,7 +632,7 @@ __global__ __launch_bounds__(kBlock) void k_transpose(KArgs a) {
   constexpr bool NTL = RELX_NT_LOAD(kFamTranspose, WIN, WOUT, 1);
   constexpr bool NTS = RELX_NT_STORE(kFamTranspose, WIN, WOUT, 1);
   asm volatile("" ::"s"(a.src), "s"(a.dst), "s"(a.work), "s"(a.sbase), "s"(a.dbase), "s"(a.t_full),
-               "s"(a.t_xcd), "s"(a.t_skew), "s"(a.t_ssc), "s"(a.t_dsq), "s"(gridDim.x));
+               "s"(a.t_flags), "s"(a.t_choff), "s"(a.t_ssc), "s"(a.t_dsq), "s"(gridDim.x));
   hot(a.t_plane);
   hot(a.t_group);
   hot(a.t_g);
@@ -640,7 +640,7 @@ __global__ __launch_bounds__(kBlock) void k_transpose(KArgs a) {
   hot(a.t_nc);
   hot_levels<kBatchLevels>(a);
   hot_chain<CH>(a);
-  const uint32_t t = a.t_xcd ? xcd_tile(blockIdx.x, gridDim.x) : blockIdx.x;
+  const uint32_t t = (a.t_flags & kTileXcd) ? xcd_tile(blockIdx.x, gridDim.x) : blockIdx.x;
   if (t >= a.work)
     return;
   uint32_t tq, tc, r2;
@@ -706,9 +706,10 @@ __global__ __launch_bounds__(kBlock) void k_transpose(KArgs a) {
 // f16 results ran 27.8 against 27.9 us and for int8 results 24.2 against
 // 23.4 us, so those keep the word tile. The body is written for any result
 // width.
-template <int WIN, int WOUT, int CH>
+template <int WIN, int WOUT, int CH, bool ROWCH, bool ZP0 = false>
 __device__ __forceinline__ void transpose_b_body(const KArgs &a) {
   static_assert(WIN == 1, "byte tiles hold one-byte source elements");
+  static_assert(!ROWCH || CH == kChainDeqF16, "row channels index the f16 dequantize's parameters");
   constexpr int TC = 128, TQ = 128;
   constexpr int PAD = WOUT == 1 ? 16 : 8, P = TC + PAD; // LDS reads of VO bytes stay aligned
   __shared__ __align__(16) uint8_t tile[TQ * P];        // [q][c]
@@ -725,7 +726,7 @@ __device__ __forceinline__ void transpose_b_body(const KArgs &a) {
   constexpr bool NTL = true;
   constexpr bool NTS = RELX_NT_STORE(kFamTranspose, 1, WOUT, 1);
   asm volatile("" ::"s"(a.src), "s"(a.dst), "s"(a.work), "s"(a.sbase), "s"(a.dbase), "s"(a.t_full),
-               "s"(a.t_xcd), "s"(a.t_skew), "s"(a.t_ssc), "s"(a.t_dsq), "s"(gridDim.x));
+               "s"(a.t_flags), "s"(a.t_choff), "s"(a.t_ssc), "s"(a.t_dsq), "s"(gridDim.x));
   hot(a.t_plane);
   hot(a.t_group);
   hot(a.t_g);
@@ -759,11 +760,44 @@ __device__ __forceinline__ void transpose_b_body(const KArgs &a) {
   };
   const int64_t drow = dbase + q0 * a.t_dsq + c0 + v * VO;
   VecParams par[NO];
+  if constexpr (ROWCH) {
+    // kTileRowChannel: the channel of row q of the box is t_choff + q; a
+    // per-tensor zero point is read once
+    const DevStage &s = a.chain.st[0];
+    const uint32_t c0r = a.t_choff + static_cast<uint32_t>(q0);
+    if (ZP0) { // kTileZeroPoint0 (2% on C3 against a zero read from the table)
 #pragma unroll
-  for (int j = 0; j < NO; ++j) {
-    int row, ch;
-    unit(j, row, ch);
-    par[j] = fetch_params<CH>(a, drow + row * a.t_dsq + ch * kTile);
+      for (int j = 0; j < NO; ++j) {
+        int row, ch;
+        unit(j, row, ch);
+        par[j].sc = a.pf[s.scale_off + c0r + row];
+        par[j].zp = 0;
+      }
+    } else if (s.zp_per_ch) {
+#pragma unroll
+      for (int j = 0; j < NO; ++j) {
+        int row, ch;
+        unit(j, row, ch);
+        par[j].sc = a.pf[s.scale_off + c0r + row];
+        par[j].zp = a.pi[s.zp_off + c0r + row];
+      }
+    } else {
+      const int32_t zp = a.pi[s.zp_off];
+#pragma unroll
+      for (int j = 0; j < NO; ++j) {
+        int row, ch;
+        unit(j, row, ch);
+        par[j].sc = a.pf[s.scale_off + c0r + row];
+        par[j].zp = zp;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < NO; ++j) {
+      int row, ch;
+      unit(j, row, ch);
+      par[j] = fetch_params<CH>(a, drow + row * a.t_dsq + ch * kTile);
+    }
   }
 #pragma unroll
   for (int j = 0; j < NI; ++j) {
@@ -801,17 +835,17 @@ __device__ __forceinline__ void transpose_b_body(const KArgs &a) {
 
 template <int WIN, int WOUT, int CH>
 __global__ __launch_bounds__(kBlock) void k_transpose_b(KArgs a) {
-  transpose_b_body<WIN, WOUT, CH>(a);
+  transpose_b_body<WIN, WOUT, CH, false>(a);
 }
 
 // The compile-time chains at eight waves per SIMD (at most 64 VGPRs, no
 // spill; unbounded, int8 -> f16 dequantization takes 70 and seven waves,
 // and int8 -> f32 measured 42.3 against 41.8 us). The generic per-stage
 // chain would spill under the bound and keeps the kernel above.
-template <int WIN, int WOUT, int CH>
+template <int WIN, int WOUT, int CH, bool ROWCH, bool ZP0>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_transpose_b8(
     KArgs a) {
-  transpose_b_body<WIN, WOUT, CH>(a);
+  transpose_b_body<WIN, WOUT, CH, ROWCH, ZP0>(a);
 }
 
 // ------------------------------------------------------------ interleave
@@ -1284,12 +1318,26 @@ template <int WIN, int WOUT, int CH>
 hipError_t transpose_launch(const KArgs &a, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(a.work)), block(kBlock);
   if (a.t_wc == 128) {
-    if constexpr (WIN == 1 && WOUT == 4 && CH != kChainGeneric)
-      hipLaunchKernelGGL((k_transpose_b8<WIN, WOUT, CH>), grid, block, 0, s, a);
-    else if constexpr (WIN == 1 && WOUT == 4)
+    if constexpr (WIN == 1 && WOUT == 2 && CH == kChainDeqF16) {
+      // parameters by row at eight waves; the channel computed from each
+      // vector's offset needs 65 registers, so that form runs unbounded
+      if ((a.t_flags & kTileRowChannel) && (a.t_flags & kTileZeroPoint0))
+        hipLaunchKernelGGL((k_transpose_b8<WIN, WOUT, CH, true, true>), grid, block, 0, s, a);
+      else if (a.t_flags & kTileRowChannel)
+        hipLaunchKernelGGL((k_transpose_b8<WIN, WOUT, CH, true, false>), grid, block, 0, s, a);
+      else
+        hipLaunchKernelGGL((k_transpose_b<WIN, WOUT, CH>), grid, block, 0, s, a);
+    } else if constexpr (WIN == 1 && WOUT == 4 && CH != kChainGeneric) {
+      if (a.t_flags & kTileRowChannel)
+        return hipErrorInvalidValue;
+      hipLaunchKernelGGL((k_transpose_b8<WIN, WOUT, CH, false, false>), grid, block, 0, s, a);
+    } else if constexpr (WIN == 1 && WOUT >= 2) {
+      if (a.t_flags & kTileRowChannel)
+        return hipErrorInvalidValue;
       hipLaunchKernelGGL((k_transpose_b<WIN, WOUT, CH>), grid, block, 0, s, a);
-    else
+    } else {
       return hipErrorInvalidValue;
+    }
   } else if (a.t_wq == 128) {
     if constexpr (WIN == 1)
       hipLaunchKernelGGL((k_transpose<WIN, WOUT, CH, 128>), grid, block, 0, s, a);

@@ -514,10 +514,11 @@ std::unique_ptr<DeviceProgram> build_program(const Bound &b, const Prepared &p, 
           dp->qa = qa;
           dp->ca = r - 1;
           // one-byte sources take tiles 128 q wide when q allows it (each
-          // tile row then reads a whole 128-byte line); with four-byte
-          // results, 128 c wide too, kept in LDS as bytes, when c allows it
+          // tile row then reads a whole 128-byte line); with two- and
+          // four-byte results, 128 c wide too, kept in LDS as bytes, when c
+          // allows it
           a.t_wq = win == 1 && a.vext[qa] % 128 == 0 ? 128 : 64;
-          a.t_wc = a.t_wq == 128 && wout == 4 && a.vext[r - 1] % 128 == 0 ? 128 : 64;
+          a.t_wc = a.t_wq == 128 && wout >= 2 && a.vext[r - 1] % 128 == 0 ? 128 : 64;
         }
       }
     }
@@ -752,6 +753,41 @@ KArgs edge_args(const DeviceProgram &dp, const Box &b) {
 
 bool pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 
+// A byte-tile transpose launch indexes the parameters of its dequantize ->
+// f16 chain by destination row (kTileRowChannel) when the stage has one
+// channel per
+// destination row of the box. For a result offset o = D + q * dsq + c of
+// box row q < Q and column c < C (the box is one plane: no batch levels),
+// chan_of(o) = (o / rs) mod re = D / dsq + q exactly when rs = dsq,
+// (D mod dsq) + C <= dsq (the box's columns stay inside one row) and
+// D / dsq + Q <= re (no wrap). t_choff = D / dsq.
+bool row_channel(KArgs &a, const Box &b, int qa, int ca) {
+  if (a.chain_code != kChainDeqF16 || a.wout != 2)
+    return false;
+  const DevStage &s = a.chain.st[0];
+  const int64_t dsq = a.ds[qa];
+  if (s.mode != kChanDim || s.vec != 0 || s.ch_rs != dsq || a.ds[ca] != 1 || dsq <= 0)
+    return false;
+  for (int j = 0; j < kBatchLevels; ++j)
+    if (a.lv[j].div.d != 1)
+      return false;
+  if (a.dbase % dsq + b.ext[ca] > dsq || a.dbase / dsq + b.ext[qa] > s.ch_re)
+    return false;
+  a.t_choff = static_cast<uint32_t>(a.dbase / dsq);
+  return true;
+}
+
+// The zero points of channels [c0, c0 + n) of a dequantize stage are all 0.
+bool zero_points_zero(const DeviceProgram &dp, const DevStage &s, int64_t c0, int64_t n) {
+  const int64_t lo = s.zp_off + (s.zp_per_ch ? c0 : 0), hi = lo + (s.zp_per_ch ? n : 1);
+  if (lo < 0 || hi > static_cast<int64_t>(dp.pi.size()))
+    return false;
+  for (int64_t i = lo; i < hi; ++i)
+    if (dp.pi[static_cast<size_t>(i)] != 0)
+      return false;
+  return true;
+}
+
 // A permute launch runs the direct body when its divisions are shifts (G*E,
 // E and the 16-byte vectors of a run are powers of two, so make_div gives
 // m = 1 and s = log2 d), its batch entries lie along one level (the outer
@@ -844,8 +880,13 @@ KArgs launch_args(const DeviceProgram &dp, const Box &b) {
       a.t_tail = make_div(nq - full > 0 ? nq - full : 1);
       a.t_nc = make_div(nc);
       a.t_full = static_cast<uint32_t>(full);
-      a.t_xcd = bytes && !wide ? 1u : 0u;
-      a.t_skew = wide ? 1u : 0u;
+      a.t_flags = (bytes && !wide ? kTileXcd : 0u) | (wide ? kTileSkew : 0u);
+      a.t_choff = 0;
+      if (a.t_wc == 128 && row_channel(a, b, dp.qa, dp.ca)) {
+        a.t_flags |= kTileRowChannel;
+        if (zero_points_zero(dp, a.chain.st[0], a.t_choff, b.ext[dp.qa]))
+          a.t_flags |= kTileZeroPoint0;
+      }
     }
     a.t_ssc = a.ss[dp.ca];
     a.t_dsq = a.ds[dp.qa];
@@ -1084,11 +1125,13 @@ void verify_launch(const DeviceProgram &dp_in, const KArgs &a) {
     const int VO = 16 / wout;
     const int64_t TQ = a.t_wq, TC = a.t_wc;
     if (!(TQ == 64 || (TQ == 128 && win == 1)) || !(TC == 64 || (TC == 128 && TQ == 128)) ||
-        a.t_nc.d != a.t_group.d / a.t_g.d || (a.t_skew && a.t_xcd) || (TC == 128 && a.t_xcd))
+        a.t_nc.d != a.t_group.d / a.t_g.d || (a.t_flags & ~(kTileXcd | kTileSkew | kTileRowChannel | kTileZeroPoint0)) ||
+        ((a.t_flags & kTileSkew) && (a.t_flags & kTileXcd)) || (TC == 128 && (a.t_flags & kTileXcd)) ||
+        ((a.t_flags & kTileRowChannel) && TC != 128))
       bad_launch(dp, "tile geometry disagrees with the kernel");
     std::vector<bool> seen(a.work, false); // the order must be a bijection
     for (uint32_t blk = 0; blk < a.work; ++blk) { // grid = one block per tile
-      const uint32_t t = a.t_xcd ? xcd_tile(blk, a.work) : blk;
+      const uint32_t t = (a.t_flags & kTileXcd) ? xcd_tile(blk, a.work) : blk;
       if (t >= a.work)
         bad_launch(dp, "a block maps past the last tile");
       uint32_t tq, tc, r2;
@@ -1120,9 +1163,20 @@ void verify_launch(const DeviceProgram &dp_in, const KArgs &a) {
       }
       if ((a.t_ssc * win) % 16 != 0 || (a.t_dsq * wout) % 16 != 0)
         bad_launch(dp, "row strides break 16-byte alignment");
+      const bool rowch = (a.t_flags & kTileRowChannel) != 0;
+      if (rowch && (r2 != 0 || a.chain_code != kChainDeqF16 || a.chain.st[0].vec != 0))
+        bad_launch(dp, "row-indexed parameters with a chain or batch they do not fit");
+      if ((a.t_flags & kTileZeroPoint0) &&
+          (!rowch || !zero_points_zero(dp, a.chain.st[0], a.t_choff, int64_t{a.t_plane.d} /
+                                                                       a.t_nc.d * TQ)))
+        bad_launch(dp, "a launch that leaves zero points out reads one that is not 0");
       for (int64_t row = 0; row < TQ; ++row)
-        for (int64_t cv = 0; cv < TC; cv += VO)
-          ck.channels(dbase + (q0 + row) * a.t_dsq + c0 + cv, VO);
+        for (int64_t cv = 0; cv < TC; cv += VO) {
+          const int64_t o = dbase + (q0 + row) * a.t_dsq + c0 + cv;
+          ck.channels(o, VO);
+          if (rowch && chan_of(a.chain.st[0], o) != a.t_choff + static_cast<uint32_t>(q0 + row))
+            bad_launch(dp, "a row-indexed launch reads another parameter entry");
+        }
     }
     break;
   }

@@ -137,6 +137,17 @@ constexpr int interleave_pixels(int win, int wout, int cp) {
 #endif
 constexpr uint32_t kTileGroup = RELX_TILE_GROUP;
 
+// Transpose tile orders and parameter indexing (KArgs::t_flags).
+constexpr uint32_t kTileXcd = 1;  // each XCD takes a contiguous run of the order
+constexpr uint32_t kTileSkew = 2; // q-tile tq visits its c-tiles rotated by tq (mod nc)
+// The parameter stage's channel of every vector is t_choff plus its
+// box-relative destination row: the kernel indexes the parameters by row
+// (the host proves it for the launch, the verifier for every vector).
+constexpr uint32_t kTileRowChannel = 4;
+// With kTileRowChannel: every zero point the launch reads is 0 (symmetric
+// dequantization), so the kernel leaves the subtraction out.
+constexpr uint32_t kTileZeroPoint0 = 8;
+
 // Decomposition levels of the batch axes of the 2-D families.
 constexpr int kBatchLevels = 3;
 // Work items per launch of a fast kernel, and the source and destination
@@ -173,14 +184,14 @@ struct KArgs {
   // of g q-tiles (see tile_of): plane = nq * nc tiles, group = g * nc tiles,
   // g, tail = the q-tiles of the last, partial group, nc = c-tiles
   FastDiv t_plane, t_group, t_g, t_tail, t_nc;
-  uint32_t t_full; // q-tiles in whole groups
-  uint32_t t_xcd;  // 1: each XCD takes a contiguous run of the order
+  uint32_t t_full;  // q-tiles in whole groups
+  uint32_t t_flags; // kTileXcd | kTileSkew | kTileRowChannel
   // q-tile width (64, or 128 for one-byte sources) and c-tile width (64, or
-  // 128 for one-byte sources with four-byte results: byte tiles), read on
+  // 128 for one-byte sources with wider results: byte tiles), read on
   // the host only; 16 bits each keep the fields the kernels read where they
   // were
   uint16_t t_wq, t_wc;
-  uint32_t t_skew; // 1: q-tile tq visits its c-tiles rotated by tq (mod nc)
+  uint32_t t_choff; // kTileRowChannel: the parameter channel of tile row 0 of the box
   int64_t t_ssc, t_dsq; // source stride of c, destination stride of q
   // interleave: pixel groups along the source-contiguous axis p; channel axis c
   FastDiv i_ng;

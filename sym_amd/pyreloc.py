@@ -340,9 +340,15 @@ class Bound:
     @property
     def transpose_tile_c(self):
         """c width of a transpose program's tiles (128 for a one-byte source
-        with four-byte results whose q and c extents allow it, else 64; 0
-        for other kernel families)."""
+        with two- or four-byte results whose q and c extents allow it, else
+        64; 0 for other kernel families)."""
         return self.info.transpose_tile_c
+
+    @property
+    def transpose_row_params(self):
+        """True when every tile launch of a transpose program indexes its
+        dequantize parameters by destination row."""
+        return bool(self.info.transpose_row_params)
 
     def bytes_at(self, boundary):
         return self.info.bytes_at[boundary]

@@ -61,8 +61,11 @@ def test_c2_launches(n):
 def test_c3_launches():
     b = P.Bound(P.Plan(W.c3_plan().blob), {"s0": 4096, "s1": 11008},
                 W.param("scale", np.ones(11008, np.float32)))
-    # 11008 = 86 x 128: one-byte source rows read as whole 128-byte lines
-    assert b.kernel == "transpose" and (b.transpose_tile_q, b.transpose_tile_c) == (128, 64)
+    # 11008 = 86 x 128 and 4096 = 32 x 128: 128 x 128 byte tiles, whose
+    # tile rows read whole 128-byte lines
+    assert b.kernel == "transpose" and (b.transpose_tile_q, b.transpose_tile_c) == (128, 128)
+    # the per-row scale of the dequantize stage: one channel per result row
+    assert b.transpose_row_params
     _check(b, [0])
 
 
@@ -74,8 +77,8 @@ def test_c3_launches():
 def test_transpose_tile_width(rows, cols, tile_q, tile_c, f32):
     """One-byte transposes take tiles 128 q wide when the source-contiguous
     extent is a multiple of 128 (edge strips element-wise), else 64, and
-    with f32 results 128 c wide byte tiles when the c extent is a multiple
-    of 128 too; the
+    with f16 and f32 results 128 c wide byte tiles when the c extent is a
+    multiple of 128 too; the
     verifier walks the rotated tile order of the wide tiles (a bijection onto
     the plane) at several chunk sizes, so chunk boundaries along c and q
     keep the tile alignment."""
@@ -86,8 +89,10 @@ def test_transpose_tile_width(rows, cols, tile_q, tile_c, f32):
     if cols % 16:
         assert b.kernel != "transpose"
         return
-    want_c = tile_c if f32 else 64
+    want_c = tile_c
     assert b.kernel == "transpose" and (b.transpose_tile_q, b.transpose_tile_c) == (tile_q, want_c)
+    # the scale runs along the result rows: f16 byte tiles index it by row
+    assert b.transpose_row_params == (want_c == 128 and not f32)
     _check(b, range(len(b.footprints())), chunks=[0, 1 << 12, 1 << 16, 3 << 20])
 
 
@@ -96,15 +101,17 @@ def test_random_one_byte_transposes():
     batched or not; edge strips): each transpose program takes the tile
     width its q extent allows, and every launch is verified at several
     chunk sizes."""
-    kinds = set()
+    kinds, rows = set(), 0
     for name, blob, x, width in TC.random_cases(120):
         b = P.Bound(P.Plan(blob), {}, {})
         if b.kernel == "transpose":
             assert (b.transpose_tile_q, b.transpose_tile_c) == width, name
+        rows += b.transpose_row_params
         kinds.add((b.kernel, b.transpose_tile_q, b.transpose_tile_c))
         _check(b, [0], chunks=[0, 4096, 1 << 16])
     assert kinds == {("transpose", 128, 128), ("transpose", 128, 64), ("transpose", 64, 64),
                      ("generic", 0, 0)}
+    assert rows > 0
 
 
 def test_transpose_tile_width_wider_elements():
