@@ -1043,13 +1043,15 @@ struct Checker {
   const KArgs &a;
   int64_t wire, dst; // elements
   size_t npf, npi;
+  int64_t wire_lo; // first wire element the launch may read
 
   // n elements from `off`, accessed as one vector of n * width bytes when
   // `vec` (which must then be aligned to its size)
   void src_run(int64_t off, int64_t n, bool vec) const {
-    if (off < 0 || off + n > wire)
+    if (off < wire_lo || off + n > wire)
       bad_launch(dp, "source run [" + std::to_string(off) + ", " + std::to_string(off + n) +
-                         ") outside " + std::to_string(wire) + " wire elements");
+                         ") outside wire elements [" + std::to_string(wire_lo) + ", " +
+                         std::to_string(wire) + ")");
     if (vec && (off * a.win) % (n * a.win) != 0)
       bad_launch(dp, "unaligned " + std::to_string(n * a.win) + "-byte source access at element " +
                          std::to_string(off));
@@ -1083,14 +1085,16 @@ struct Checker {
 
 } // namespace
 
-void verify_launch(const DeviceProgram &dp_in, const KArgs &a) {
+void verify_launch(const DeviceProgram &dp_in, const KArgs &a, int64_t wire_lo, int64_t wire_hi) {
   DeviceProgram edge;
   if (a.edge_box && dp_in.family != kFamGeneric) { // run by the element-wise kernel
     edge = dp_in;
     edge.family = kFamGeneric;
   }
   const DeviceProgram &dp = a.edge_box && dp_in.family != kFamGeneric ? edge : dp_in;
-  const Checker ck{dp, a, dp.wire_elems, dp.dst_elems, dp.pf.size(), dp.pi.size()};
+  const Checker ck{dp,          a,           wire_hi < 0 ? dp.wire_elems : wire_hi,
+                   dp.dst_elems, dp.pf.size(), dp.pi.size(),
+                   wire_lo};
   if (dp.family != kFamGeneric) { // the levels' 32-bit offsets cannot wrap
     int64_t ss = 0, ds = 0;
     for (const Level &l : a.lv) {
@@ -1302,11 +1306,14 @@ bool verify_enabled() {
 int64_t launch_program(const DeviceProgram &dp, int64_t v0, int64_t v1, bool first, bool last,
                        const void *src, void *dst, const float *pf, const int32_t *pi,
                        int32_t *status, hipStream_t s) {
-  return launch_all(dp, box_launches(dp, v0, v1, first, last), src, dst, pf, pi, status, s);
+  const bool part = dp.chunk_axis >= 0 && v1 > v0; // else the whole box
+  return launch_all(dp, box_launches(dp, v0, v1, first, last), src, dst, pf, pi, status, s,
+                    part ? v0 * dp.chunk_stride : 0, part ? v1 * dp.chunk_stride : -1);
 }
 
 int64_t launch_all(const DeviceProgram &dp, std::vector<KArgs> launches, const void *src,
-                   void *dst, const float *pf, const int32_t *pi, int32_t *status, hipStream_t s) {
+                   void *dst, const float *pf, const int32_t *pi, int32_t *status, hipStream_t s,
+                   int64_t wire_lo, int64_t wire_hi) {
   // the fast kernels move 16-byte vectors: buffers that are not 16-byte
   // aligned take the element-wise kernel
   const bool aligned = reinterpret_cast<uintptr_t>(src) % 16 == 0 &&
@@ -1324,7 +1331,7 @@ int64_t launch_all(const DeviceProgram &dp, std::vector<KArgs> launches, const v
     if (verify_enabled()) {
       DeviceProgram view = dp;
       view.family = family;
-      verify_launch(view, a);
+      verify_launch(view, a, wire_lo, wire_hi);
     }
     a.src = static_cast<const uint8_t *>(src);
     a.dst = static_cast<uint8_t *>(dst);

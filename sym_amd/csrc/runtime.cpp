@@ -967,8 +967,10 @@ void execute(Context &ctx, std::vector<Member> &ms, const relx_options &opt,
         HIPCHECK(hipEventRecord(tev[0], cs));
       const int64_t nl = launch_program(dp, kb0, v1, kb0 == 0, v1 == p.units, kwire, m.dst,
                                         par.pf, par.pi, status, cs);
-      if (zc_slot >= 0)
+      if (zc_slot >= 0) {
         slot_release(ctx, zc_slot, cs, zc_track);
+        zc_slot = -1;
+      }
       if (tev) {
         HIPCHECK(hipEventRecord(tev[1], cs));
         ctx.kt.launches += nl;
@@ -1428,8 +1430,11 @@ int64_t verify_launches(BoundHandle &h, uint32_t k, int64_t chunk_bytes) {
   for (int i = 0; i < dp.base.rank; ++i)
     total *= dp.base.pext[i];
   int64_t covered = 0;
+  // A kernel batch reads only the wire of its own chunks, which have landed
+  // when it starts: the other copy stream may still be writing the next.
+  int64_t lo = 0, hi = -1;
   auto check = [&](const KArgs &a) {
-    verify_launch(dp, a);
+    verify_launch(dp, a, lo, hi);
     int64_t e = 1;
     for (int i = 0; i < a.rank; ++i)
       e *= a.box_ext[i];
@@ -1450,9 +1455,13 @@ int64_t verify_launches(BoundHandle &h, uint32_t k, int64_t chunk_bytes) {
       const int64_t v1 = kb.end(v0);
       if (v0 % p.per_chunk || (v1 % p.per_chunk && v1 != p.units))
         throw Error("internal_launch_check", "a kernel batch does not end on a chunk boundary");
+      lo = dp.chunk_axis >= 0 ? v0 * dp.chunk_stride : 0;
+      hi = dp.chunk_axis >= 0 ? v1 * dp.chunk_stride : -1;
       for (const KArgs &a : box_launches(dp, v0, v1, v0 == 0, v1 == p.units))
         check(a);
     }
+    lo = 0;
+    hi = -1;
     schedule_done();
     whole = whole || (dp.chunk_axis >= 0 && p.units > p.per_chunk);
   }

@@ -89,8 +89,11 @@ std::vector<KArgs> prefix_launches(const DeviceProgram &dp, const int64_t *fixed
                                    int64_t plo, int64_t phi);
 // Coordinates a box along axis i must keep together (0: never split).
 int64_t axis_align(const DeviceProgram &dp, int i);
+// Launch boxes (verified first when RELX_VERIFY_LAUNCHES is set, their
+// source reads inside wire elements [wire_lo, wire_hi), wire_hi < 0: all).
 int64_t launch_all(const DeviceProgram &dp, std::vector<KArgs> launches, const void *src,
-                   void *dst, const float *pf, const int32_t *pi, int32_t *status, hipStream_t s);
+                   void *dst, const float *pf, const int32_t *pi, int32_t *status, hipStream_t s,
+                   int64_t wire_lo = 0, int64_t wire_hi = -1);
 // Launch the program over valid chunk-axis coordinates [v0, v1) (the whole
 // box when it has no chunk axis); returns the number of kernel launches.
 int64_t launch_program(const DeviceProgram &dp, int64_t v0, int64_t v1, bool first, bool last,
@@ -99,7 +102,10 @@ int64_t launch_program(const DeviceProgram &dp, int64_t v0, int64_t v1, bool fir
 hipError_t launch_box(int family, const KArgs &a, int32_t *status, hipStream_t s);
 // Host-side check that one launch stays inside the wire and the result, with
 // aligned vectors and parameter indices inside their tables (throws Error).
-void verify_launch(const DeviceProgram &dp, const KArgs &a);
+// Its source reads must lie in wire elements [wire_lo, wire_hi) (wire_hi < 0:
+// the whole wire).
+void verify_launch(const DeviceProgram &dp, const KArgs &a, int64_t wire_lo = 0,
+                   int64_t wire_hi = -1);
 
 // Chunk schedule of one program: `units` valid coordinates of the chunk axis
 // (1 without one), `per_chunk` per chunk, wire/source bytes per unit.
