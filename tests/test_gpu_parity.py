@@ -8,6 +8,7 @@ rows, plus size-independent checks (checksums of the whole buffer against
 the sampled oracle where exact).
 """
 import hashlib
+import os
 import sys
 
 import numpy as np
@@ -21,6 +22,9 @@ from tests import golden_io as G
 from tests import permute_cases as PC
 from tests import transpose_cases as TC
 from tests.test_encoder import small_cases
+
+# RELX_TRANSPOSE_DRAW=n:seed widens the random transposes (the suite runs 120:11)
+_TN, _TS = (int(v) for v in os.environ.get("RELX_TRANSPOSE_DRAW", "120:11").split(":"))
 
 pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
@@ -405,7 +409,7 @@ def test_random_one_byte_transposes(ctx):
     4 KiB chunks), device-resident, and device -> host into pageable memory
     (default and 4 KiB chunks, alternately)."""
     wide = byte_tiles = 0
-    for i, (name, blob, x, width) in enumerate(TC.random_cases(120)):
+    for i, (name, blob, x, width) in enumerate(TC.random_cases(_TN, seed=_TS)):
         want = (O.run_typed(blob, {}, {}, x).tobytes() if P.Plan(blob).typed else
                 O.execute_layout(O.bind(O.decode_plan(blob), {}), x.tobytes()))
         for chunk in (0, 4096):
